@@ -1,0 +1,352 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized linear-layer path on one MI355X.
+
+Headline workload (the `value`): the Q4_K decode GEMV set of one
+Qwen2-0.5B-shaped layer at batch 1 -- q/o 896x896, k/v 128x896, gate/up
+4864x896, down 896x4864, f32 activations and outputs.  One step is one decode
+token through R distinct device copies of that layer (R*7 GEMV launches,
+R*8.48 MB >= 1 GB so the 256 MB Infinity Cache cannot hold the weights),
+captured once as a HIP graph and replayed.  value = algorithmic bytes per step
+(GGUF block bytes + activation bytes + output bytes) / time per step.
+
+The same JSON line carries the roofline of the dominant kernel (the gate/up
+projection GEMV, timed in its own graph of R launches), a CPU baseline (the
+oracle's runtimed-gguf dequant + f32 GEMV on this host's cores) and, under
+"extra", the other workloads: the Q8_0 GEMV, the small-M verify sweep, the
+M=512 prefill GEMMs and the FP8 e4m3 GEMM.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
+
+# (name, n, k) of the Qwen2-0.5B layer, y = x W^T with W [n, k]
+LAYER = [("q", 896, 896), ("k", 128, 896), ("v", 128, 896), ("o", 896, 896),
+         ("gate", 4864, 896), ("up", 4864, 896), ("down", 896, 4864)]
+Q4K_BLOCK = 144
+
+
+def layer_bytes(act_bytes=4, out_bytes=4, m=1):
+    w = sum(n * k // 256 * Q4K_BLOCK for _, n, k in LAYER)
+    x = sum(m * k * act_bytes for _, n, k in LAYER)
+    y = sum(m * n * out_bytes for _, n, k in LAYER)
+    return w + x + y
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+class Timer:
+    """HIP-event timing of graph replays on the current stream."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def replay(self, graph, steps, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            graph.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / steps  # ms per replay
+
+
+def capture(torch, fn):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def decode_workload(torch, rq, synth, layers, steps, warmup, dev):
+    """The headline: R layers x 7 Q4_K GEMVs, one token, f32 in and out."""
+    blocks = {name: synth.q4_k_blocks(100 + i, n * k // 256) for i, (name, n, k) in enumerate(LAYER)}
+    W = [{name: rq.QWeight(rq.Q4_K, blocks[name], n, k) for name, n, k in LAYER} for _ in range(layers)]
+    x896 = torch.from_numpy(synth.activations(1, 1, 896)).to(dev)
+    x4864 = torch.from_numpy(synth.activations(2, 1, 4864)).to(dev)
+    ys = {name: torch.empty((1, n), dtype=torch.float32, device=dev) for name, n, k in LAYER}
+
+    def token():
+        for lw in W:
+            for name, n, k in LAYER:
+                lw[name].forward(x4864 if k == 4864 else x896, out=ys[name])
+
+    def gates():
+        for lw in W:
+            lw["gate"].forward(x896, out=ys["gate"])
+
+    timer = Timer(torch)
+    g = capture(torch, token)
+    ms = timer.replay(g, steps, warmup)
+    gg = capture(torch, gates)
+    gate_ms = timer.replay(gg, max(steps, 20), warmup) / layers
+    del g, gg
+    return W, ms, gate_ms
+
+
+def cpu_baseline(oracle, synth, budget_s):
+    """Oracle dequant (load time) + f32 GEMV over the dequantized layer."""
+    threads = cpu_threads()
+    blocks = {name: synth.q4_k_blocks(100 + i, n * k // 256) for i, (name, n, k) in enumerate(LAYER)}
+    t0 = time.perf_counter()
+    dense = {}
+    for name, n, k in LAYER:
+        rc, wf = oracle.dequant_tensor(12, blocks[name], n * k)
+        dense[name] = wf.reshape(n, k)
+    deq_1t = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    for name, n, k in LAYER:
+        oracle.dequant_tensor(12, blocks[name], n * k, threads=threads)
+    deq_mt = time.perf_counter() - t0
+    copies = 16  # 16 x 33.5 MB of f32 weights: larger than a CPU last-level cache slice
+    layers = [{nm: w.copy() for nm, w in dense.items()} for _ in range(copies)]
+    x896 = synth.activations(1, 1, 896)
+    x4864 = synth.activations(2, 1, 4864)
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        for lw in layers:
+            for name, n, k in LAYER:
+                oracle.linear_f32(x4864 if k == 4864 else x896, lw[name], threads=threads)
+        passes += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    per_layer = el / (passes * copies)
+    gbs = layer_bytes() / per_layer / 1e9
+    w_bytes = sum(n * k // 256 * Q4K_BLOCK for _, n, k in LAYER)
+    return {
+        "value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": f"{passes} passes over {copies} Qwen2-0.5B Q4_K layers (7 f32 GEMVs each on "
+                  f"oracle-dequantized weights, blocked OpenMP SGEMV, {threads} threads); "
+                  f"{el:.1f} s",
+        "ms_per_layer": round(per_layer * 1e3, 4),
+        "dequant_load_gbs_1thread": round(w_bytes / deq_1t / 1e9, 3),
+        f"dequant_load_gbs_{threads}threads": round(w_bytes / deq_mt / 1e9, 3),
+    }
+
+
+def extra_q8_gemv(torch, rq, synth, dev, steps, warmup):
+    n, k = 4864, 896
+    blocks = synth.q8_0_blocks(5, n * k // 32)
+    copies = 224  # 224 x 4.63 MB > 1 GB
+    W = [rq.QWeight(rq.Q8_0, blocks, n, k) for _ in range(copies)]
+    x = torch.from_numpy(synth.activations(3, 1, k)).to(dev)
+    y = torch.empty((1, n), device=dev)
+    g = capture(torch, lambda: [w.forward(x, out=y) for w in W])
+    ms = Timer(torch).replay(g, steps, warmup) / copies
+    b = n * k // 32 * 34 + k * 4 + n * 4
+    return {"workload": "Q8_0 GEMV 4864x896 f32, M=1", "us_per_gemv": round(ms * 1e3, 3),
+            "GB/s": round(b / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def extra_verify(torch, rq, W, dev, steps, warmup):
+    out = []
+    for m in (1, 2, 4, 8, 16, 64):
+        xs = {k: torch.randn((m, k), device=dev).to(torch.bfloat16) for k in (896, 4864)}
+        ys = {name: torch.empty((m, n), dtype=torch.bfloat16, device=dev) for name, n, k in LAYER}
+
+        def tok():
+            for lw in W:
+                for name, n, k in LAYER:
+                    lw[name].forward(xs[k], out=ys[name])
+
+        g = capture(torch, tok)
+        ms = Timer(torch).replay(g, max(2, steps // 4), 1)
+        b = layer_bytes(2, 2, m) * len(W)
+        fl = 2.0 * m * sum(n * k for _, n, k in LAYER) * len(W)
+        out.append({"m": m, "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                    "TFLOP/s": round(fl / (ms * 1e-3) / 1e12, 3),
+                    "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+        del g
+    return {"workload": "verify sweep, Qwen2-0.5B Q4_K layer, bf16 activations", "sweep": out}
+
+
+def extra_prefill(torch, rq, synth, dev, steps, warmup):
+    m = 512
+    shapes = [("q/k/o Q4_K", rq.Q4_K, 2048, 2048), ("v Q6_K", rq.Q6_K, 2048, 2048),
+              ("gate/up Q4_K", rq.Q4_K, 8192, 2048), ("down Q6_K", rq.Q6_K, 2048, 8192),
+              ("lm_head Q6_K", rq.Q6_K, 262144, 2048)]
+    res = []
+    for name, qt, n, k in shapes:
+        w = rq.QWeight(qt, synth.weight_blocks(qt, 7, n, k), n, k)
+        x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+        y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        w.forward(x, out=y)
+        torch.cuda.synchronize()
+        reps = 3 if n * k > 1e8 else max(3, steps // 2)
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            w.forward(x, out=y)
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / reps
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        res.append({"shape": f"{name} {n}x{k}", "ms": round(ms, 4), "TFLOP/s": round(tf, 2),
+                    "frac_mfma_bf16": round(tf / BF16_PEAK_TFLOPS, 4)})
+        del w
+        torch.cuda.empty_cache()
+    return {"workload": "prefill M=512, bf16 activations and outputs, f32 accumulation", "shapes": res}
+
+
+def extra_fp8(torch, rq, synth, dev, steps, warmup):
+    m, n, k = 2048, 14336, 4096
+    wv = torch.from_numpy(synth.fp8_weight_values(11, n, k)).to(dev)
+    wq, _ = rq.fp8_quantize(wv, rq.FP8_UNSCALED)
+    del wv
+    ws = torch.from_numpy(synth.fp8_row_scales(11, n)).to(dev)
+    x = torch.from_numpy(synth.activations(12, m, k)).to(dev).to(torch.bfloat16)
+    xq = torch.empty((m, k), dtype=torch.uint8, device=dev)
+    xs = torch.empty(m, dtype=torch.float32, device=dev)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+
+    def quant():
+        rq.check(rq.lib().rq_fp8_quantize(rq._ptr(x), rq.BF16, m, k, rq.FP8_PER_TOKEN, rq._ptr(xq),
+                                          rq._ptr(xs), rq._stream(dev)))
+
+    def gemm():
+        rq.fp8_gemm_q(xq, xs, wq, ws, y)
+
+    t = Timer(torch)
+    gq = capture(torch, quant)
+    ms_q = t.replay(gq, steps, warmup)
+    gg = capture(torch, gemm)
+    ms_g = t.replay(gg, steps, warmup)
+    tf = 2.0 * m * n * k / (ms_g * 1e-3) / 1e12
+    return {"workload": "FP8 e4m3 GEMM 2048x14336x4096, per-token activation scales, bf16 out",
+            "gemm_ms": round(ms_g, 4), "TFLOP/s": round(tf, 1), "frac_mfma_fp8": round(tf / FP8_PEAK_TFLOPS, 4),
+            "quantize_ms": round(ms_q, 4)}
+
+
+def traffic_from_profile():
+    p = ROOT / "profiles" / "traffic_q4k_gate_gemv.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+        except Exception:
+            return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=128)
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the quantized linear path runs on a single MI355X "
+              "(no tensor parallelism, no collectives); run it with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import runtimed_amd  # noqa: F401
+    from runtimed_amd import rq, synth
+
+    rq.lib()
+    dev = torch.device("cuda", 0)
+    log(f"decode workload: {args.layers} layer copies, steps={args.steps} warmup={args.warmup}")
+    W, ms, gate_ms = decode_workload(torch, rq, synth, args.layers, args.steps, args.warmup, dev)
+    step_bytes = layer_bytes() * args.layers
+    value = step_bytes / (ms * 1e-3) / 1e9
+    gate_bytes = 4864 * 896 // 256 * Q4K_BLOCK + 896 * 4 + 4864 * 4
+    gate_gbs = gate_bytes / (gate_ms * 1e-3) / 1e9
+    log(f"decode: {ms:.4f} ms/step, {value:.1f} GB/s; gate GEMV {gate_ms * 1e3:.3f} us, {gate_gbs:.1f} GB/s")
+
+    extra = {}
+    if not args.no_extras:
+        for name, fn in (("q8_0_gemv", lambda: extra_q8_gemv(torch, rq, synth, dev, args.steps, args.warmup)),
+                         ("verify", lambda: extra_verify(torch, rq, W[:32], dev, args.steps, args.warmup)),
+                         ("prefill", lambda: extra_prefill(torch, rq, synth, dev, args.steps, args.warmup)),
+                         ("fp8_gemm", lambda: extra_fp8(torch, rq, synth, dev, args.steps, args.warmup))):
+            log(f"extra: {name}")
+            try:
+                extra[name] = fn()
+                log(f"  {json.dumps(extra[name])}")
+            except Exception as e:  # report, keep the headline line
+                extra[name] = {"error": f"{type(e).__name__}: {e}"}
+                log(f"  failed: {e}")
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+    del W
+
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+
+        log("cpu baseline (oracle on host cores)")
+        cpu = cpu_baseline(oracle, synth, args.cpu_seconds)
+        log(f"  {json.dumps(cpu)}")
+
+    line = {
+        "metric": "Q4_K decode GEMV GB/s (% HBM peak); prefill dequant-GEMM TFLOPS (% MFMA)",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded splitmix64 GGUF Q4_K blocks, N(0,1) activations)",
+        "config": {"workload": "Q4_K decode GEMV set, one Qwen2-0.5B layer (q/o 896x896, k/v 128x896, "
+                               "gate/up 4864x896, down 896x4864), M=1, f32 activations",
+                   "layer_copies": args.layers, "bytes_per_step": step_bytes,
+                   "frac_hbm": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gate_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
+                     "kernel": "k_gemv_m1<FmtQ4K,1> (gate/up 4864x896)",
+                     "bytes_per_launch": gate_bytes, "us_per_launch": round(gate_ms * 1e3, 3)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

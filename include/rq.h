@@ -1,0 +1,176 @@
+/*
+ * rq.h -- C ABI of librq, the MI355X (gfx950) quantized linear-layer library.
+ *
+ * This is the drop-in boundary for runtimed's quantized linear path.  Each
+ * entry point names the reference interface it replaces (paths relative to
+ * the runtimed repository root):
+ *
+ *   rq_weight_create / rq_weight_destroy
+ *       candle `qtensor_from_ggml` + `QMatMul::from_arc`, reached from
+ *       crates/runtimed-model/src/weights/load_gguf.rs:28-38; the handle is the
+ *       value held in `Weights::q_map` (crates/runtimed-model/src/weights/store.rs:18)
+ *       behind an Arc and released by its Drop.
+ *   rq_weight_info
+ *       `QTensor::storage_size_in_bytes` as summed by `Weights::resident_bytes`
+ *       (store.rs:57-76), plus the shape candle keeps as [dims1, dims0]
+ *       (load_gguf.rs:35).
+ *   rq_dequant_f32
+ *       `QTensor::dequantize` as called by `Weights::get` (store.rs:88-94),
+ *       with runtimed-gguf's bit-exact semantics
+ *       (crates/runtimed-gguf/src/quant/dequant.rs:83-146).
+ *   rq_dequant_tensor
+ *       `dequant_tensor` (crates/runtimed-gguf/src/quant/dequant.rs:83-146) on
+ *       GGUF bytes already in device memory, same error rules.
+ *   rq_linear
+ *       `QMatMul::forward` as called by `Weights::linear`
+ *       (crates/runtimed-model/src/weights/linear_layer.rs:45-52).
+ *   rq_fp8_quantize, rq_fp8_gemm
+ *       `SubstratePort::fp8_gemm` (crates/runtimed-model/src/substrate/port.rs:73)
+ *       -> `ops::fp8_gemm` (crates/runtimed-model/src/ops/fp8_gemm.rs:77-191),
+ *       used by `Fp8Weight::forward` (crates/runtimed-model/src/weights/fp8_weight.rs:95-97)
+ *       and by the F8E4M3 branch of `Weights::linear_dense` (linear_layer.rs:78-87).
+ *   rq_last_error
+ *       the message carried by `ModelError::{Shape, Config}`
+ *       (crates/runtimed-model/src/error.rs:5-27).
+ *
+ * Conventions
+ *   - Every call returns RQ_OK (0) or a negative rq_status; the thread-local
+ *     message from rq_last_error() says what was wrong.
+ *   - Shapes follow candle: a weight is [n, k] (n output rows, k inputs,
+ *     GGUF dims [k, n]); y[m, n] = sum_k x[m, k] * W[n, k].  Rows are cut from
+ *     the flat GGUF block stream, so a block may straddle two rows when k is
+ *     not a multiple of the block size (dequant.rs:83-91 checks only the total).
+ *   - Activation, output and scale pointers are device pointers owned by the
+ *     caller; `stream` is a hipStream_t (NULL = the legacy default stream).
+ *     All launches are asynchronous on `stream`.
+ *   - Calls on different handles and streams may run concurrently from
+ *     different threads.  A weight handle is immutable after creation.
+ *   - The device is bound per call: every entry point makes the handle's
+ *     device current on the calling thread (store.rs:128-145 does the same
+ *     with `ensure_current`).
+ */
+#ifndef RQ_H
+#define RQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RQ_ABI_VERSION 1
+
+/* Block formats, numbered as GgmlDtype (crates/runtimed-gguf/src/quant/dtype.rs:6-24). */
+typedef enum rq_qtype {
+  RQ_Q4_0 = 2,
+  RQ_Q5_0 = 6,
+  RQ_Q8_0 = 8,
+  RQ_Q4_K = 12,
+  RQ_Q5_K = 13,
+  RQ_Q6_K = 14
+} rq_qtype;
+
+/* Dense element types for activations and outputs.  F32/F16/BF16 keep their
+ * GgmlDtype ids; F8E4M3 (OCP e4m3fn, as candle's DType::F8E4M3) has none. */
+typedef enum rq_ftype {
+  RQ_F32 = 0,
+  RQ_F16 = 1,
+  RQ_BF16 = 30,
+  RQ_F8E4M3 = 128
+} rq_ftype;
+
+typedef enum rq_status {
+  RQ_OK = 0,
+  RQ_E_UNSUPPORTED = -1, /* GgufError::Unsupported (dequant.rs:84-86) */
+  RQ_E_OVERFLOW = -2,    /* GgufError::Overflow: n % block elems != 0 (dequant.rs:87-91) */
+  RQ_E_TRUNCATED = -3,   /* GgufError::Truncated: too few bytes (dequant.rs:92-95) */
+  RQ_E_SHAPE = -4,       /* ModelError::Shape (error.rs:13-18) */
+  RQ_E_ARG = -5,         /* null pointer, bad enum or negative size */
+  RQ_E_DEVICE = -6,      /* a HIP runtime call failed */
+  RQ_E_NOMEM = -7        /* device allocation failed */
+} rq_status;
+
+/* Activation encodings for the FP8 GEMM. */
+typedef enum rq_fp8_mode {
+  /* x -> e4m3 with no scale through the reference encoder (nearest, ties to
+   * the lower magnitude, saturating at 448): the CUDA path's semantics,
+   * fp8_gemm.rs:94-101. */
+  RQ_FP8_UNSCALED = 0,
+  /* per-row dynamic scale s[m] = max|x[m,:]| / 448, codes
+   * e4m3_rne(x * (448 / max|x[m,:]|)); y is multiplied back by s[m]. */
+  RQ_FP8_PER_TOKEN = 1
+} rq_fp8_mode;
+
+typedef struct rq_weight rq_weight;
+
+typedef struct rq_weight_desc {
+  int32_t qtype;          /* rq_qtype */
+  int32_t device;         /* HIP device ordinal */
+  int64_t n;              /* output rows */
+  int64_t k;              /* inputs per row */
+  uint64_t gguf_bytes;    /* size of the GGUF block stream: n*k/elems*block_bytes */
+  uint64_t device_bytes;  /* device memory held by the handle */
+} rq_weight_desc;
+
+/* ABI version of the loaded library (RQ_ABI_VERSION at build time). */
+int rq_abi_version(void);
+
+/* Thread-local description of the last error on this thread ("" if none). */
+const char *rq_last_error(void);
+
+/* Upload one GGUF tensor of n x k elements in block format `qtype` from host
+ * memory to `device`.  nbytes must cover n*k/elems*block_bytes
+ * (header.rs:191-205); n*k must be a multiple of the block size.  Q8_0 and
+ * Q6_K are split into 16-byte-aligned arrays on the device; the element
+ * values are unchanged.  The handle owns its device memory. */
+int rq_weight_create(int qtype, const void *host_blocks, size_t nbytes, int64_t n,
+                     int64_t k, int device, rq_weight **out);
+
+/* Release a handle and its device memory.  NULL is ignored. */
+void rq_weight_destroy(rq_weight *w);
+
+int rq_weight_info(const rq_weight *w, rq_weight_desc *out);
+
+/* Decode the whole weight to f32 (n*k values, row-major [n, k]) into device
+ * memory.  Bit-identical to runtimed-gguf's dequant_tensor. */
+int rq_dequant_f32(const rq_weight *w, float *dev_out, void *stream);
+
+/* Decode a flat GGUF block stream that already sits in device memory, with
+ * dequant_tensor's rules: RQ_E_UNSUPPORTED for a type without a decoder,
+ * RQ_E_OVERFLOW if n_elements is not a block multiple, RQ_E_TRUNCATED if
+ * nbytes is short. */
+int rq_dequant_tensor(int qtype, const void *dev_bytes, size_t nbytes, size_t n_elements,
+                      float *dev_out, void *stream);
+
+/* y[m, n] = sum_k x[m, k] * W[n, k] for an m x k activation (row-major, type
+ * xtype in {F32, F16, BF16}) into y (row-major m x n, type ytype in {F32, F16,
+ * BF16}).  Accumulation is in f32.  m = 0 is a no-op. */
+int rq_linear(const rq_weight *w, const void *x, int xtype, int64_t m, void *y, int ytype,
+              void *stream);
+
+/* Encode an m x k activation (F32, F16 or BF16) to e4m3 codes xq (m*k bytes)
+ * and per-row scales xscale (m floats) according to `mode` (RQ_FP8_UNSCALED
+ * writes scale 1). */
+int rq_fp8_quantize(const void *x, int xtype, int64_t m, int64_t k, int mode, uint8_t *xq,
+                    float *xscale, void *stream);
+
+/* FP8 e4m3 GEMM: y[m, n] = sx[m] * w_scale[n] * sum_k xq[m, k] * w[n, k] on
+ * CDNA4 fp8 matrix cores with f32 accumulation.  w is n x k e4m3 codes,
+ * w_scale has n floats (or NULL for all ones, linear_layer.rs:82-85).  If
+ * xtype is RQ_F8E4M3, x holds codes used as they are (sx = 1); otherwise x is
+ * encoded first according to `mode`, in stream-ordered scratch memory.
+ * ytype is F32, F16 or BF16. */
+int rq_fp8_gemm(const void *x, int xtype, int64_t m, const uint8_t *w, const float *w_scale,
+                int64_t n, int64_t k, void *y, int ytype, int mode, void *stream);
+
+/* The GEMM proper on codes already encoded by rq_fp8_quantize (xscale may be
+ * NULL for all ones). */
+int rq_fp8_gemm_q(const uint8_t *xq, const float *xscale, int64_t m, const uint8_t *w,
+                  const float *w_scale, int64_t n, int64_t k, void *y, int ytype,
+                  void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,255 @@
+// rq_api.cpp -- the C ABI of librq (include/rq.h): argument checks, handle
+// ownership, device binding and dispatch to the HIP kernels.
+//
+// Error rules follow the reference: dequant_tensor's Unsupported / Overflow /
+// Truncated (crates/runtimed-gguf/src/quant/dequant.rs:84-95) for block
+// streams, ModelError::Shape for activation shapes (linear_layer.rs:88-94).
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "rq_internal.h"
+
+namespace rq {
+
+static thread_local std::string g_last_error;
+
+int set_error(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
+
+bool geometry(int qtype, Geometry *g) {
+  switch (qtype) {
+    case RQ_Q4_0: *g = {32, 18}; return true;
+    case RQ_Q5_0: *g = {32, 22}; return true;
+    case RQ_Q8_0: *g = {32, 34}; return true;
+    case RQ_Q4_K: *g = {256, 144}; return true;
+    case RQ_Q5_K: *g = {256, 176}; return true;
+    case RQ_Q6_K: *g = {256, 210}; return true;
+    default: return false;
+  }
+}
+
+static bool valid_ftype(int t) { return t == RQ_F32 || t == RQ_F16 || t == RQ_BF16; }
+
+static int hip_check(hipError_t e, const char *what) {
+  if (e == hipSuccess) return RQ_OK;
+  return set_error(e == hipErrorOutOfMemory ? RQ_E_NOMEM : RQ_E_DEVICE, "%s: %s", what,
+                   hipGetErrorString(e));
+}
+
+// Dequant_tensor's checks on a flat stream of n_elements (dequant.rs:83-95).
+static int stream_checks(int qtype, uint64_t nbytes, uint64_t n_elements, Geometry *g) {
+  if (!geometry(qtype, g)) return set_error(RQ_E_UNSUPPORTED, "decode of qtype %d not implemented", qtype);
+  if (n_elements % (uint64_t)g->elems != 0)
+    return set_error(RQ_E_OVERFLOW, "%llu not a multiple of %d", (unsigned long long)n_elements, g->elems);
+  const uint64_t need = n_elements / (uint64_t)g->elems * (uint64_t)g->bytes;
+  if (nbytes < need)
+    return set_error(RQ_E_TRUNCATED, "truncated: %llu bytes, need %llu", (unsigned long long)nbytes,
+                     (unsigned long long)need);
+  return RQ_OK;
+}
+
+static uint64_t align256(uint64_t v) { return (v + 255) & ~(uint64_t)255; }
+
+// Host-side split of Q8_0 / Q6_K streams into the aligned device layout
+// described in rq_internal.h.
+static void split_layout(int qtype, const uint8_t *src, uint64_t nblocks, std::vector<uint8_t> &dst,
+                         uint64_t &aux_off) {
+  if (qtype == RQ_Q8_0) {
+    aux_off = align256(nblocks * 32);
+    dst.assign(aux_off + nblocks * 2, 0);
+    for (uint64_t b = 0; b < nblocks; ++b) {
+      const uint8_t *blk = src + b * 34;
+      memcpy(&dst[b * 32], blk + 2, 32);
+      memcpy(&dst[aux_off + b * 2], blk, 2);
+    }
+  } else {  // Q6_K
+    aux_off = align256(nblocks * 208);
+    dst.assign(aux_off + nblocks * 2, 0);
+    for (uint64_t b = 0; b < nblocks; ++b) {
+      const uint8_t *blk = src + b * 210;
+      memcpy(&dst[b * 208], blk, 208);
+      memcpy(&dst[aux_off + b * 2], blk + 208, 2);
+    }
+  }
+}
+
+}  // namespace rq
+
+using namespace rq;
+
+extern "C" {
+
+int rq_abi_version(void) { return RQ_ABI_VERSION; }
+
+const char *rq_last_error(void) { return g_last_error.c_str(); }
+
+int rq_weight_create(int qtype, const void *host_blocks, size_t nbytes, int64_t n, int64_t k,
+                     int device, rq_weight **out) {
+  g_last_error.clear();
+  if (!out) return set_error(RQ_E_ARG, "out is null");
+  *out = nullptr;
+  if (!host_blocks) return set_error(RQ_E_ARG, "host_blocks is null");
+  if (n <= 0 || k <= 0) return set_error(RQ_E_SHAPE, "shape [%lld, %lld] must be positive", (long long)n, (long long)k);
+  Geometry g;
+  const uint64_t count = (uint64_t)n * (uint64_t)k;
+  int rc = stream_checks(qtype, nbytes, count, &g);
+  if (rc) return rc;
+  rc = hip_check(hipSetDevice(device), "hipSetDevice");
+  if (rc) return rc;
+  const uint64_t nblocks = count / (uint64_t)g.elems;
+  const uint8_t *src = static_cast<const uint8_t *>(host_blocks);
+  std::vector<uint8_t> staged;
+  uint64_t aux_off = 0, bytes = nblocks * (uint64_t)g.bytes;
+  if (qtype == RQ_Q8_0 || qtype == RQ_Q6_K) {
+    split_layout(qtype, src, nblocks, staged, aux_off);
+    src = staged.data();
+    bytes = staged.size();
+  }
+  uint8_t *dptr = nullptr;
+  rc = hip_check(hipMalloc(reinterpret_cast<void **>(&dptr), bytes), "hipMalloc");
+  if (rc) return rc;
+  rc = hip_check(hipMemcpy(dptr, src, bytes, hipMemcpyHostToDevice), "hipMemcpy");
+  if (rc) {
+    (void)hipFree(dptr);
+    return rc;
+  }
+  rq_weight *w = new rq_weight;
+  w->qtype = qtype;
+  w->device = device;
+  w->n = n;
+  w->k = k;
+  w->gguf_bytes = nblocks * (uint64_t)g.bytes;
+  w->nblocks = nblocks;
+  w->data = dptr;
+  w->data_bytes = bytes;
+  w->aux_off = aux_off;
+  *out = w;
+  return RQ_OK;
+}
+
+void rq_weight_destroy(rq_weight *w) {
+  if (!w) return;
+  int cur = 0;
+  if (hipGetDevice(&cur) == hipSuccess && cur != w->device) (void)hipSetDevice(w->device);
+  (void)hipFree(w->data);
+  if (cur != w->device) (void)hipSetDevice(cur);
+  delete w;
+}
+
+int rq_weight_info(const rq_weight *w, rq_weight_desc *out) {
+  if (!w || !out) return set_error(RQ_E_ARG, "null argument");
+  out->qtype = w->qtype;
+  out->device = w->device;
+  out->n = w->n;
+  out->k = w->k;
+  out->gguf_bytes = w->gguf_bytes;
+  out->device_bytes = w->data_bytes;
+  return RQ_OK;
+}
+
+int rq_dequant_f32(const rq_weight *w, float *dev_out, void *stream) {
+  g_last_error.clear();
+  if (!w || !dev_out) return set_error(RQ_E_ARG, "null argument");
+  int rc = hip_check(hipSetDevice(w->device), "hipSetDevice");
+  if (rc) return rc;
+  return launch_dequant_weight(w, dev_out, as_stream(stream));
+}
+
+int rq_dequant_tensor(int qtype, const void *dev_bytes, size_t nbytes, size_t n_elements,
+                      float *dev_out, void *stream) {
+  g_last_error.clear();
+  Geometry g;
+  int rc = stream_checks(qtype, nbytes, n_elements, &g);
+  if (rc) return rc;
+  if (n_elements == 0) return RQ_OK;
+  if (!dev_bytes || !dev_out) return set_error(RQ_E_ARG, "null argument");
+  return launch_dequant_raw(qtype, static_cast<const uint8_t *>(dev_bytes),
+                            n_elements / (uint64_t)g.elems, dev_out, as_stream(stream));
+}
+
+int rq_linear(const rq_weight *w, const void *x, int xtype, int64_t m, void *y, int ytype,
+              void *stream) {
+  g_last_error.clear();
+  if (!w) return set_error(RQ_E_ARG, "weight is null");
+  if (!valid_ftype(xtype)) return set_error(RQ_E_ARG, "activation type %d not supported", xtype);
+  if (!valid_ftype(ytype)) return set_error(RQ_E_ARG, "output type %d not supported", ytype);
+  if (m < 0) return set_error(RQ_E_SHAPE, "negative row count %lld", (long long)m);
+  if (m == 0) return RQ_OK;
+  if (!x || !y) return set_error(RQ_E_ARG, "null activation or output");
+  int rc = hip_check(hipSetDevice(w->device), "hipSetDevice");
+  if (rc) return rc;
+  hipStream_t s = as_stream(stream);
+  rc = launch_linear_fused(w, x, xtype, m, y, ytype, s);
+  if (rc != RQ_E_UNSUPPORTED) return rc;
+  // No fused kernel for this format or shape: decode to f32 in stream-ordered
+  // scratch, then multiply.
+  float *tmp = nullptr;
+  const uint64_t bytes = (uint64_t)w->n * (uint64_t)w->k * sizeof(float);
+  rc = hip_check(hipMallocAsync(reinterpret_cast<void **>(&tmp), bytes, s), "hipMallocAsync");
+  if (rc) return rc;
+  rc = launch_dequant_weight(w, tmp, s);
+  if (!rc) rc = launch_linear_dense_f32(tmp, w->n, w->k, x, xtype, m, y, ytype, s);
+  const int rc2 = hip_check(hipFreeAsync(tmp, s), "hipFreeAsync");
+  return rc ? rc : rc2;
+}
+
+int rq_fp8_quantize(const void *x, int xtype, int64_t m, int64_t k, int mode, uint8_t *xq,
+                    float *xscale, void *stream) {
+  g_last_error.clear();
+  if (!valid_ftype(xtype)) return set_error(RQ_E_ARG, "activation type %d not supported", xtype);
+  if (mode != RQ_FP8_UNSCALED && mode != RQ_FP8_PER_TOKEN) return set_error(RQ_E_ARG, "bad fp8 mode %d", mode);
+  if (m < 0 || k <= 0) return set_error(RQ_E_SHAPE, "bad shape [%lld, %lld]", (long long)m, (long long)k);
+  if (m == 0) return RQ_OK;
+  if (!x || !xq || !xscale) return set_error(RQ_E_ARG, "null argument");
+  return launch_fp8_quantize(x, xtype, m, k, mode, xq, xscale, as_stream(stream));
+}
+
+int rq_fp8_gemm_q(const uint8_t *xq, const float *xscale, int64_t m, const uint8_t *w,
+                  const float *w_scale, int64_t n, int64_t k, void *y, int ytype, void *stream) {
+  g_last_error.clear();
+  if (!valid_ftype(ytype)) return set_error(RQ_E_ARG, "output type %d not supported", ytype);
+  if (m < 0 || n <= 0 || k <= 0)
+    return set_error(RQ_E_SHAPE, "bad shape m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
+  if (m == 0) return RQ_OK;
+  if (!xq || !w || !y) return set_error(RQ_E_ARG, "null argument");
+  return launch_fp8_gemm(xq, xscale, m, w, w_scale, n, k, y, ytype, as_stream(stream));
+}
+
+int rq_fp8_gemm(const void *x, int xtype, int64_t m, const uint8_t *w, const float *w_scale,
+                int64_t n, int64_t k, void *y, int ytype, int mode, void *stream) {
+  g_last_error.clear();
+  if (xtype == RQ_F8E4M3)
+    return rq_fp8_gemm_q(static_cast<const uint8_t *>(x), nullptr, m, w, w_scale, n, k, y, ytype, stream);
+  if (!valid_ftype(xtype)) return set_error(RQ_E_ARG, "activation type %d not supported", xtype);
+  if (mode != RQ_FP8_UNSCALED && mode != RQ_FP8_PER_TOKEN) return set_error(RQ_E_ARG, "bad fp8 mode %d", mode);
+  if (m < 0 || n <= 0 || k <= 0)
+    return set_error(RQ_E_SHAPE, "bad shape m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
+  if (m == 0) return RQ_OK;
+  if (!x || !w || !y) return set_error(RQ_E_ARG, "null argument");
+  hipStream_t s = as_stream(stream);
+  const uint64_t qbytes = ((uint64_t)m * (uint64_t)k + 255) & ~(uint64_t)255;
+  uint8_t *scratch = nullptr;
+  int rc = hip_check(hipMallocAsync(reinterpret_cast<void **>(&scratch), qbytes + (uint64_t)m * 4, s),
+                     "hipMallocAsync");
+  if (rc) return rc;
+  float *xs = reinterpret_cast<float *>(scratch + qbytes);
+  rc = launch_fp8_quantize(x, xtype, m, k, mode, scratch, xs, s);
+  if (!rc) rc = launch_fp8_gemm(scratch, xs, m, w, w_scale, n, k, y, ytype, s);
+  const int rc2 = hip_check(hipFreeAsync(scratch, s), "hipFreeAsync");
+  return rc ? rc : rc2;
+}
+
+}  // extern "C"

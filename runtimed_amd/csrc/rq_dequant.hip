@@ -1,0 +1,219 @@
+// rq_dequant.hip -- bit-exact block decode to f32 on gfx950.
+//
+// Semantics: runtimed-gguf's scalar decoders (crates/runtimed-gguf/src/quant/
+// dequant.rs:40-77 for Q8_0/Q4_0/Q5_0, dequant_k.rs:19-111 for Q4_K/Q5_K/Q6_K)
+// and the flat dispatcher dequant_tensor (dequant.rs:83-146).  Every product
+// the decoders form before their last rounding is exact in f32 (at most 22
+// significant bits), and each kernel keeps the reference's evaluation order
+// for the one rounding that remains, so the result is bit-identical with or
+// without FMA contraction.  f16 scales are widened with integer arithmetic so
+// that NaN payloads pass through unchanged, as dequant.rs:11-33 does.
+//
+// Roofline: HBM-bound; per element the algorithmic traffic is the block bytes
+// per element read plus 4 bytes of f32 written.
+#include "rq_internal.h"
+
+namespace rq {
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ uint32_t rd_u16(const uint8_t *p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8);
+}
+
+// scale_min_k4 (dequant_k.rs:8-16) on the 12 packed scale bytes.
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t *s, uint32_t &sc,
+                                             uint32_t &m) {
+  if (j < 4) {
+    sc = s[j] & 63u;
+    m = s[j + 4] & 63u;
+  } else {
+    sc = (s[j + 4] & 0xFu) | ((uint32_t)(s[j - 4] >> 6) << 4);
+    m = (uint32_t)(s[j + 4] >> 4) | ((uint32_t)(s[j] >> 6) << 4);
+  }
+}
+
+// One element of one GGUF block from raw bytes (any alignment).
+__device__ float decode_raw(int qtype, const uint8_t *b, int i) {
+  switch (qtype) {
+    case RQ_Q8_0:  // dequant.rs:40-47
+      return f16_bits_to_f32(rd_u16(b)) * (float)(int8_t)b[2 + i];
+    case RQ_Q4_0: {  // dequant.rs:50-61
+      const float d = f16_bits_to_f32(rd_u16(b));
+      const int q = i < 16 ? (b[2 + i] & 0x0F) : (b[2 + i - 16] >> 4);
+      return d * (float)(q - 8);
+    }
+    case RQ_Q5_0: {  // dequant.rs:64-77; element j takes qh bit j
+      const float d = f16_bits_to_f32(rd_u16(b));
+      const uint32_t qh = (uint32_t)b[2] | ((uint32_t)b[3] << 8) | ((uint32_t)b[4] << 16) |
+                          ((uint32_t)b[5] << 24);
+      const int lo = i < 16 ? (b[6 + i] & 0x0F) : (b[6 + i - 16] >> 4);
+      const int q = lo | (int)(((qh >> i) & 1u) << 4);
+      return d * (float)(q - 16);
+    }
+    case RQ_Q4_K: {  // dequant_k.rs:19-44
+      const float d = f16_bits_to_f32(rd_u16(b));
+      const float mn = f16_bits_to_f32(rd_u16(b + 2));
+      const int chunk = i >> 6, r = i & 63, j = 2 * chunk + (r >> 5);
+      uint32_t sc, m;
+      scale_min_k4(j, b + 4, sc, m);
+      const uint8_t byte = b[16 + 32 * chunk + (r & 31)];
+      const uint32_t q = (r < 32) ? (byte & 0xFu) : (uint32_t)(byte >> 4);
+      const float d1 = d * (float)sc, m1 = mn * (float)m;
+      return d1 * (float)q - m1;
+    }
+    case RQ_Q5_K: {  // dequant_k.rs:51-80
+      const float d = f16_bits_to_f32(rd_u16(b));
+      const float mn = f16_bits_to_f32(rd_u16(b + 2));
+      const int chunk = i >> 6, r = i & 63, l = r & 31, j = 2 * chunk + (r >> 5);
+      uint32_t sc, m;
+      scale_min_k4(j, b + 4, sc, m);
+      const uint8_t byte = b[48 + 32 * chunk + l];
+      const uint32_t q = (r < 32) ? (byte & 0xFu) : (uint32_t)(byte >> 4);
+      const uint32_t mask = (r < 32 ? 1u : 2u) << (2 * chunk);
+      const float hi = (b[16 + l] & mask) ? 16.0f : 0.0f;
+      const float d1 = d * (float)sc, m1 = mn * (float)m;
+      return d1 * ((float)q + hi) - m1;
+    }
+    case RQ_Q6_K: {  // dequant_k.rs:87-111
+      const int hf = i >> 7, r = i & 127, kk = r >> 5, l = r & 31;
+      const uint8_t qlb = b[64 * hf + l + 32 * (kk & 1)];
+      const uint8_t qhb = b[128 + 32 * hf + l];
+      const uint32_t q = ((uint32_t)(qlb >> (4 * (kk >> 1))) & 0xFu) |
+                         ((((uint32_t)qhb >> (2 * kk)) & 3u) << 4);
+      const float v = (float)(int8_t)q - 32.0f;
+      const float d = f16_bits_to_f32(rd_u16(b + 208));
+      return d * (float)(int8_t)b[192 + 8 * hf + (l >> 4) + 2 * kk] * v;
+    }
+    default:
+      return 0.0f;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void k_dequant_raw(int qtype, int elems, int bbytes,
+                                                         const uint8_t *__restrict__ src,
+                                                         uint64_t total, float *__restrict__ out) {
+  const uint64_t stride = (uint64_t)gridDim.x * kThreads;
+  for (uint64_t e = (uint64_t)blockIdx.x * kThreads + threadIdx.x; e < total; e += stride) {
+    const uint64_t blk = e / (uint64_t)elems;
+    const int i = (int)(e - blk * (uint64_t)elems);
+    out[e] = decode_raw(qtype, src + blk * (uint64_t)bbytes, i);
+  }
+}
+
+// Q4_K handle layout (aligned GGUF blocks): one thread per 4 outputs.
+__global__ __launch_bounds__(kThreads) void k_dequant_q4k(const uint8_t *__restrict__ src,
+                                                         uint64_t quads, float4 *__restrict__ out) {
+  const uint64_t stride = (uint64_t)gridDim.x * kThreads;
+  for (uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x; t < quads; t += stride) {
+    const uint64_t blk = t >> 6;
+    const int i0 = (int)(t & 63) * 4;
+    const uint8_t *b = src + blk * 144;
+    const uint4 hd = *reinterpret_cast<const uint4 *>(b);
+    const int chunk = i0 >> 6, r = i0 & 63, j = 2 * chunk + (r >> 5);
+    const uint32_t qw = *reinterpret_cast<const uint32_t *>(b + 16 + 32 * chunk + (r & 31));
+    uint8_t s[12];
+    *reinterpret_cast<uint32_t *>(s) = hd.y;
+    *reinterpret_cast<uint32_t *>(s + 4) = hd.z;
+    *reinterpret_cast<uint32_t *>(s + 8) = hd.w;
+    uint32_t sc, m;
+    scale_min_k4(j, s, sc, m);
+    const float d1 = f16_bits_to_f32(hd.x & 0xFFFFu) * (float)sc;
+    const float m1 = f16_bits_to_f32(hd.x >> 16) * (float)m;
+    const uint32_t q4 = (r < 32) ? (qw & 0x0F0F0F0Fu) : ((qw >> 4) & 0x0F0F0F0Fu);
+    float4 o;
+    o.x = d1 * (float)(q4 & 0xFFu) - m1;
+    o.y = d1 * (float)((q4 >> 8) & 0xFFu) - m1;
+    o.z = d1 * (float)((q4 >> 16) & 0xFFu) - m1;
+    o.w = d1 * (float)(q4 >> 24) - m1;
+    out[t] = o;
+  }
+}
+
+// Q8_0 split layout: one thread per 4 outputs.
+__global__ __launch_bounds__(kThreads) void k_dequant_q8(const uint32_t *__restrict__ qs,
+                                                        const uint16_t *__restrict__ dsc,
+                                                        uint64_t quads, float4 *__restrict__ out) {
+  const uint64_t stride = (uint64_t)gridDim.x * kThreads;
+  for (uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x; t < quads; t += stride) {
+    const uint32_t v = qs[t];
+    const float d = f16_bits_to_f32(dsc[t >> 3]);
+    float4 o;
+    o.x = d * (float)(int8_t)(v & 0xFFu);
+    o.y = d * (float)(int8_t)((v >> 8) & 0xFFu);
+    o.z = d * (float)(int8_t)((v >> 16) & 0xFFu);
+    o.w = d * (float)(int8_t)(v >> 24);
+    out[t] = o;
+  }
+}
+
+// Q6_K split layout: one thread per 4 outputs.
+__global__ __launch_bounds__(kThreads) void k_dequant_q6k(const uint8_t *__restrict__ rec,
+                                                         const uint16_t *__restrict__ dsc,
+                                                         uint64_t quads, float4 *__restrict__ out) {
+  const uint64_t stride = (uint64_t)gridDim.x * kThreads;
+  for (uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x; t < quads; t += stride) {
+    const uint64_t blk = t >> 6;
+    const int i0 = (int)(t & 63) * 4;
+    const int hf = i0 >> 7, r = i0 & 127, kk = r >> 5, l = r & 31;
+    const uint8_t *b = rec + blk * 208;
+    const uint32_t ql = *reinterpret_cast<const uint32_t *>(b + 64 * hf + 32 * (kk & 1) + l);
+    const uint32_t qh = *reinterpret_cast<const uint32_t *>(b + 128 + 32 * hf + l);
+    const float ds = f16_bits_to_f32(dsc[blk]) * (float)(int8_t)b[192 + 8 * hf + (l >> 4) + 2 * kk];
+    const uint32_t q = ((ql >> (4 * (kk >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * kk)) & 0x03030303u) << 4);
+    float4 o;
+    o.x = ds * ((float)(q & 0xFFu) - 32.0f);
+    o.y = ds * ((float)((q >> 8) & 0xFFu) - 32.0f);
+    o.z = ds * ((float)((q >> 16) & 0xFFu) - 32.0f);
+    o.w = ds * ((float)(q >> 24) - 32.0f);
+    out[t] = o;
+  }
+}
+
+unsigned grid_for(uint64_t items) {
+  const uint64_t want = (items + kThreads - 1) / kThreads;
+  return (unsigned)(want < 65536 ? (want ? want : 1) : 65536);
+}
+
+}  // namespace
+
+int launch_dequant_raw(int qtype, const uint8_t *src, uint64_t nblocks, float *out,
+                       hipStream_t s) {
+  Geometry g;
+  if (!geometry(qtype, &g)) return set_error(RQ_E_UNSUPPORTED, "no decoder for qtype %d", qtype);
+  const uint64_t total = nblocks * (uint64_t)g.elems;
+  if (total == 0) return RQ_OK;
+  hipLaunchKernelGGL(k_dequant_raw, dim3(grid_for(total)), dim3(kThreads), 0, s, qtype, g.elems,
+                     g.bytes, src, total, out);
+  return hipGetLastError() == hipSuccess ? RQ_OK
+                                         : set_error(RQ_E_DEVICE, "dequant launch failed");
+}
+
+int launch_dequant_weight(const rq_weight *w, float *out, hipStream_t s) {
+  const uint64_t quads = (uint64_t)w->n * (uint64_t)w->k / 4;
+  if (quads == 0) return RQ_OK;
+  switch (w->qtype) {
+    case RQ_Q4_K:
+      hipLaunchKernelGGL(k_dequant_q4k, dim3(grid_for(quads)), dim3(kThreads), 0, s, w->data,
+                         quads, reinterpret_cast<float4 *>(out));
+      break;
+    case RQ_Q8_0:
+      hipLaunchKernelGGL(k_dequant_q8, dim3(grid_for(quads)), dim3(kThreads), 0, s,
+                         reinterpret_cast<const uint32_t *>(w->data),
+                         reinterpret_cast<const uint16_t *>(w->data + w->aux_off), quads,
+                         reinterpret_cast<float4 *>(out));
+      break;
+    case RQ_Q6_K:
+      hipLaunchKernelGGL(k_dequant_q6k, dim3(grid_for(quads)), dim3(kThreads), 0, s, w->data,
+                         reinterpret_cast<const uint16_t *>(w->data + w->aux_off), quads,
+                         reinterpret_cast<float4 *>(out));
+      break;
+    default:
+      return launch_dequant_raw(w->qtype, w->data, w->nblocks, out, s);
+  }
+  return hipGetLastError() == hipSuccess ? RQ_OK
+                                         : set_error(RQ_E_DEVICE, "dequant launch failed");
+}
+
+}  // namespace rq

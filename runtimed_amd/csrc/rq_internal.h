@@ -1,0 +1,116 @@
+// rq_internal.h -- shared declarations for librq (gfx950).
+//
+// Device layouts held by a weight handle (all arrays 256-byte aligned):
+//   Q4_K, Q5_K, Q4_0, Q5_0  the GGUF block stream as uploaded.  A Q4_K block
+//                           is 144 = 9 x 16 bytes, so every block of a
+//                           16-aligned stream is 16-aligned.
+//   Q8_0                    quants: n*k int8 in flat element order, then
+//                           scales: one f16 per 32-element block.
+//   Q6_K                    208-byte records [ql 128 | qh 64 | scales 16] per
+//                           block (13 x 16 bytes), then one f16 d per block.
+// The split layouts keep every element value and the flat element order of
+// GGUF (dequant.rs:83-146); only the byte placement changes so that 16-byte
+// vector loads stay aligned.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/rq.h"
+
+struct rq_weight {
+  int qtype;
+  int device;
+  int64_t n, k;
+  uint64_t gguf_bytes;
+  uint64_t nblocks;
+  uint8_t *data;       // device base
+  uint64_t data_bytes; // device bytes held
+  uint64_t aux_off;    // offset of the scale array for Q8_0 / Q6_K
+};
+
+namespace rq {
+
+// Block geometry of GgmlDtype::block (dtype.rs:49-64) for the formats with a
+// decoder here.
+struct Geometry {
+  int elems;
+  int bytes;
+};
+bool geometry(int qtype, Geometry *g);
+
+int set_error(int code, const char *fmt, ...);
+hipStream_t as_stream(void *s);
+
+// ---- launchers (each returns RQ_OK or an error code and message) ----
+int launch_dequant_weight(const rq_weight *w, float *out, hipStream_t s);
+int launch_dequant_raw(int qtype, const uint8_t *src, uint64_t nblocks, float *out,
+                       hipStream_t s);
+// Fused matmul on a handle; returns RQ_E_UNSUPPORTED when the handle's
+// shape has no fused kernel (the caller then takes the decode path).
+int launch_linear_fused(const rq_weight *w, const void *x, int xtype, int64_t m, void *y,
+                        int ytype, hipStream_t s);
+// y = x * W^T with W dense f32 [n, k] in device memory.
+int launch_linear_dense_f32(const float *w, int64_t n, int64_t k, const void *x, int xtype,
+                            int64_t m, void *y, int ytype, hipStream_t s);
+int launch_fp8_quantize(const void *x, int xtype, int64_t m, int64_t k, int mode, uint8_t *xq,
+                        float *xs, hipStream_t s);
+int launch_fp8_gemm(const uint8_t *xq, const float *xs, int64_t m, const uint8_t *w,
+                    const float *ws, int64_t n, int64_t k, void *y, int ytype, hipStream_t s);
+
+// ---- exact scalar conversions shared by device code ----
+
+// f16 bit pattern -> f32 bit pattern, integer-exact including subnormals and
+// NaN payloads: the rule of f16_to_f32 (dequant.rs:11-33).
+__host__ __device__ __forceinline__ uint32_t f16_bits_to_f32_bits(uint32_t h) {
+  const uint32_t sign = (h >> 15) & 1u;
+  const uint32_t exp = (h >> 10) & 0x1Fu;
+  const uint32_t mant = h & 0x3FFu;
+  if (exp == 0) {
+    if (mant == 0) return sign << 31;
+    // A subnormal m * 2^-24 with its leading one at bit p is 2^(p-24) * 1.f.
+    const int p = 31 - __builtin_clz(mant);
+    return (sign << 31) | ((uint32_t)(103 + p) << 23) | (((mant << (10 - p)) & 0x3FFu) << 13);
+  }
+  if (exp == 31) return (sign << 31) | (0xFFu << 23) | (mant << 13);
+  return (sign << 31) | ((exp + 112u) << 23) | (mant << 13);
+}
+
+__host__ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  return __uint_as_float(f16_bits_to_f32_bits(h));
+}
+
+// f32 -> bf16 bits, round to nearest even, NaN stays NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// Store one f32 result as the requested output type.
+__device__ __forceinline__ void store_out(void *y, int ytype, int64_t idx, float v) {
+  if (ytype == RQ_F32) {
+    static_cast<float *>(y)[idx] = v;
+  } else if (ytype == RQ_BF16) {
+    static_cast<uint16_t *>(y)[idx] = (uint16_t)f32_to_bf16_bits(v);
+  } else {
+    static_cast<_Float16 *>(y)[idx] = (_Float16)v;
+  }
+}
+
+// Load 4 consecutive activations starting at element idx (idx % 4 == 0) as f32.
+__device__ __forceinline__ float4 load_x4(const void *x, int xtype, int64_t idx) {
+  if (xtype == RQ_F32) return *reinterpret_cast<const float4 *>(static_cast<const float *>(x) + idx);
+  const uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(x) + idx);
+  if (xtype == RQ_BF16) {
+    return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u),
+                       __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xFFFF0000u));
+  }
+  const _Float16 *h = reinterpret_cast<const _Float16 *>(&v);
+  return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+}
+
+}  // namespace rq

@@ -1,0 +1,130 @@
+"""Fused quantized matmuls (rq_linear) against the dense reference
+runtimed-gguf dequant + f32 matmul (linear_layer.rs:88-104), evaluated by the
+oracle in double precision on the bit-exact dequantized weights.
+
+Gate: normalized error max|y - r| / max|r| <= 1e-3 for f32 activations and
+f32 accumulation (decode), <= 2e-2 where activations or outputs are bf16."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from runtimed_amd import rq, synth
+from tests.conftest import norm_err
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-3
+TOL_BF16 = 2e-2
+
+
+def make(qtype, n, k, seed):
+    data = synth.weight_blocks(qtype, seed, n, k)
+    rc, wf = oracle.dequant_tensor(qtype, data, n * k)
+    assert rc == 0
+    return rq.QWeight(qtype, data, n, k), wf.reshape(n, k)
+
+
+def ref(x: np.ndarray, wf: np.ndarray) -> np.ndarray:
+    return oracle.linear_f64(x, wf)
+
+
+# The Q8_0 CPU-runnable workload (4864 x 896) and the Qwen2-0.5B decode set.
+DECODE_SHAPES = [(4864, 896), (896, 896), (128, 896), (896, 4864)]
+
+
+@pytest.mark.parametrize("qtype", [rq.Q8_0, rq.Q4_K, rq.Q6_K])
+@pytest.mark.parametrize("n,k", DECODE_SHAPES + [(2048, 2048), (512, 8192), (96, 1024)])
+def test_decode_gemv_f32(dev, qtype, n, k):
+    print(f"gemv qtype={qtype} n={n} k={k}", flush=True)
+    w, wf = make(qtype, n, k, 10 + n + k)
+    x = synth.activations(3, 1, k)
+    y = w.forward(torch.from_numpy(x).to(dev)).cpu().numpy()
+    assert y.shape == (1, n)
+    assert norm_err(y, ref(x, wf)) <= TOL_F32
+
+
+@pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0])
+@pytest.mark.parametrize("m", [2, 4, 8, 16, 64])
+def test_verify_small_m_bf16(dev, qtype, m):
+    n, k = 896, 4864
+    if qtype == rq.Q4_K:
+        n, k = 4864, 896
+    print(f"verify qtype={qtype} m={m}", flush=True)
+    w, wf = make(qtype, n, k, 20 + m)
+    xb = torch.from_numpy(synth.activations(4 + m, m, k)).to(torch.bfloat16)
+    y = w.forward(xb.to(dev), out_dtype=torch.float32).cpu().numpy()
+    assert norm_err(y, ref(xb.float().numpy(), wf)) <= TOL_BF16
+
+
+@pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K])
+def test_prefill_bf16_out(dev, qtype):
+    m, n, k = 128, 1024, 2048
+    w, wf = make(qtype, n, k, 31)
+    xb = torch.from_numpy(synth.activations(5, m, k)).to(torch.bfloat16)
+    y = w.forward(xb.to(dev)).float().cpu().numpy()
+    assert norm_err(y, ref(xb.float().numpy(), wf)) <= TOL_BF16
+
+
+@pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float16), (torch.float16, torch.float32),
+                                     (torch.bfloat16, torch.bfloat16)])
+def test_activation_and_output_types(dev, xdt, ydt):
+    w, wf = make(rq.Q4_K, 256, 512, 41)
+    x = torch.from_numpy(synth.activations(6, 3, 512)).to(xdt)
+    y = w.forward(x.to(dev), out_dtype=ydt).float().cpu().numpy()
+    tol = TOL_F32 if (xdt == torch.float32 and ydt == torch.float32) else TOL_BF16
+    assert norm_err(y, ref(x.float().numpy(), wf)) <= tol
+
+
+@pytest.mark.parametrize("qtype,n,k", [
+    (rq.Q4_K, 8, 160),    # k % 64 != 0: rows cut inside a chunk -> decode path
+    (rq.Q8_0, 2, 48),     # k % 32 != 0: blocks straddle rows mid-block
+    (rq.Q6_K, 2, 384),    # fused, row 1 starts in the second half of block 1
+    (rq.Q6_K, 4, 192),    # k % 128 != 0 -> decode path
+    (rq.Q4_0, 64, 96), (rq.Q5_0, 64, 96), (rq.Q5_K, 32, 512),
+])
+def test_other_shapes_and_formats(dev, qtype, n, k):
+    w, wf = make(qtype, n, k, 51 + k)
+    for m in (1, 5):
+        x = synth.activations(7 + m, m, k)
+        y = w.forward(torch.from_numpy(x).to(dev)).cpu().numpy()
+        assert norm_err(y, ref(x, wf)) <= TOL_F32
+
+
+def test_k896_rows_straddle_blocks(dev):
+    # K = 896 puts 3.5 super-blocks in a row: odd rows start mid-block.  A
+    # single nonzero input column isolates W[:, j] exactly.
+    n, k = 6, 896
+    w, wf = make(rq.Q4_K, n, k, 61)
+    for j in (0, 127, 128, 255, 640, 767, 768, 895):
+        x = np.zeros((1, k), np.float32)
+        x[0, j] = 1.0
+        y = w.forward(torch.from_numpy(x).to(dev)).cpu().numpy()[0]
+        assert np.array_equal(y, wf[:, j])
+
+
+def test_zero_rows_is_noop(dev):
+    w, _ = make(rq.Q4_K, 64, 256, 71)
+    x = torch.empty((0, 256), device=dev)
+    assert w.forward(x).shape == (0, 64)
+
+
+def test_linear_dense_and_quantized_kat(dev):
+    # linear_layer.rs:129-140 and the Marlin KAT [10, 14] of linear_layer.rs:143-155,
+    # here with Q8_0 blocks holding the small integer weights exactly (d = 1).
+    rows = [[1, 2, 3, 4] + [0] * 28, [2, 3, 4, 5] + [0] * 28]
+    blocks = b"".join(bytes([0x00, 0x3C]) + bytes(np.array(r, np.int8).view(np.uint8)) for r in rows)
+    w = rq.QWeight(rq.Q8_0, np.frombuffer(blocks, np.uint8), 2, 32)
+    x = torch.zeros((1, 32), device=dev)
+    x[0, :4] = 1.0
+    y = w.forward(x).cpu().numpy()
+    assert y.shape == (1, 2) and y[0].tolist() == [10.0, 14.0]
+
+
+def test_golden_gemv_on_device(dev):
+    from tests.golden import load_golden
+
+    for case in load_golden()["gemv"]:
+        w = rq.QWeight(case["qtype"], case["blocks"], case["n"], case["k"])
+        y = w.forward(torch.from_numpy(case["x"]).to(dev)).cpu().numpy()
+        assert norm_err(y, case["y"]) <= TOL_F32, case["name"]

@@ -1,0 +1,277 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the GPU checker.
+
+Each oracle function is checked by at least one of:
+  * the reference's own known-answer tests, transcribed verbatim
+    (dequant.rs:153-169, dequant_k.rs:118-178, dtype.rs:76-95,
+    fp8_weight.rs:105-134, fp8_gemm.rs:198-208, linear_layer.rs:129-160,
+    safetensors_load.rs:41-66);
+  * closed forms fixed by the format (IEEE half -> single for all 65,536
+    inputs, the OCP e4m3 table, torch's float8_e4m3fn conversion);
+  * an independent numpy restatement of each block format
+    (tests/reference_np.py) on thousands of seeded blocks, bit for bit.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from runtimed_amd import synth
+from tests import reference_np as ref
+
+
+# ---------------------------------------------------------------- f16 -----
+
+def test_f16_corners():  # dequant.rs:153-160
+    def f(h):
+        return np.uint32(oracle.f16_to_f32_bits(h)).view(np.float32)
+
+    assert f(0x3C00) == 1.0
+    assert f(0xBC00) == -1.0
+    assert f(0x0000) == 0.0
+    assert np.isinf(f(0x7C00))
+    assert abs(f(0x0001) - 2.0 ** -24) < 1e-30
+
+
+def test_f16_exhaustive_against_ieee():
+    # numpy's half widening is the IEEE closed form; it keeps NaN payloads
+    # exactly as dequant.rs:28 does (mantissa << 13, no quieting).
+    h = np.arange(65536, dtype=np.uint32)
+    got = np.array([oracle.f16_to_f32_bits(int(v)) for v in h], dtype=np.uint32)
+    want = h.astype(np.uint16).view(np.float16).astype(np.float32).view(np.uint32)
+    assert np.array_equal(got, want)
+
+
+# ----------------------------------------------------------- geometry -----
+
+def test_block_geometry():  # dtype.rs:85-95
+    assert oracle.geometry(8) == (32, 34)
+    assert oracle.geometry(10) == (256, 84)
+    assert oracle.geometry(11) == (256, 110)
+    assert oracle.geometry(12) == (256, 144)
+    assert oracle.geometry(13) == (256, 176)
+    assert oracle.geometry(14) == (256, 210)
+    assert oracle.geometry(0) == (1, 4)
+    assert oracle.geometry(2) == (32, 18)
+    assert oracle.geometry(6) == (32, 22)
+    assert oracle.geometry(99) is None  # dtype.rs:82 Unknown(99) not decodable
+    assert oracle.geometry(3) is None   # Q4_1 has no geometry
+
+
+# --------------------------------------------------------------- KATs -----
+
+def test_q8_0_scales_ints():  # dequant.rs:162-169
+    block = bytes([0x00, 0x3C]) + bytes(range(32))
+    out = oracle.dequant_block("q8_0", block)
+    assert np.array_equal(out, np.arange(32, dtype=np.float32))
+
+
+def test_q4_k_nibbles_and_high_bits():  # dequant_k.rs:118-129
+    block = bytes([0x00, 0x3C, 0x00, 0x00]) + bytes([65] + [1] * 11) + bytes([0x11] * 128)
+    out = oracle.dequant_block("q4_k", block)
+    assert out.shape == (256,)
+    assert np.all(out[0:32] == 1.0)
+    assert np.all(out[32:64] == 1.0)
+    assert np.all(out[128:160] == 17.0)
+
+
+def test_q5_k_high_bit_reuse_across_groups():  # dequant_k.rs:132-152
+    block = bytearray([0x00, 0x3C, 0x00, 0x00]) + bytearray([1] * 12) + bytearray(32) + bytearray([0x11] * 128)
+    assert np.all(oracle.dequant_block("q5_k", block) == 1.0)
+    hi = bytearray(block)
+    hi[16:48] = bytes([0xFF] * 32)
+    assert np.all(oracle.dequant_block("q5_k", hi) == 17.0)
+    one = bytearray(block)
+    one[16] = 0x01
+    out = oracle.dequant_block("q5_k", one)
+    assert out[0] == 17.0 and out[1] == 1.0 and out[32] == 1.0
+
+
+def test_q6_k_signed_values_and_scales():  # dequant_k.rs:155-177
+    block = bytearray(208) + bytearray([0x00, 0x3C])
+    block[192:208] = bytes([1] * 16)
+    assert np.all(oracle.dequant_block("q6_k", block) == -32.0)
+    q = bytearray(block)
+    q[0] = 0x11
+    q[128] = 0xFF
+    q[192:200] = bytes([1, 2, 3, 4, 5, 6, 7, 8])
+    out = oracle.dequant_block("q6_k", q)
+    assert out[0] == 17.0 and out[32] == 48.0 and out[64] == 85.0 and out[96] == 112.0
+    lane = bytearray(block)
+    lane[192:200] = bytes([1, 2, 3, 4, 5, 6, 7, 8])
+    lane[16] = 0x11
+    assert oracle.dequant_block("q6_k", lane)[16] == -62.0
+
+
+# ------------------------------------- independent restatements ----------
+
+@pytest.mark.parametrize("qtype", [8, 2, 6, 12, 13, 14])
+def test_blocks_match_numpy_restatement(qtype):
+    elems, bb = synth.GEOMETRY[qtype]
+    nb = 3000
+    data = synth.weight_blocks(qtype, 1234 + qtype, nb * elems, 1)
+    rc, got = oracle.dequant_tensor(qtype, data, nb * elems)
+    assert rc == oracle.OK
+    want = ref.DECODERS[qtype](data)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype", [8, 2, 6, 12, 13, 14])
+def test_raw_random_blocks_match_numpy_restatement(qtype):
+    # Every byte random: f16 scales hit subnormals, infinities and NaNs.
+    elems, bb = synth.GEOMETRY[qtype]
+    nb = 4000
+    data = synth.random_bytes(99 + qtype, nb * bb)
+    rc, got = oracle.dequant_tensor(qtype, data, nb * elems)
+    assert rc == oracle.OK
+    with np.errstate(all="ignore"):
+        want = ref.DECODERS[qtype](data)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_multithreaded_decode_matches_single():
+    data = synth.q4_k_blocks(5, 2048)
+    rc1, a = oracle.dequant_tensor(12, data, 2048 * 256)
+    rc2, b = oracle.dequant_tensor(12, data, 2048 * 256, threads=4)
+    assert rc1 == rc2 == 0 and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ------------------------------------------- dequant_tensor error rules ---
+
+def test_dequant_tensor_errors():  # dequant.rs:84-95, 143
+    data = np.zeros(1000, dtype=np.uint8)
+    assert oracle.dequant_tensor(3, data, 32)[0] == oracle.E_UNSUPPORTED    # Q4_1
+    assert oracle.dequant_tensor(10, data, 256)[0] == oracle.E_UNSUPPORTED  # Q2K: no decoder
+    assert oracle.dequant_tensor(11, data, 256)[0] == oracle.E_UNSUPPORTED  # Q3K
+    assert oracle.dequant_tensor(77, data, 256)[0] == oracle.E_UNSUPPORTED
+    assert oracle.dequant_tensor(12, data, 100)[0] == oracle.E_OVERFLOW
+    assert oracle.dequant_tensor(12, data[:143], 256)[0] == oracle.E_TRUNCATED
+    assert oracle.dequant_tensor(12, data[:144], 256)[0] == oracle.OK
+    assert oracle.dequant_tensor(14, data[:419], 512)[0] == oracle.E_TRUNCATED
+
+
+def test_dense_passthrough_types():  # dequant.rs:98-117
+    v = np.array([1.5, -2.25, 3e-8, np.inf], dtype=np.float32)
+    rc, out = oracle.dequant_tensor(0, v.view(np.uint8), 4)
+    assert rc == 0 and np.array_equal(out.view(np.uint32), v.view(np.uint32))
+    h = np.array([1.0, -0.5, 65504.0, 6e-8], dtype=np.float16)
+    rc, out = oracle.dequant_tensor(1, h.view(np.uint8), 4)
+    assert rc == 0 and np.array_equal(out, h.astype(np.float32))
+    bf = torch.tensor([1.0, -3.5, 1e30, 2.0 ** -100], dtype=torch.bfloat16)
+    rc, out = oracle.dequant_tensor(30, bf.view(torch.int16).numpy().view(np.uint8), 4)
+    assert rc == 0 and np.array_equal(out, bf.float().numpy())
+
+
+# ------------------------------------------------------------------ FP8 ---
+
+def test_e4m3_decode_kats():  # fp8_weight.rs:120, safetensors_load.rs:41-66
+    assert oracle.fp8_decode(0x38) == 1.0
+    assert oracle.fp8_decode(0x40) == 2.0
+    assert oracle.fp8_decode(0x30) == 0.5
+    assert oracle.fp8_decode(0x44) == 3.0
+
+
+def test_e4m3_decode_exhaustive():
+    got = np.array([oracle.fp8_decode(b) for b in range(256)], dtype=np.float32)
+    via_torch = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    table = ref.e4m3_table()
+    for want in (via_torch, table):
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan)
+        assert np.array_equal(got[~nan], want[~nan])
+    assert np.isnan(got[0x7F]) and np.isnan(got[0xFF]) and got[0x7E] == 448.0
+
+
+def _encoder_probe_values():
+    t = ref.e4m3_table()[:127].astype(np.float64)
+    mids = (t[:-1] + t[1:]) / 2.0
+    vals = np.concatenate([t, mids, np.nextafter(mids.astype(np.float32), 0),
+                           np.nextafter(mids.astype(np.float32), 1000),
+                           synth.normal(3, 20000) * 40.0, synth.normal(4, 2000) * 1e-3,
+                           [0.0, 447.9, 448.0, 448.5, 464.0, 480.0, 1e9, np.inf, 1e-45]])
+    vals = vals.astype(np.float32)
+    return np.concatenate([vals, -vals, [np.float32(-0.0), np.float32(np.nan)]]).astype(np.float32)
+
+
+def test_e4m3_reference_encoder_is_nearest_tie_low():  # load_safetensors.rs:53-69
+    x = _encoder_probe_values()
+    got = oracle.fp8_encode_array(x)
+    want = ref.e4m3_nearest_tie_low(x)
+    assert np.array_equal(got, want)
+    assert oracle.fp8_encode(-0.0) == 0x80 and oracle.fp8_encode(float("nan")) == 0x7F
+
+
+def test_e4m3_rne_encoder_matches_torch():
+    x = _encoder_probe_values()
+    x = x[~np.isnan(x)]
+    got = np.array([oracle.fp8_encode_rne(float(v)) for v in x], dtype=np.uint8)
+    want = torch.from_numpy(np.clip(x, -448.0, 448.0)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(got, want)
+
+
+def test_cpu_fp8_gemm_matches_reference():  # fp8_gemm.rs:198-208
+    x = np.array([[1.0, 2.0], [3.0, 4.0]], dtype=np.float32)
+    w = np.array([[0x38, 0x00], [0x00, 0x40]], dtype=np.uint8)  # [[1, 0], [0, 2]]
+    s = np.array([2.0, 0.5], dtype=np.float32)
+    y = oracle.fp8_gemm_fallback(x, w, s)
+    assert y.shape == (2, 2)
+    assert y.reshape(-1).tolist() == [2.0, 2.0, 6.0, 4.0]
+
+
+def test_fp8_weight_forward_matches_dequant():  # fp8_weight.rs:117-133
+    w = np.array([[0x38, 0x40], [0x30, 0x44]], dtype=np.uint8)
+    s = np.array([2.0, 0.5], dtype=np.float32)
+    x = np.array([[1.5, -2.0]], dtype=np.float32)
+    out = oracle.fp8_gemm_fallback(x, w, s)
+    deq = np.array([[1.0, 2.0], [0.5, 3.0]], dtype=np.float32) * s[:, None]
+    assert np.allclose(out, x @ deq.T, atol=1e-3)
+    assert out.reshape(-1).tolist() == [-5.0, -2.625]
+
+
+def test_per_token_quantize_closed_form():
+    x = synth.activations(7, 16, 512)
+    x[3] = 0.0
+    xq, xs = oracle.fp8_quantize_rows(x)
+    amax = np.abs(x).max(axis=1)
+    assert xs[3] == 0.0 and not xq[3].any()
+    live = amax > 0
+    assert np.array_equal(xs[live], (amax[live] / np.float32(448.0)).astype(np.float32))
+    dec = torch.from_numpy(xq).view(torch.float8_e4m3fn).float().numpy()
+    # the largest element maps to +-448 exactly; every code is within half a
+    # step (relative 2^-4) of x / s
+    assert np.all(np.abs(dec[live]).max(axis=1) == 448.0)
+    inv = (np.float32(448.0) / amax[live]).astype(np.float32)
+    scaled = (x[live] * inv[:, None]).astype(np.float32)
+    want = torch.from_numpy(scaled).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(xq[live], want)
+
+
+def test_quantized_gemm_f64_closed_form():
+    xq = synth.random_bytes(8, 4 * 64).reshape(4, 64) & 0x77  # finite codes
+    w = synth.random_bytes(9, 6 * 64).reshape(6, 64) & 0xF7
+    xs = np.array([1.0, 0.5, 2.0, 0.25], dtype=np.float32)
+    ws = np.linspace(0.5, 2.0, 6).astype(np.float32)
+    y = oracle.fp8_gemm_quantized_f64(xq, xs, w, ws)
+    t = ref.e4m3_table().astype(np.float64)
+    want = (t[xq] @ t[w].T) * xs[:, None] * ws[None, :]
+    assert np.allclose(y, want, rtol=1e-15, atol=0)
+
+
+# ------------------------------------------------------------ linear ------
+
+def test_linear_dense_kats():  # linear_layer.rs:129-160
+    w = np.array([[1, 2, 3], [4, 5, 6]], dtype=np.float32)
+    y = oracle.linear_f64(np.ones((1, 3), np.float32), w)
+    assert y.shape == (1, 2) and y.reshape(-1).tolist() == [6.0, 15.0]
+    w2 = np.array([[1, 2, 3, 4], [2, 3, 4, 5]], dtype=np.float32)
+    assert oracle.linear_f64(np.ones((1, 4), np.float32), w2).reshape(-1).tolist() == [10.0, 14.0]
+
+
+def test_linear_matches_numpy():
+    x = synth.activations(1, 5, 300)
+    w = synth.activations(2, 7, 300)
+    want = x.astype(np.float64) @ w.astype(np.float64).T
+    assert np.allclose(oracle.linear_f64(x, w), want, rtol=1e-12, atol=1e-12)
+    y32 = oracle.linear_f32(x, w, threads=2)
+    assert np.max(np.abs(y32 - want)) / np.max(np.abs(want)) < 1e-5
