@@ -256,6 +256,43 @@ def extra_fp8(torch, rq, synth, dev, steps, warmup):
             "quantize_ms": round(ms_q, 4)}
 
 
+def mode_gate(torch, rq, synth, dev, steps, warmup, eager=False):
+    """Only the dominant kernel: R distinct 4864x896 Q4_K gate weights
+    (R * 2.45 MB >= 1 GB), one GEMV each, in one HIP graph (or launched
+    eagerly, for counter collection)."""
+    n, k = 4864, 896
+    copies = 512
+    blocks = synth.q4_k_blocks(104, n * k // 256)
+    W = [rq.QWeight(rq.Q4_K, blocks, n, k) for _ in range(copies)]
+    x = torch.from_numpy(synth.activations(1, 1, k)).to(dev)
+    y = torch.empty((1, n), device=dev)
+    b = n * k // 256 * Q4K_BLOCK + k * 4 + n * 4
+    if eager:
+        for _ in range(steps):
+            for w in W:
+                w.forward(x, out=y)
+        torch.cuda.synchronize()
+        print(json.dumps({"mode": "gate-eager", "launches": copies * steps, "bytes_per_launch": b}), flush=True)
+        return
+    g = capture(torch, lambda: [w.forward(x, out=y) for w in W])
+    ms = Timer(torch).replay(g, steps, warmup) / copies
+    print(json.dumps({"mode": "gate", "launches": copies * (steps + warmup + 2), "us_per_launch": round(ms * 1e3, 3),
+                      "GB/s": round(b / (ms * 1e-3) / 1e9, 1)}), flush=True)
+
+
+def mode_copy(torch, dev, steps):
+    """A plain device copy of 512 MiB: the calibration kernel for HBM byte
+    counters (FETCH_SIZE / WRITE_SIZE per dispatch vs. 512 MiB moved)."""
+    nbytes = 512 << 20
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "copy", "bytes_read_per_copy": nbytes, "bytes_written_per_copy": nbytes,
+                      "copies": steps}), flush=True)
+
+
 def traffic_from_profile():
     p = ROOT / "profiles" / "traffic_q4k_gate_gemv.json"
     if p.exists():
@@ -275,6 +312,9 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
+    ap.add_argument("--mode", choices=["full", "gate", "copy"], default="full",
+                    help="gate: only the dominant GEMV; copy: counter calibration copy")
+    ap.add_argument("--eager", action="store_true", help="gate mode without a HIP graph")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the quantized linear path runs on a single MI355X "
@@ -288,6 +328,10 @@ def main():
 
     rq.lib()
     dev = torch.device("cuda", 0)
+    if args.mode == "gate":
+        return mode_gate(torch, rq, synth, dev, args.steps, args.warmup, args.eager)
+    if args.mode == "copy":
+        return mode_copy(torch, dev, args.steps)
     log(f"decode workload: {args.layers} layer copies, steps={args.steps} warmup={args.warmup}")
     W, ms, gate_ms = decode_workload(torch, rq, synth, args.layers, args.steps, args.warmup, dev)
     step_bytes = layer_bytes() * args.layers

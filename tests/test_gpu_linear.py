@@ -128,3 +128,14 @@ def test_golden_gemv_on_device(dev):
         w = rq.QWeight(case["qtype"], case["blocks"], case["n"], case["k"])
         y = w.forward(torch.from_numpy(case["x"]).to(dev)).cpu().numpy()
         assert norm_err(y, case["y"]) <= TOL_F32, case["name"]
+
+
+@pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0])
+@pytest.mark.parametrize("m,n,k", [(257, 130, 512), (33, 1000, 256), (65, 64, 1024), (300, 256, 2048)])
+def test_mfma_gemm_edge_tiles(dev, qtype, m, n, k):
+    # bf16 activations with m > 1 run on the matrix cores; tiles are 32..256 x 128
+    w, wf = make(qtype, n, k, 81 + m + n)
+    xb = torch.from_numpy(synth.activations(9 + m, m, k)).to(torch.bfloat16)
+    for ydt in (torch.float32, torch.bfloat16):
+        y = w.forward(xb.to(dev), out_dtype=ydt).float().cpu().numpy()
+        assert norm_err(y, ref(xb.float().numpy(), wf)) <= TOL_BF16
