@@ -18,7 +18,11 @@ LIB = PKG / "librq.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["rq_api.cpp", "rq_dequant.hip", "rq_gemv.hip", "rq_fp8.hip", "rq_gemm.hip"]
+SOURCES = ["csrc/rq_api.cpp", "csrc/rq_dequant.hip", "csrc/rq_gemv.hip", "csrc/rq_fp8.hip",
+           "csrc/rq_gemm.hip", "host/rq_host.cpp"]
+ROOT = PKG.parent
+HOST_TEST_SRC = ROOT / "tests" / "cpp" / "test_host.cpp"
+HOST_TEST_BIN = ROOT / "tests" / "cpp" / "test_host"
 
 # Packed FP32 ops stay off: the compiler must not emit v_pk_{add,mul,fma}_f32.
 COMMON = [
@@ -29,7 +33,7 @@ COMMON = [
 
 def _compile(src: str) -> Path:
     obj = OUT / (Path(src).stem + ".o")
-    cmd = [HIPCC, *COMMON, "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON, "-x", "hip", "-c", str(PKG / src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{res.stderr}")
@@ -38,7 +42,7 @@ def _compile(src: str) -> Path:
 
 def build(verbose: bool = False) -> Path:
     OUT.mkdir(exist_ok=True)
-    srcs = [s for s in SOURCES if (CSRC / s).exists()]
+    srcs = [s for s in SOURCES if (PKG / s).exists()]
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB.with_suffix(".so.tmp")
@@ -50,6 +54,21 @@ def build(verbose: bool = False) -> Path:
     if verbose:
         print(f"built {LIB}")
     return LIB
+
+
+def build_host_tests(verbose: bool = False) -> Path:
+    """The C++ test program of the host layer; links librq.so and the oracle
+    (test infrastructure) through rpaths relative to the binary."""
+    oracle_dir = ROOT / "oracle"
+    cmd = [HIPCC, "-O2", "-std=c++17", f"--offload-arch={ARCH}", "-x", "hip", str(HOST_TEST_SRC),
+           "-o", str(HOST_TEST_BIN), f"-L{PKG}", "-lrq", f"-L{oracle_dir}", "-lrq_oracle",
+           "-Wl,-rpath,$ORIGIN/../../runtimed_amd", "-Wl,-rpath,$ORIGIN/../../oracle"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"host test build failed:\n{res.stderr}")
+    if verbose:
+        print(f"built {HOST_TEST_BIN}")
+    return HOST_TEST_BIN
 
 
 if __name__ == "__main__":

@@ -1,0 +1,194 @@
+// rq_host.hpp -- C++ host layer above the librq C ABI, mirroring the Rust
+// interface of runtimed's quantized linear path so that callers (and tests)
+// read as they do against the reference:
+//
+//   GgufFile            crates/runtimed-gguf/src/header.rs:109-219
+//   QMatMul             the q_map value, candle QMatMul::QTensor (load_gguf.rs:28-38)
+//   Weights             crates/runtimed-model/src/weights/store.rs:12-166,
+//                       linear_layer.rs:45-105, load_gguf.rs:40-120
+//   Fp8Weight           crates/runtimed-model/src/weights/fp8_weight.rs:9-97
+//   SubstratePort /
+//   HipSubstrate        crates/runtimed-model/src/substrate/port.rs:14-77 (fp8_gemm)
+//   ModelError/GgufError crates/runtimed-model/src/error.rs:5-27,
+//                       crates/runtimed-gguf/src/error.rs:3-37
+//
+// Errors are thrown as exceptions carrying the reference's error kind.  Device
+// memory is HIP memory on one ordinal; every call runs on the stream given at
+// construction (default: the legacy stream).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/rq.h"
+
+namespace runtimed {
+
+enum class DType { F32, F16, BF16, F8E4M3, U8, U32 };
+size_t dtype_size(DType t);
+int dtype_rq(DType t);  // rq_ftype, or -1
+
+// GgufError (crates/runtimed-gguf/src/error.rs:3-37)
+struct GgufError : std::runtime_error {
+  enum Kind { Io, BadMagic, Version, Truncated, MetaType, Range, Overflow, Unsupported };
+  Kind kind;
+  GgufError(Kind k, const std::string &msg) : std::runtime_error(msg), kind(k) {}
+  bool is_missing() const { return kind == Io; }
+};
+
+// ModelError (crates/runtimed-model/src/error.rs:5-27)
+struct ModelError : std::runtime_error {
+  enum Kind { Arch, Config, MissingWeight, Shape, Gguf };
+  Kind kind;
+  std::string name;
+  std::vector<size_t> expected, got;
+  ModelError(Kind k, const std::string &msg) : std::runtime_error(msg), kind(k) {}
+  static ModelError shape(const std::string &name, std::vector<size_t> expected,
+                          std::vector<size_t> got);
+};
+
+// A dense device tensor (row-major).  A tensor with no storage ("meta") only
+// carries dims and dtype.
+class Tensor {
+ public:
+  Tensor() = default;
+  static Tensor zeros(std::vector<size_t> dims, DType t, int device);
+  static Tensor from_host(const void *src, std::vector<size_t> dims, DType t, int device);
+  static Tensor meta(std::vector<size_t> dims, DType t);
+  std::vector<uint8_t> to_host() const;
+  template <class T>
+  std::vector<T> to_vec() const {
+    auto b = to_host();
+    return std::vector<T>(reinterpret_cast<const T *>(b.data()),
+                          reinterpret_cast<const T *>(b.data() + b.size()));
+  }
+  const std::vector<size_t> &dims() const { return dims_; }
+  size_t dim(size_t i) const { return dims_.at(i); }
+  size_t elem_count() const;
+  DType dtype() const { return dtype_; }
+  int device() const { return device_; }
+  void *data() const { return ptr_.get(); }
+  bool has_storage() const { return ptr_ != nullptr; }
+
+ private:
+  std::shared_ptr<void> ptr_;
+  std::vector<size_t> dims_;
+  DType dtype_ = DType::F32;
+  int device_ = -1;
+};
+
+// MetaValue / TensorInfo / GgufFile (header.rs:14-39, 109-219), GGUF v3.
+struct TensorInfo {
+  std::string name;
+  std::vector<uint64_t> dims;  // [fast, slow]
+  uint32_t dtype;              // GgmlDtype id
+  uint64_t offset;             // absolute file offset
+  size_t n_elements;
+};
+
+class GgufFile {
+ public:
+  static GgufFile open(const std::string &path);
+  static GgufFile parse(std::vector<uint8_t> bytes);
+  const TensorInfo *tensor(const std::string &name) const;
+  // Bounds-checked raw bytes (header.rs:191-205).
+  const uint8_t *tensor_bytes(const TensorInfo &info, size_t *len) const;
+  std::vector<TensorInfo> tensors;
+  std::map<std::string, std::string> meta_str;  // string-valued metadata
+  uint64_t alignment = 32;
+
+ private:
+  std::vector<uint8_t> bytes_;
+};
+
+// The quantized q_map value: a librq weight handle behind shared ownership
+// (Arc<QMatMul> in store.rs:18).
+class QMatMul {
+ public:
+  QMatMul(int qtype, const void *blocks, size_t nbytes, size_t n, size_t k, int device);
+  Tensor forward(const Tensor &x, void *stream = nullptr) const;  // y = x W^T
+  Tensor dequantize(void *stream = nullptr) const;                // [n, k] f32
+  size_t storage_size_in_bytes() const;
+  size_t n() const { return n_; }
+  size_t k() const { return k_; }
+  int device() const { return device_; }
+  int qtype() const { return qtype_; }
+
+ private:
+  std::shared_ptr<rq_weight> w_;
+  size_t n_, k_;
+  int device_, qtype_;
+};
+
+// SubstratePort (port.rs:14-77), the FP8 entry only.
+class SubstratePort {
+ public:
+  virtual ~SubstratePort() = default;
+  virtual Tensor fp8_gemm(const Tensor &x, const Tensor &w, const Tensor *scale) const = 0;
+};
+
+// librq behind the port: x is encoded with the reference's unscaled e4m3
+// encoder (fp8_gemm.rs:94-101) unless per_token is set; output F16 when x is
+// F16 or F8E4M3, else F32 (fp8_gemm.rs:106).
+class HipSubstrate : public SubstratePort {
+ public:
+  explicit HipSubstrate(bool per_token = false, void *stream = nullptr)
+      : per_token_(per_token), stream_(stream) {}
+  Tensor fp8_gemm(const Tensor &x, const Tensor &w, const Tensor *scale) const override;
+
+ private:
+  bool per_token_;
+  void *stream_;
+};
+
+// Fp8Weight (fp8_weight.rs:9-97).
+class Fp8Weight {
+ public:
+  static Fp8Weight create(Tensor weight, Tensor scale, size_t in_dim, size_t out_dim);
+  size_t in_dim() const { return in_dim_; }
+  size_t out_dim() const { return out_dim_; }
+  size_t resident_bytes() const;
+  Tensor forward(const Tensor &x, const SubstratePort &port) const;
+  const Tensor &weight() const { return weight_; }
+  const Tensor &scale() const { return scale_; }
+
+ private:
+  Tensor weight_, scale_;
+  size_t in_dim_ = 0, out_dim_ = 0;
+};
+
+// Weights (store.rs:12-19): dense map + quantized q_map.
+class Weights {
+ public:
+  static Weights from_parts(int device, std::unordered_map<std::string, Tensor> map);
+  static Weights from_quantized(int device, std::unordered_map<std::string, Tensor> map,
+                                std::unordered_map<std::string, std::shared_ptr<QMatMul>> q_map);
+  // load_gguf.rs:40-120: 2-D quantized tensors become QMatMul handles (raw
+  // block bytes uploaded as they are), dense tensors are uploaded as their
+  // dtype; a missing output.weight aliases token_embd.weight.
+  static Weights load(const GgufFile &file, int device);
+
+  Tensor linear(const Tensor &x, const std::string &name) const;        // linear_layer.rs:45-66
+  Tensor linear_dense(const Tensor &x, const std::string &name) const;  // linear_layer.rs:68-105
+  Tensor get(const std::string &name) const;                            // store.rs:78-101
+  const Tensor &get_raw(const std::string &name) const;                 // store.rs:103-107
+  std::shared_ptr<QMatMul> q_matmul(const std::string &name) const;
+  size_t resident_bytes() const;                                         // store.rs:57-76
+  bool contains_key(const std::string &name) const;
+  int device() const { return device_; }
+  void set_substrate(std::shared_ptr<SubstratePort> s) { substrate_ = std::move(s); }
+
+ private:
+  int device_ = 0;
+  std::unordered_map<std::string, Tensor> map_;
+  std::unordered_map<std::string, std::shared_ptr<QMatMul>> q_map_;
+  std::shared_ptr<SubstratePort> substrate_ = std::make_shared<HipSubstrate>();
+};
+
+}  // namespace runtimed
