@@ -293,6 +293,24 @@ def mode_copy(torch, dev, steps):
                       "copies": steps}), flush=True)
 
 
+def mode_fp8(torch, rq, synth, dev, steps):
+    """Only the FP8 GEMM 2048x14336x4096 (eager launches, for counters)."""
+    r = extra_fp8(torch, rq, synth, dev, steps, 1)
+    print(json.dumps({"mode": "fp8", **r}), flush=True)
+
+
+def mode_prefill_head(torch, rq, synth, dev, steps):
+    """Only the Q6_K 262144x2048 head GEMM at M=512 (eager, for counters)."""
+    m, n, k = 512, 262144, 2048
+    w = rq.QWeight(rq.Q6_K, synth.weight_blocks(rq.Q6_K, 7, n, k), n, k)
+    x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    for _ in range(steps):
+        w.forward(x, out=y)
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "prefill-head", "launches": steps}), flush=True)
+
+
 def traffic_from_profile():
     p = ROOT / "profiles" / "traffic_q4k_gate_gemv.json"
     if p.exists():
@@ -312,7 +330,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
-    ap.add_argument("--mode", choices=["full", "gate", "copy"], default="full",
+    ap.add_argument("--mode", choices=["full", "gate", "copy", "fp8", "prefill-head"], default="full",
                     help="gate: only the dominant GEMV; copy: counter calibration copy")
     ap.add_argument("--eager", action="store_true", help="gate mode without a HIP graph")
     args = ap.parse_args()
@@ -332,6 +350,10 @@ def main():
         return mode_gate(torch, rq, synth, dev, args.steps, args.warmup, args.eager)
     if args.mode == "copy":
         return mode_copy(torch, dev, args.steps)
+    if args.mode == "fp8":
+        return mode_fp8(torch, rq, synth, dev, args.steps)
+    if args.mode == "prefill-head":
+        return mode_prefill_head(torch, rq, synth, dev, args.steps)
     log(f"decode workload: {args.layers} layer copies, steps={args.steps} warmup={args.warmup}")
     W, ms, gate_ms = decode_workload(torch, rq, synth, args.layers, args.steps, args.warmup, dev)
     step_bytes = layer_bytes() * args.layers

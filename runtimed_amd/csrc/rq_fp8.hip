@@ -12,13 +12,16 @@
 //     reference applies the per-channel scale as an extra broadcast_mul pass
 //     (fp8_gemm.rs:180-186).
 //
-// GEMM tiling: a 256-thread workgroup computes a 128 x 128 tile of y; the
-// four waves own 64 x 64 quadrants (2 x 2 MFMA tiles of 32 x 32).  K advances
-// 128 bytes per step through two LDS buffers (double buffering), rows padded
-// to 144 bytes so that the 32 lanes reading one MFMA operand column touch
-// distinct 16-byte bank groups.
+// GEMM tiling: a 256-thread workgroup computes a 256 x 256 tile of y with
+// 128 x 128 per wave (4 x 4 MFMA tiles of 32 x 32, accumulators in AGPRs) for
+// large problems (K-step 64 bytes, LDS rows of 80 bytes), or 128 x 128 with
+// 64 x 64 per wave otherwise (K-step 128 bytes, rows of 144 bytes).  Two LDS
+// buffers (double buffering); the row padding makes the 32 lanes that read
+// one MFMA operand column touch distinct 16-byte bank groups.
 //
 // Roofline: MFMA-bound (fp8 dense peak 5.0 PFLOP/s); flops = 2*m*n*k.
+#include <stdlib.h>
+
 #include "rq_internal.h"
 
 namespace rq {
@@ -130,45 +133,57 @@ __global__ __launch_bounds__(256) void k_fp8_gemm_scalar(const uint8_t *__restri
   store_out(y, ytype, idx, acc * (sx * sw));
 }
 
-constexpr int BM = 128, BN = 128, BK = 128, LDS_STRIDE = BK + 16;
-
+// A BM x BN tile of y per 256-thread workgroup of WM x WN waves; each wave
+// owns (BM/WM) x (BN/WN) = MI x NI MFMA tiles of 32 x 32.  With 128 x 128 wave
+// tiles every 32-byte operand fragment read from LDS feeds four MFMAs.  BK is
+// the K-step in bytes (64 or 128); LDS rows are BK + 16 bytes.
+template <int BM, int BN, int WM, int WN, int BK>
 __global__ __launch_bounds__(256) void k_fp8_gemm_mfma(const uint8_t *__restrict__ a,
                                                       const float *__restrict__ xs, int64_t m,
                                                       const uint8_t *__restrict__ b,
                                                       const float *__restrict__ ws, int64_t n,
                                                       int64_t k, void *__restrict__ y, int ytype) {
+  static_assert(WM * WN == 4, "four waves");
+  constexpr int LDS_STRIDE = BK + 16;
+  constexpr int TPR = BK / 16;              // threads per row in a load round
+  constexpr int RPR = 256 / TPR;            // rows per load round
+  constexpr int MI = BM / WM / 32, NI = BN / WN / 32;
+  constexpr int A_LOADS = BM / RPR, B_LOADS = BN / RPR;  // 16-byte loads per thread per step
   __shared__ __attribute__((aligned(16))) uint8_t As[2][BM * LDS_STRIDE];
   __shared__ __attribute__((aligned(16))) uint8_t Bs[2][BN * LDS_STRIDE];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
 
-  // Global -> register staging: each thread moves 4 x 16 bytes of A and of B.
-  const int lrow = tid >> 3, lcol = (tid & 7) * 16;
-  uint4 ra[4], rb[4];
+  // Global -> register staging: TPR threads per row, RPR rows per round.
+  const int lrow = tid / TPR, lcol = (tid % TPR) * 16;
+  uint4 ra[A_LOADS], rb[B_LOADS];
   auto gload = [&](int64_t k0) {
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int r = lrow + 32 * it;
-      const int64_t gm = m0 + r, gn = n0 + r;
+    for (int it = 0; it < A_LOADS; ++it) {
+      const int64_t gm = m0 + lrow + RPR * it;
       ra[it] = gm < m ? *reinterpret_cast<const uint4 *>(a + gm * k + k0 + lcol) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int it = 0; it < B_LOADS; ++it) {
+      const int64_t gn = n0 + lrow + RPR * it;
       rb[it] = gn < n ? *reinterpret_cast<const uint4 *>(b + gn * k + k0 + lcol) : make_uint4(0, 0, 0, 0);
     }
   };
   auto sstore = [&](int buf) {
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int r = lrow + 32 * it;
-      *reinterpret_cast<uint4 *>(&As[buf][r * LDS_STRIDE + lcol]) = ra[it];
-      *reinterpret_cast<uint4 *>(&Bs[buf][r * LDS_STRIDE + lcol]) = rb[it];
-    }
+    for (int it = 0; it < A_LOADS; ++it)
+      *reinterpret_cast<uint4 *>(&As[buf][(lrow + RPR * it) * LDS_STRIDE + lcol]) = ra[it];
+#pragma unroll
+    for (int it = 0; it < B_LOADS; ++it)
+      *reinterpret_cast<uint4 *>(&Bs[buf][(lrow + RPR * it) * LDS_STRIDE + lcol]) = rb[it];
   };
 
-  f32x16 acc[2][2];
+  f32x16 acc[MI][NI];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = (f32x16){0};
+    for (int j = 0; j < NI; ++j) acc[i][j] = (f32x16){0};
 
   const int64_t nk = k / BK;
   gload(0);
@@ -180,49 +195,239 @@ __global__ __launch_bounds__(256) void k_fp8_gemm_mfma(const uint8_t *__restrict
 #pragma unroll
     for (int ks = 0; ks < BK / 64; ++ks) {
       const int kb = ks * 64 + 32 * (lane >> 5);
-      i32x8 fa[2], fb[2];
+      i32x8 fa[MI], fb[NI];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int ar = wm * 64 + i * 32 + (lane & 31);
+      for (int i = 0; i < MI; ++i) {
+        const int ar = wm * (BM / WM) + i * 32 + (lane & 31);
         const uint4 *pa = reinterpret_cast<const uint4 *>(&As[buf][ar * LDS_STRIDE + kb]);
         const uint4 a0 = pa[0], a1 = pa[1];
         fa[i] = (i32x8){(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-        const int br = wn * 64 + i * 32 + (lane & 31);
-        const uint4 *pb = reinterpret_cast<const uint4 *>(&Bs[buf][br * LDS_STRIDE + kb]);
-        const uint4 b0 = pb[0], b1 = pb[1];
-        fb[i] = (i32x8){(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
       }
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int j = 0; j < NI; ++j) {
+        const int br = wn * (BN / WN) + j * 32 + (lane & 31);
+        const uint4 *pb = reinterpret_cast<const uint4 *>(&Bs[buf][br * LDS_STRIDE + kb]);
+        const uint4 b0 = pb[0], b1 = pb[1];
+        fb[j] = (i32x8){(int)b0.x, (int)b0.y, (int)b0.z, (int)b0.w, (int)b1.x, (int)b1.y, (int)b1.z, (int)b1.w};
+      }
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fb[j], acc[i][j], 0, 0,
                                                                       0, 0, 0, 0);
     }
-    if (kt + 1 < nk) {
-      sstore(buf ^ 1);
-    }
+    if (kt + 1 < nk) sstore(buf ^ 1);
     __syncthreads();
   }
 
   // Epilogue: C layout of the 32x32 tile: column lane%32, row
   // 8*(r/4) + 4*(lane/32) + r%4 for register r.
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
-      if (col >= n) continue;
-      const float sw = ws ? ws[col] : 1.0f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < m) {
+  static_for<MI>([&](auto I) {
+    static_for<NI>([&](auto J) {
+      const int64_t col = n0 + wn * (BN / WN) + J * 32 + (lane & 31);
+      const float sw = (col < n && ws) ? ws[col] : 1.0f;
+      static_for<16>([&](auto R) {
+        const int64_t row = m0 + wm * (BM / WM) + I * 32 + 8 * (R / 4) + 4 * (lane >> 5) + (R % 4);
+        if (row < m && col < n) {
           const float sx = xs ? xs[row] : 1.0f;
-          store_out(y, ytype, row * n + col, acc[i][j][r] * (sx * sw));
+          store_out(y, ytype, row * n + col, acc[I][J][decltype(R)::value] * (sx * sw));
         }
-      }
+      });
+    });
+  });
+}
+
+// ---- pipelined 256 x 256 kernel ------------------------------------------
+//
+// Four waves of 128 x 128 (4 x 4 MFMA tiles, 256 accumulators in AGPRs).  K
+// advances 64 bytes per step through four LDS stages of 32 KB (A rows then B
+// rows, 64 bytes each), filled by direct global -> LDS loads
+// (global_load_lds_dwordx4: lane L of a wave lands at base + 16*L) issued
+// three steps ahead, so about three steps of MFMA work cover the load latency
+// without staging registers.  Rows carry no padding; instead the four 16-byte
+// chunks of row r are stored XOR-swizzled by (r >> 2) & 3, so the 32 lanes
+// that read one operand column of 32 rows hit 16 distinct 16-byte bank slots.
+constexpr int P_STAGE = 32768, P_B = 16384;
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
+
+template <int VM>
+__device__ __forceinline__ void wait_vm() {
+  // s_waitcnt vmcnt(VM) with expcnt / lgkmcnt left at their maxima (gfx9 encoding)
+  __builtin_amdgcn_s_waitcnt((VM & 0xF) | ((VM >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Issue the direct loads of one stage.  The LDS pointer is __restrict__ so
+// that, once inlined, the accesses carry scoped alias metadata and the
+// compiler's wait insertion can tell the four stage buffers apart instead of
+// draining every load before each LDS read.
+__device__ __forceinline__ void pipe_issue(uint8_t *__restrict__ S, const uint8_t *const (&ga)[4],
+                                           const uint8_t *const (&gb)[4], int64_t k0, int wave) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    __builtin_amdgcn_global_load_lds(ga[j] + k0, (lds_void *)(S + (64 * wave + 16 * j) * 64), 16, 0, 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    __builtin_amdgcn_global_load_lds(gb[j] + k0, (lds_void *)(S + P_B + (64 * wave + 16 * j) * 64), 16, 0, 0);
+}
+
+// LDS operand reads are issued as explicit ds_read_b128 and completed by one
+// s_waitcnt lgkmcnt(0) that takes every loaded register as an operand, so no
+// use can be scheduled before the wait.  (As compiler-visible LDS loads they
+// would each be preceded by a wait for all in-flight direct loads, because
+// the compiler cannot prove that those target another stage buffer.)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x4 ds_read16(const uint8_t *p) {
+  u32x4 v;
+  const uint32_t off = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(off));
+  return v;
+}
+
+// Fragment registers of one K-step: 8 x 16 bytes of A rows, 8 of B rows.
+struct Frags {
+  u32x4 x[16];
+};
+
+// Address (LDS byte offset) of fragment f (0..7 A, 8..15 B) of a stage.
+__device__ __forceinline__ const uint8_t *frag_addr(const uint8_t *S, int f, int wm, int wn, int lane) {
+  const int g = lane >> 5, half = f & 1, t = (f >> 1) & 3;
+  const int r = (f < 8 ? 128 * wm : 128 * wn) + 32 * t + (lane & 31);
+  return S + (f < 8 ? 0 : P_B) + r * 64 + 16 * ((2 * g + half) ^ swz(r));
+}
+
+__device__ __forceinline__ i32x8 frag_a(const Frags &F, int i) {
+  const u32x4 x0 = F.x[2 * i], x1 = F.x[2 * i + 1];
+  return (i32x8){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+}
+
+__device__ __forceinline__ void wait_lds(Frags &F) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(F.x[0]), "+v"(F.x[1]), "+v"(F.x[2]), "+v"(F.x[3]));
+  asm volatile("" : "+v"(F.x[4]), "+v"(F.x[5]), "+v"(F.x[6]), "+v"(F.x[7]));
+  asm volatile("" : "+v"(F.x[8]), "+v"(F.x[9]), "+v"(F.x[10]), "+v"(F.x[11]));
+  asm volatile("" : "+v"(F.x[12]), "+v"(F.x[13]), "+v"(F.x[14]), "+v"(F.x[15]));
+}
+
+__device__ __forceinline__ void read_all(const uint8_t *__restrict__ S, Frags &F, int wm, int wn, int lane) {
+#pragma unroll
+  for (int f = 0; f < 16; ++f) F.x[f] = ds_read16(frag_addr(S, f, wm, wn, lane));
+}
+
+// The 16 MFMAs of one K-step on `cur`, each followed by one LDS read of the
+// next step's fragments into `nxt` (nullptr S: no next step), pinned in that
+// order so the LDS reads run under the matrix work.
+__device__ __forceinline__ void mfma_step(const Frags &cur, Frags &nxt, const uint8_t *__restrict__ S,
+                                          f32x16 (&acc)[4][4], int wm, int wn, int lane) {
+  static_for<4>([&](auto I) {
+    const i32x8 fa = frag_a(cur, I);
+    static_for<4>([&](auto J) {
+      const i32x8 fb = frag_a(cur, 4 + J);
+      acc[I][J] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa, fb, acc[I][J], 0, 0, 0, 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (S) nxt.x[4 * I + J] = ds_read16(frag_addr(S, 4 * I + J, wm, wn, lane));
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  });
+}
+
+__global__ __launch_bounds__(256) void k_fp8_gemm_pipe(const uint8_t *__restrict__ a,
+                                                      const float *__restrict__ xs, int64_t m,
+                                                      const uint8_t *__restrict__ b,
+                                                      const float *__restrict__ ws, int64_t n,
+                                                      int64_t k, void *__restrict__ y, int ytype) {
+  __shared__ __attribute__((aligned(1024))) uint8_t S0[P_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t S1[P_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t S2[P_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t S3[P_STAGE];
+  uint8_t *const SB[4] = {S0, S1, S2, S3};
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.y * 256, n0 = (int64_t)blockIdx.x * 256;
+  const int64_t nk = k / 64;
+
+  // Load assignment: wave w fills rows 64w .. 64w+63 of the A and B halves of
+  // a stage, 16 rows (4 lanes x 16 bytes per row) per instruction.  Rows past
+  // m or n re-read the last valid row; their results are never stored.
+  const uint8_t *ga[4], *gb[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 64 * wave + 16 * j + (lane >> 2);
+    const int gc = (lane & 3) ^ swz(r);
+    const int64_t gm = m0 + r < m ? m0 + r : m - 1;
+    const int64_t gn = n0 + r < n ? n0 + r : n - 1;
+    ga[j] = a + gm * k + 16 * gc;
+    gb[j] = b + gn * k + 16 * gc;
+  }
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = (f32x16){0};
+
+  // Stages 0..3 in flight; fragments of step 0 in registers.
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    if (s < nk) pipe_issue(SB[s], ga, gb, 64 * s, wave);
+  if (nk > 3) wait_vm<24>();
+  else if (nk > 2) wait_vm<16>();
+  else if (nk > 1) wait_vm<8>();
+  else wait_vm<0>();
+  __builtin_amdgcn_s_barrier();
+  Frags F0, F1;
+  read_all(S0, F0, wm, wn, lane);
+  wait_lds(F0);
+
+  // Step t: stage t's fragments are in registers.  Make stage t+1 resident
+  // (its loads landed in every wave: wait, then a bare barrier -- a release
+  // fence would drain the younger stages too), refill buffer t%4 with stage
+  // t+4 (everyone finished reading it before this barrier), then run step t's
+  // MFMAs with the reads of step t+1 interleaved.
+  auto step = [&](const Frags &cur, Frags &nxt, int64_t t, int buf) {
+    const uint8_t *next = nullptr;
+    if (t + 1 < nk) {
+      if (t + 3 < nk) wait_vm<16>();
+      else if (t + 2 < nk) wait_vm<8>();
+      else wait_vm<0>();
+      __builtin_amdgcn_s_barrier();
+      if (t + 4 < nk) pipe_issue(SB[buf], ga, gb, 64 * (t + 4), wave);
+      next = SB[(buf + 1) & 3];
     }
+    mfma_step(cur, nxt, next, acc, wm, wn, lane);
+    if (next) wait_lds(nxt);
+  };
+  for (int64_t t = 0; t < nk; t += 4) {
+    step(F0, F1, t, 0);
+    if (t + 1 < nk) step(F1, F0, t + 1, 1);
+    if (t + 2 < nk) step(F0, F1, t + 2, 2);
+    if (t + 3 < nk) step(F1, F0, t + 3, 3);
+  }
+
+  static_for<4>([&](auto I) {
+    static_for<4>([&](auto J) {
+      const int64_t col = n0 + 128 * wn + J * 32 + (lane & 31);
+      const float sw = (col < n && ws) ? ws[col] : 1.0f;
+      static_for<16>([&](auto R) {
+        const int64_t row = m0 + 128 * wm + I * 32 + 8 * (R / 4) + 4 * (lane >> 5) + (R % 4);
+        if (row < m && col < n) {
+          const float sx = xs ? xs[row] : 1.0f;
+          store_out(y, ytype, row * n + col, acc[I][J][decltype(R)::value] * (sx * sw));
+        }
+      });
+    });
+  });
+}
+
+template <int BM, int BN, int WM, int WN, int BK>
+void launch_tiled(const uint8_t *xq, const float *xs, int64_t m, const uint8_t *w, const float *ws,
+                  int64_t n, int64_t k, void *y, int ytype, hipStream_t s) {
+  const dim3 grid((unsigned)((n + BN - 1) / BN), (unsigned)((m + BM - 1) / BM));
+  hipLaunchKernelGGL((k_fp8_gemm_mfma<BM, BN, WM, WN, BK>), grid, dim3(256), 0, s, xq, xs, m, w, ws, n, k, y,
+                     ytype);
 }
 
 }  // namespace
@@ -239,9 +444,21 @@ int launch_fp8_gemm(const uint8_t *xq, const float *xs, int64_t m, const uint8_t
   if (m == 0 || n == 0) return RQ_OK;
   const bool aligned = (reinterpret_cast<uintptr_t>(xq) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(w) % 16 == 0);
-  if (k % BK == 0 && aligned) {
-    const dim3 grid((unsigned)((n + BN - 1) / BN), (unsigned)((m + BM - 1) / BM));
-    hipLaunchKernelGGL(k_fp8_gemm_mfma, grid, dim3(256), 0, s, xq, xs, m, w, ws, n, k, y, ytype);
+  if (k % 128 == 0 && aligned) {
+    // 256 x 256 tiles (128 x 128 per wave) when there are enough of them to
+    // cover the CUs, else 128 x 128.
+    // RQ_FP8_TILE=128|256 overrides the choice (tuning and profiling).
+    static const int forced = [] {
+      const char *e = getenv("RQ_FP8_TILE");
+      return e ? atoi(e) : 0;
+    }();
+    const int64_t big = ((m + 255) / 256) * ((n + 255) / 256);
+    if (forced == 256 || (forced != 128 && big >= 200)) {
+      const dim3 grid((unsigned)((n + 255) / 256), (unsigned)((m + 255) / 256));
+      hipLaunchKernelGGL(k_fp8_gemm_pipe, grid, dim3(256), 0, s, xq, xs, m, w, ws, n, k, y, ytype);
+    } else {
+      launch_tiled<128, 128, 2, 2, 128>(xq, xs, m, w, ws, n, k, y, ytype, s);
+    }
   } else {
     const int64_t total = m * n;
     hipLaunchKernelGGL(k_fp8_gemm_scalar, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, xq,

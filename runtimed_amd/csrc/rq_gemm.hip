@@ -137,18 +137,15 @@ __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restric
   }
 
   // 32x32 accumulator layout: column lane % 32, row 8*(r/4) + 4*(lane/32) + r%4.
-#pragma unroll
-  for (int i = 0; i < MI; ++i)
-#pragma unroll
-    for (int j = 0; j < NI; ++j) {
-      const int64_t col = n0 + wn * (BN / WN) + j * 32 + (lane & 31);
-      if (col >= n) continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < m) store_out(y, ytype, row * n + col, acc[i][j][r]);
-      }
-    }
+  static_for<MI>([&](auto I) {
+    static_for<NI>([&](auto J) {
+      const int64_t col = n0 + wn * (BN / WN) + J * 32 + (lane & 31);
+      static_for<16>([&](auto R) {
+        const int64_t row = m0 + wm * (BM / WM) + I * 32 + 8 * (R / 4) + 4 * (lane >> 5) + (R % 4);
+        if (row < m && col < n) store_out(y, ytype, row * n + col, acc[I][J][decltype(R)::value]);
+      });
+    });
+  });
 }
 
 template <class F, int BM, int BN, int WM, int WN>

@@ -17,6 +17,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <utility>
+
 #include "../../include/rq.h"
 
 struct rq_weight {
@@ -31,6 +33,18 @@ struct rq_weight {
 };
 
 namespace rq {
+
+// f(std::integral_constant<int, 0>) ... f(std::integral_constant<int, N-1>):
+// indices stay compile-time constants, so register arrays indexed by them
+// (MFMA accumulators) are never demoted to scratch memory.
+template <int... I, class F>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, I...>, F &&f) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(std::make_integer_sequence<int, N>{}, f);
+}
 
 // Block geometry of GgmlDtype::block (dtype.rs:49-64) for the formats with a
 // decoder here.

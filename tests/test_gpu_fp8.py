@@ -108,3 +108,15 @@ def test_fp8_gemm_full_size_sampled(dev):
     # information only: error against the reference's unquantized-x semantics
     ref_sem = oracle.fp8_gemm_fallback(xb[rows].float().cpu().numpy(), wq.cpu().numpy(), ws.cpu().numpy())
     print(f"per-token fp8 vs unquantized-x reference: {norm_err(y[rows].float().cpu().numpy(), ref_sem):.4f}")
+
+
+@pytest.mark.parametrize("m,n,k", [(1300, 10000, 640), (513, 25700, 256), (2048, 14336, 192)])
+def test_fp8_gemm_pipelined_ragged(dev, m, n, k):
+    # >= 200 tiles of 256 x 256: the 4-stage direct-to-LDS kernel, with ragged
+    # M/N edges and K-step counts that are not a multiple of the stage count
+    xb, wq, ws = _fp8_problem(m, n, k, 300 + m)
+    y = rq.fp8_gemm(xb, wq, ws, out_dtype=torch.float32)
+    rows = np.array([0, 1, m // 2, m - 2, m - 1])
+    xq, xs = oracle.fp8_quantize_rows(xb[rows].float().cpu().numpy())
+    r = oracle.fp8_gemm_quantized_f64(xq, xs, wq.cpu().numpy(), ws.cpu().numpy())
+    assert norm_err(y[rows].cpu().numpy(), r) <= 1e-4
