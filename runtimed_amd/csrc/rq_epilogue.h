@@ -1,0 +1,150 @@
+// rq_epilogue.h -- stores of 32 x 32 MFMA accumulator tiles (gfx950).
+//
+// A v_mfma_f32_32x32x* accumulator (16 f32 per lane) holds column lane % 32
+// and rows 8*(r/4) + 4*(lane/32) + r%4 in element r.  Stored as is, every
+// element is its own 2- or 4-byte write and 64 lanes touch two rows per
+// instruction; at 1 workgroup per CU the write phase then costs several
+// times the MFMA phase of a GEMM tile.  Instead each group of four
+// consecutive rows is transposed across the four lanes of a quad (DPP
+// quad_perm, no LDS), after which lane 4q+t holds row 4*(lane/32)+t of the
+// group at columns 4q..4q+3: one 16-byte (f32) or 8-byte (bf16 / f16) store.
+#pragma once
+
+#include "rq_internal.h"
+
+namespace rq {
+
+typedef float rq_f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 rq_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 rq_f16x2 __attribute__((ext_vector_type(2)));
+typedef float rq_f32x2 __attribute__((ext_vector_type(2)));
+
+// Two f32 -> packed bf16 (low half = lo), round to nearest even
+// (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((rq_f32x2){lo, hi}, rq_bf16x2));
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((rq_f32x2){lo, hi}, rq_f16x2));
+}
+
+// One f32 as the output type; same rounding as the four-wide store below.
+__device__ __forceinline__ void store_one(void *y, int ytype, int64_t idx, float v) {
+  if (ytype == RQ_F32) {
+    static_cast<float *>(y)[idx] = v;
+  } else if (ytype == RQ_BF16) {
+    static_cast<uint16_t *>(y)[idx] = (uint16_t)pack_bf16x2(v, 0.0f);
+  } else {
+    static_cast<uint16_t *>(y)[idx] = (uint16_t)pack_f16x2(v, 0.0f);
+  }
+}
+
+// Four consecutive outputs y[idx .. idx+3]; idx % 4 == 0 and y 16-aligned.
+__device__ __forceinline__ void store_four(void *y, int ytype, int64_t idx, float a, float b, float c,
+                                           float d) {
+  if (ytype == RQ_F32) {
+    *reinterpret_cast<float4 *>(static_cast<float *>(y) + idx) = make_float4(a, b, c, d);
+  } else if (ytype == RQ_BF16) {
+    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(y) + idx) =
+        make_uint2(pack_bf16x2(a, b), pack_bf16x2(c, d));
+  } else {
+    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(y) + idx) =
+        make_uint2(pack_f16x2(a, b), pack_f16x2(c, d));
+  }
+}
+
+template <int CTRL>
+__device__ __forceinline__ float quad_perm(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// 4 x 4 transpose inside each quad of lanes: afterwards lane 4q+t holds in
+// v_j what lane 4q+j held in v_t.  Two exchange stages (lane ^ 1, lane ^ 2).
+__device__ __forceinline__ void quad_transpose(float &v0, float &v1, float &v2, float &v3, int lane) {
+  constexpr int XOR1 = 0xB1;  // quad_perm [1, 0, 3, 2]
+  constexpr int XOR2 = 0x4E;  // quad_perm [2, 3, 0, 1]
+  const bool odd = lane & 1, upper = lane & 2;
+  const float p0 = quad_perm<XOR1>(v0), p1 = quad_perm<XOR1>(v1);
+  const float p2 = quad_perm<XOR1>(v2), p3 = quad_perm<XOR1>(v3);
+  const float a0 = odd ? p1 : v0, a1 = odd ? v1 : p0;
+  const float a2 = odd ? p3 : v2, a3 = odd ? v3 : p2;
+  const float q0 = quad_perm<XOR2>(a0), q1 = quad_perm<XOR2>(a1);
+  const float q2 = quad_perm<XOR2>(a2), q3 = quad_perm<XOR2>(a3);
+  v0 = upper ? q2 : a0;
+  v1 = upper ? q3 : a1;
+  v2 = upper ? a2 : q0;
+  v3 = upper ? a3 : q1;
+}
+
+// Scales of a lane's share of the 32 x 32 tile at (row0, col0) after the
+// quad transpose: sx[g] for its row in row group g, sw[j] for its columns
+// col0 + (lane & 28) + j.  A null array, or a row or column outside y,
+// gives 1.  Loaded once before any store: on gfx9 stores count in vmcnt, so
+// a load issued between stores would make its wait drain the stores too.
+__device__ __forceinline__ void tile_row_scales(const float *xs, int64_t m, int64_t row0, int lane,
+                                                float (&sx)[4]) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int64_t row = row0 + 8 * g + 4 * (lane >> 5) + (lane & 3);
+    sx[g] = (xs && row < m) ? xs[row] : 1.0f;
+  }
+}
+
+__device__ __forceinline__ void tile_col_scales(const float *ws, int64_t n, int64_t col0, int lane,
+                                                float (&sw)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t col = col0 + (lane & 28) + j;
+    sw[j] = (ws && col < n) ? ws[col] : 1.0f;
+  }
+}
+
+// Writes the 32 x 32 tile at (row0, col0) of y[m, n] (row stride n) as
+// acc * (xs[row] * ws[col]) when SCALED (a null xs or ws counts as 1), else
+// as acc.  sx, sw: the lane's scales from tile_row_scales / tile_col_scales
+// (read only when SCALED).  vec: y is 16-byte aligned and n % 4 == 0.  Tiles
+// not wholly inside y, or not vec, take the per-element path.
+template <bool SCALED>
+__device__ __forceinline__ void store_tile32(const rq_f32x16 &acc, void *y, int ytype, int64_t m,
+                                             int64_t n, int64_t row0, int64_t col0, const float (&sx)[4],
+                                             const float (&sw)[4], const float *xs, const float *ws,
+                                             int lane, bool vec) {
+  const int h = lane >> 5;
+  if (vec && row0 + 32 <= m && col0 + 32 <= n) {
+    const int t = lane & 3;
+    const int64_t col = col0 + (lane & 28);
+    static_for<4>([&](auto G) {
+      constexpr int g = decltype(G)::value;
+      float v0 = acc[4 * g], v1 = acc[4 * g + 1], v2 = acc[4 * g + 2], v3 = acc[4 * g + 3];
+      quad_transpose(v0, v1, v2, v3, lane);
+      const int64_t row = row0 + 8 * g + 4 * h + t;
+      if (SCALED) {
+        v0 *= sx[g] * sw[0];
+        v1 *= sx[g] * sw[1];
+        v2 *= sx[g] * sw[2];
+        v3 *= sx[g] * sw[3];
+      }
+      store_four(y, ytype, row * n + col, v0, v1, v2, v3);
+    });
+  } else {
+    const int64_t col = col0 + (lane & 31);
+    const float swe = (SCALED && ws && col < n) ? ws[col] : 1.0f;
+    static_for<16>([&](auto R) {
+      constexpr int r = decltype(R)::value;
+      const int64_t row = row0 + 8 * (r / 4) + 4 * h + (r % 4);
+      if (row < m && col < n) {
+        float v = acc[r];
+        if (SCALED) v *= (xs ? xs[row] : 1.0f) * swe;
+        store_one(y, ytype, row * n + col, v);
+      }
+    });
+  }
+}
+
+// vec flag of store_tile32 for an output buffer.
+__device__ __forceinline__ bool vec_stores_ok(const void *y, int64_t n) {
+  return ((reinterpret_cast<uintptr_t>(y) & 15) == 0) && ((n & 3) == 0);
+}
+
+}  // namespace rq

@@ -22,6 +22,7 @@
 // Roofline: MFMA-bound (fp8 dense peak 5.0 PFLOP/s); flops = 2*m*n*k.
 #include <stdlib.h>
 
+#include "rq_epilogue.h"
 #include "rq_internal.h"
 
 namespace rq {
@@ -221,19 +222,16 @@ __global__ __launch_bounds__(256) void k_fp8_gemm_mfma(const uint8_t *__restrict
     __syncthreads();
   }
 
-  // Epilogue: C layout of the 32x32 tile: column lane%32, row
-  // 8*(r/4) + 4*(lane/32) + r%4 for register r.
+  const bool vec = vec_stores_ok(y, n);
+  float sx[MI][4], sw[NI][4];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) tile_row_scales(xs, m, m0 + wm * (BM / WM) + i * 32, lane, sx[i]);
+#pragma unroll
+  for (int j = 0; j < NI; ++j) tile_col_scales(ws, n, n0 + wn * (BN / WN) + j * 32, lane, sw[j]);
   static_for<MI>([&](auto I) {
     static_for<NI>([&](auto J) {
-      const int64_t col = n0 + wn * (BN / WN) + J * 32 + (lane & 31);
-      const float sw = (col < n && ws) ? ws[col] : 1.0f;
-      static_for<16>([&](auto R) {
-        const int64_t row = m0 + wm * (BM / WM) + I * 32 + 8 * (R / 4) + 4 * (lane >> 5) + (R % 4);
-        if (row < m && col < n) {
-          const float sx = xs ? xs[row] : 1.0f;
-          store_out(y, ytype, row * n + col, acc[I][J][decltype(R)::value] * (sx * sw));
-        }
-      });
+      store_tile32<true>(acc[I][J], y, ytype, m, n, m0 + wm * (BM / WM) + I * 32,
+                         n0 + wn * (BN / WN) + J * 32, sx[I], sw[J], xs, ws, lane, vec);
     });
   });
 }
@@ -407,17 +405,16 @@ __global__ __launch_bounds__(256) void k_fp8_gemm_pipe(const uint8_t *__restrict
     if (t + 3 < nk) step(F1, F0, t + 3, 3);
   }
 
+  const bool vec = vec_stores_ok(y, n);
+  float sx[4][4], sw[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) tile_row_scales(xs, m, m0 + 128 * wm + i * 32, lane, sx[i]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) tile_col_scales(ws, n, n0 + 128 * wn + j * 32, lane, sw[j]);
   static_for<4>([&](auto I) {
     static_for<4>([&](auto J) {
-      const int64_t col = n0 + 128 * wn + J * 32 + (lane & 31);
-      const float sw = (col < n && ws) ? ws[col] : 1.0f;
-      static_for<16>([&](auto R) {
-        const int64_t row = m0 + 128 * wm + I * 32 + 8 * (R / 4) + 4 * (lane >> 5) + (R % 4);
-        if (row < m && col < n) {
-          const float sx = xs ? xs[row] : 1.0f;
-          store_out(y, ytype, row * n + col, acc[I][J][decltype(R)::value] * (sx * sw));
-        }
-      });
+      store_tile32<true>(acc[I][J], y, ytype, m, n, m0 + 128 * wm + I * 32, n0 + 128 * wn + J * 32,
+                         sx[I], sw[J], xs, ws, lane, vec);
     });
   });
 }

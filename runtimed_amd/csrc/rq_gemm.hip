@@ -20,6 +20,7 @@
 //
 // Roofline: MFMA-bound for M >= ~300 (bf16 dense peak 2.5 PFLOP/s,
 // flops = 2*m*n*k); HBM-bound below (weight bytes dominate).
+#include "rq_epilogue.h"
 #include "rq_formats.h"
 
 namespace rq {
@@ -136,14 +137,12 @@ __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restric
     __syncthreads();
   }
 
-  // 32x32 accumulator layout: column lane % 32, row 8*(r/4) + 4*(lane/32) + r%4.
+  const bool vec = vec_stores_ok(y, n);
+  const float one[4] = {1.0f, 1.0f, 1.0f, 1.0f};
   static_for<MI>([&](auto I) {
     static_for<NI>([&](auto J) {
-      const int64_t col = n0 + wn * (BN / WN) + J * 32 + (lane & 31);
-      static_for<16>([&](auto R) {
-        const int64_t row = m0 + wm * (BM / WM) + I * 32 + 8 * (R / 4) + 4 * (lane >> 5) + (R % 4);
-        if (row < m && col < n) store_out(y, ytype, row * n + col, acc[I][J][decltype(R)::value]);
-      });
+      store_tile32<false>(acc[I][J], y, ytype, m, n, m0 + wm * (BM / WM) + I * 32,
+                          n0 + wn * (BN / WN) + J * 32, one, one, nullptr, nullptr, lane, vec);
     });
   });
 }
