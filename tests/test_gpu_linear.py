@@ -139,3 +139,22 @@ def test_mfma_gemm_edge_tiles(dev, qtype, m, n, k):
     for ydt in (torch.float32, torch.bfloat16):
         y = w.forward(xb.to(dev), out_dtype=ydt).float().cpu().numpy()
         assert norm_err(y, ref(xb.float().numpy(), wf)) <= TOL_BF16
+
+
+# Shapes with >= 256 tiles of 256 x 256 run the 256 x 256 tile kernel:
+# exact tiles, ragged rows and columns, rows that straddle super-blocks
+# (k % 256 != 0), odd and single K-step counts.
+@pytest.mark.parametrize("qtype,m,n,k", [
+    (rq.Q4_K, 512, 32768, 256),
+    (rq.Q6_K, 300, 32868, 320),
+    (rq.Q8_0, 257, 33000, 128),
+    (rq.Q4_K, 512, 32768, 64),
+    (rq.Q6_K, 512, 32768, 448),
+])
+def test_large_gemm(dev, qtype, m, n, k):
+    w, wf = make(qtype, n, k, 5 + m + k)
+    xb = torch.from_numpy(synth.activations(3 + m, m, k)).to(torch.bfloat16)
+    r = oracle.linear_f32(xb.float().numpy(), wf, threads=8)
+    for ydt in (torch.bfloat16, torch.float32):
+        y = w.forward(xb.to(dev), out_dtype=ydt).float().cpu().numpy()
+        assert norm_err(y, r) <= TOL_BF16, (ydt, norm_err(y, r))
