@@ -5,7 +5,8 @@
 // kernels (rq_gemm.hip) share these decoders.  `decode` yields the exact f32
 // weights of runtimed-gguf's dequant (dequant.rs:40-47, dequant_k.rs:19-44,
 // dequant_k.rs:87-111); `dot` is the M=1 form that keeps activations in
-// registers.  Pieces with PE = 32 and RUNS = 2 all cover the same k
+// registers; `decode_bf16` feeds the bf16 MFMA GEMM (one fused multiply-add
+// per weight, then the bf16 rounding).  Pieces with PE = 32 and RUNS = 2 all cover the same k
 // positions, two runs of 16 at 64*(p/2) + 16*(p%2) and that + 32, so a GEMM
 // K-step of 64 is two pieces per row whatever the format.
 #pragma once
@@ -19,6 +20,14 @@ __device__ __forceinline__ float h2f(uint32_t bits) {
 }
 
 __device__ __forceinline__ float ub(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xFFu); }
+
+typedef __bf16 fmt_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float fmt_f32x2 __attribute__((ext_vector_type(2)));
+
+// Two f32 -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((fmt_f32x2){lo, hi}, fmt_bf16x2));
+}
 
 // Load `len` (multiple of 4) activations starting at x[idx] into f32 registers.
 template <int LEN>
@@ -97,6 +106,23 @@ struct FmtQ4K {
     const float sl = (dl[0] + dl[1]) + (dl[2] + dl[3]);
     const float shh = ((dh[0] + dh[1]) + (dh[2] + dh[3])) * 0.0625f;  // high nibbles were x16
     return (a0 * sl - b0 * sx[0]) + (a1 * shh - b1 * sx[1]);
+  }
+  // Weights of the piece as bf16 pairs in run order (o[8r + j]: elements
+  // 2j, 2j + 1 of run r) for the MFMA GEMM: one fused multiply-add per
+  // weight (a single rounding, then the bf16 rounding), not the exact
+  // two-rounding value of decode().
+  __device__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
+    float a0, b0, a1, b1;
+    scales(pc, a0, b0, a1, b1);
+    const uint32_t q[4] = {pc.qv.x, pc.qv.y, pc.qv.z, pc.qv.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = q[j] & 0x0F0F0F0Fu, hi = (q[j] >> 4) & 0x0F0F0F0Fu;
+      o[2 * j] = pk_bf16(fmaf(ub(lo, 0), a0, -b0), fmaf(ub(lo, 1), a0, -b0));
+      o[2 * j + 1] = pk_bf16(fmaf(ub(lo, 2), a0, -b0), fmaf(ub(lo, 3), a0, -b0));
+      o[8 + 2 * j] = pk_bf16(fmaf(ub(hi, 0), a1, -b1), fmaf(ub(hi, 1), a1, -b1));
+      o[8 + 2 * j + 1] = pk_bf16(fmaf(ub(hi, 2), a1, -b1), fmaf(ub(hi, 3), a1, -b1));
+    }
   }
   // Exact dequantized weights of the piece, in run order.
   __device__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
@@ -227,6 +253,18 @@ struct FmtQ8 {
     }
     return acc;
   }
+  __device__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const float d = h2f(pc.d[r]);
+      const uint32_t q[4] = {pc.q[r].x, pc.q[r].y, pc.q[r].z, pc.q[r].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        o[8 * r + 2 * j] = pk_bf16(d * (float)(int8_t)(q[j] & 0xFFu), d * (float)(int8_t)((q[j] >> 8) & 0xFFu));
+        o[8 * r + 2 * j + 1] = pk_bf16(d * (float)(int8_t)((q[j] >> 16) & 0xFFu), d * (float)(int8_t)(q[j] >> 24));
+      }
+    }
+  }
   __device__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
@@ -270,6 +308,23 @@ struct FmtQ6KG {
     pc.sc = *reinterpret_cast<const uint32_t *>(rec + 192 + 8 * hf + 4 * pc.ch) >> (8 * hh);
     pc.d = reinterpret_cast<const uint16_t *>(aux)[blk];
     return pc;
+  }
+  __device__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
+    const float d = h2f(pc.d);
+    const float ds0 = d * (float)(int8_t)(pc.sc & 0xFFu);
+    const float ds1 = d * (float)(int8_t)((pc.sc >> 16) & 0xFFu);
+    const float z0 = -32.0f * ds0, z1 = -32.0f * ds1;
+    const int nsh = 4 * pc.ch;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t a = (&pc.a.x)[j], b = (&pc.b.x)[j], h = (&pc.h.x)[j] >> nsh;
+      const uint32_t q0 = ((a >> nsh) & 0x0F0F0F0Fu) | ((h & 0x03030303u) << 4);
+      const uint32_t q1 = ((b >> nsh) & 0x0F0F0F0Fu) | ((h & 0x0C0C0C0Cu) << 2);
+      o[2 * j] = pk_bf16(fmaf(ub(q0, 0), ds0, z0), fmaf(ub(q0, 1), ds0, z0));
+      o[2 * j + 1] = pk_bf16(fmaf(ub(q0, 2), ds0, z0), fmaf(ub(q0, 3), ds0, z0));
+      o[8 + 2 * j] = pk_bf16(fmaf(ub(q1, 0), ds1, z1), fmaf(ub(q1, 1), ds1, z1));
+      o[8 + 2 * j + 1] = pk_bf16(fmaf(ub(q1, 2), ds1, z1), fmaf(ub(q1, 3), ds1, z1));
+    }
   }
   __device__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
     const float d = h2f(pc.d);

@@ -33,22 +33,19 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int BK = 64, LDS_K = BK + 8;
 
-// Two f32 -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32 on gfx950).
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  const bf16x2 v = __builtin_convertvector((float2v){lo, hi}, bf16x2);
-  return __builtin_bit_cast(uint32_t, v);
-}
-
 // A BM x BN tile of y per workgroup of WM x WN waves; each wave owns a
 // (BM / WM) x (BN / WN) sub-tile made of MI x NI MFMA tiles of 32 x 32.  Each
 // thread decodes exactly one 32-element weight piece per K-step
 // (BN * 2 == 64 * WM * WN).
+// Split K: workgroup z covers K-steps [z * steps, (z + 1) * steps) and, when
+// part is not null, writes its f32 partial tile to part + z * m * n instead
+// of y (k_splitk_sum adds the partials).
 template <class F, int BM, int BN, int WM, int WN>
 __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restrict__ w,
                                                        const uint8_t *__restrict__ aux,
                                                        const uint16_t *__restrict__ x, int64_t m,
                                                        int64_t n, int64_t k, void *__restrict__ y,
-                                                       int ytype) {
+                                                       int ytype, int64_t steps, float *__restrict__ part) {
   constexpr int NT = 64 * WM * WN;
   static_assert(BN * 2 == NT, "one weight piece per thread");
   constexpr int MI = BM / WM / 32, NI = BN / WN / 32;
@@ -83,24 +80,19 @@ __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restric
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i)
       *reinterpret_cast<uint4 *>(&As[buf][(arow + A_ROWS * i) * LDS_K + acol]) = ra[i];
-    float wv[2][16];
+    uint32_t ob[16];
     if (bvalid) {
-      F::decode(pb, wv);
+      F::decode_bf16(pb, ob);
     } else {
 #pragma unroll
-      for (int r = 0; r < 2; ++r)
-#pragma unroll
-        for (int t = 0; t < 16; ++t) wv[r][t] = 0.0f;
+      for (int t = 0; t < 16; ++t) ob[t] = 0u;
     }
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       uint4 *dst = reinterpret_cast<uint4 *>(&Bs[buf][brow * LDS_K + 16 * bh + 32 * r]);
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const float *v = &wv[r][8 * q];
-        dst[q] = make_uint4(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]),
-                            pack_bf16(v[6], v[7]));
-      }
+      for (int q = 0; q < 2; ++q)
+        dst[q] = make_uint4(ob[8 * r + 4 * q], ob[8 * r + 4 * q + 1], ob[8 * r + 4 * q + 2], ob[8 * r + 4 * q + 3]);
     }
   };
 
@@ -110,13 +102,14 @@ __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restric
 #pragma unroll
     for (int j = 0; j < NI; ++j) acc[i][j] = (f32x16){0};
 
-  const int64_t nk = k / BK;
-  gload(0);
+  const int64_t kt0 = (int64_t)blockIdx.z * steps;
+  const int64_t nk = (k / BK - kt0 < steps ? k / BK - kt0 : steps);
+  gload(kt0);
   sstore(0);
   __syncthreads();
   for (int64_t kt = 0; kt < nk; ++kt) {
     const int buf = (int)(kt & 1);
-    if (kt + 1 < nk) gload(kt + 1);
+    if (kt + 1 < nk) gload(kt0 + kt + 1);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       const int kc = ks * 16 + 8 * (lane >> 5);
@@ -137,22 +130,61 @@ __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restric
     __syncthreads();
   }
 
-  const bool vec = vec_stores_ok(y, n);
+  void *out = part ? static_cast<void *>(part + (int64_t)blockIdx.z * m * n) : y;
+  const int otype = part ? (int)RQ_F32 : ytype;
+  const bool vec = vec_stores_ok(out, n);
   const float one[4] = {1.0f, 1.0f, 1.0f, 1.0f};
   static_for<MI>([&](auto I) {
     static_for<NI>([&](auto J) {
-      store_tile32<false>(acc[I][J], y, ytype, m, n, m0 + wm * (BM / WM) + I * 32,
+      store_tile32<false>(acc[I][J], out, otype, m, n, m0 + wm * (BM / WM) + I * 32,
                           n0 + wn * (BN / WN) + J * 32, one, one, nullptr, nullptr, lane, vec);
     });
   });
 }
 
+// y = sum over s < splits of part[s] (f32 partials of m * n outputs).
+__global__ __launch_bounds__(256) void k_splitk_sum(const float *__restrict__ part, int splits, int64_t mn,
+                                                    void *__restrict__ y, int ytype) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < mn; i += (int64_t)gridDim.x * 256) {
+    float v = part[i];
+    for (int s = 1; s < splits; ++s) v += part[s * mn + i];
+    store_one(y, ytype, i, v);
+  }
+}
+
+// Workgroups per tile along K: enough to give the 256 CUs a workgroup each,
+// but only for long K (at least 32 K-steps of 64 per split): the f32
+// partials and their sum cost about as much as a 2048-deep tile; at most 8.
+int splits_for(int64_t tiles, int64_t nk) {
+  int sp = 1;
+  while (sp < 8 && tiles * sp < 256 && nk >= 32 * (2 * sp)) sp *= 2;
+  return sp;
+}
+
 template <class F, int BM, int BN, int WM, int WN>
 int launch(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {
-  const dim3 grid((unsigned)((wt->n + BN - 1) / BN), (unsigned)((m + BM - 1) / BM));
+  const int64_t nk = wt->k / BK;
+  const int64_t gx = (wt->n + BN - 1) / BN, gy = (m + BM - 1) / BM;
+  const int sp = splits_for(gx * gy, nk);
+  const int64_t steps = (nk + sp - 1) / sp;
+  const int used = (int)((nk + steps - 1) / steps);  // splits that own at least one step
+  float *part = nullptr;
+  if (used > 1) {
+    if (hipMallocAsync(reinterpret_cast<void **>(&part), (size_t)used * m * wt->n * sizeof(float), s) !=
+        hipSuccess)
+      return set_error(RQ_E_NOMEM, "split-K workspace of %d x %lld x %lld f32", used, (long long)m,
+                       (long long)wt->n);
+  }
+  const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)used);
   hipLaunchKernelGGL((k_qgemm<F, BM, BN, WM, WN>), grid, dim3(64 * WM * WN), 0, s, wt->data,
                      wt->data + wt->aux_off, static_cast<const uint16_t *>(x), m, wt->n, wt->k, y,
-                     ytype);
+                     ytype, steps, part);
+  if (part) {
+    const int64_t mn = m * wt->n;
+    const int64_t blocks = (mn + 255) / 256 < 4096 ? (mn + 255) / 256 : 4096;
+    hipLaunchKernelGGL(k_splitk_sum, dim3((unsigned)blocks), dim3(256), 0, s, part, used, mn, y, ytype);
+    (void)hipFreeAsync(part, s);
+  }
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemm launch failed");
 }
 

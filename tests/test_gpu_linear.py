@@ -131,8 +131,11 @@ def test_golden_gemv_on_device(dev):
 
 
 @pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0])
-@pytest.mark.parametrize("m,n,k", [(257, 130, 512), (33, 1000, 256), (65, 64, 1024), (300, 256, 2048)])
+@pytest.mark.parametrize("m,n,k", [(257, 130, 512), (33, 1000, 256), (65, 64, 1024), (300, 256, 2048),
+                                   (300, 256, 8192), (129, 200, 8384)])
 def test_mfma_gemm_edge_tiles(dev, qtype, m, n, k):
+    # K >= 4096 with few tiles splits K across workgroups (f32 partials, then
+    # a sum); 8384 = 131 K-steps leaves a shorter last split.
     # bf16 activations with m > 1 run on the matrix cores; tiles are 32..256 x 128
     w, wf = make(qtype, n, k, 81 + m + n)
     xb = torch.from_numpy(synth.activations(9 + m, m, k)).to(torch.bfloat16)
