@@ -267,10 +267,12 @@ int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m
                         int ytype, hipStream_t s) {
   // The fused kernels read activations with 8- or 16-byte vector loads.
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
-  // Small m stays on the VALU kernel (weights decoded once per row, every
-  // activation row reused from registers); larger m goes to the matrix cores.
-  if (m > 16 && xtype == RQ_BF16) {
-    const int rc = launch_linear_mfma(wt, x, m, y, ytype, s);
+  // bf16 activations with m > 1 run on the matrix cores: up to 64 rows with
+  // the weights as the A operand decoded straight into registers, beyond
+  // that the LDS-tiled GEMM.  f32 / f16 activations stay on the VALU.
+  if (m > 1 && xtype == RQ_BF16) {
+    int rc = m <= 64 ? launch_linear_smallm(wt, x, m, y, ytype, s) : RQ_E_UNSUPPORTED;
+    if (rc == RQ_E_UNSUPPORTED) rc = launch_linear_mfma(wt, x, m, y, ytype, s);
     if (rc != RQ_E_UNSUPPORTED) return rc;
   }
   switch (wt->qtype) {

@@ -69,6 +69,10 @@ int launch_linear_fused(const rq_weight *w, const void *x, int xtype, int64_t m,
 // format has no tiled kernel).
 int launch_linear_mfma(const rq_weight *w, const void *x, int64_t m, void *y, int ytype,
                        hipStream_t s);
+// Matrix-core kernel for bf16 activations and 2 <= m <= 64 (speculative
+// verify), RQ_E_UNSUPPORTED outside that or for formats it has no decoder for.
+int launch_linear_smallm(const rq_weight *w, const void *x, int64_t m, void *y, int ytype,
+                         hipStream_t s);
 // y = x * W^T with W dense f32 [n, k] in device memory.
 int launch_linear_dense_f32(const float *w, int64_t n, int64_t k, const void *x, int xtype,
                             int64_t m, void *y, int ytype, hipStream_t s);

@@ -1,0 +1,255 @@
+// rq_smallm.hip -- quantized linear y = x W^T for 2 <= M <= 64 bf16
+// activation rows (speculative verify; config-4 shapes) on the matrix cores.
+//
+// The weight rows are the MFMA A operand (v_mfma_f32_16x16x32_bf16: lane l
+// holds row l % 16 and 8 k-values chosen by l / 16) and the activation rows
+// the B operand, so a weight is decoded once, straight into A registers (no
+// LDS), and used by all M rows.  The cost per weight is then the decode
+// (about 3 VALU instructions) whatever M is, against decode + M FMAs on the
+// VALU, and the kernel stays near the weight-streaming bound up to M = 64.
+//
+// K order inside an MFMA is free as long as A and B agree.  Per 64-wide
+// chunk of a weight row, lane group g = l / 16 takes chunk elements
+// [8g, 8g + 8) and [32 + 8g, 32 + 8g + 8) -- the two 4-bit halves of 8 qs
+// bytes of Q4_K, or the matching Q6_K / Q8_0 bytes -- and MFMA h in {0, 1}
+// takes the quarter [8g + 4h, + 4) of each.  The activations are loaded for
+// the same positions.
+//
+// Workgroup: 4 waves on 16 weight rows; wave w takes chunks w, w + 4, ...;
+// the four partial 16 x (16 MT) tiles are summed through LDS.
+#include <hip/hip_runtime.h>
+
+#include "rq_epilogue.h"
+#include "rq_formats.h"
+#include "rq_internal.h"
+
+namespace rq {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// The 16 weights of lane group g in chunk t of `row` as bf16 pairs:
+// o[0..3] = chunk elements 8g .. 8g+7, o[4..7] = 32 + 8g .. 32 + 8g + 7.
+
+// Q4_K (dequant_k.rs:19-44): elements j and 32 + j of chunk c are the low
+// and high nibbles of qs[32c + j].
+struct SmQ4K {
+  struct Chunk {
+    uint4 hd;
+    uint2 q;
+    int c;
+  };
+  __device__ static Chunk load(const uint8_t *w, const uint8_t *, int64_t row, int64_t k, int64_t t, int g) {
+    const uint64_t e = (uint64_t)row * (uint64_t)k + 64u * (uint64_t)t;
+    const uint8_t *bp = w + (e >> 8) * 144u;
+    Chunk ch;
+    ch.c = (int)((e >> 6) & 3u);
+    ch.hd = *reinterpret_cast<const uint4 *>(bp);
+    ch.q = *reinterpret_cast<const uint2 *>(bp + 16 + 32 * ch.c + 8 * g);
+    return ch;
+  }
+  __device__ static void decode(const Chunk &ch, uint32_t (&o)[8]) {
+    FmtQ4K::Piece pc;
+    pc.hd = ch.hd;
+    pc.c = ch.c;
+    float a0, b0, a1, b1;
+    FmtQ4K::scales(pc, a0, b0, a1, b1);
+    const uint32_t q[2] = {ch.q.x, ch.q.y};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t lo = q[j] & 0x0F0F0F0Fu, hi = (q[j] >> 4) & 0x0F0F0F0Fu;
+      o[2 * j] = pk_bf16(fmaf(ub(lo, 0), a0, -b0), fmaf(ub(lo, 1), a0, -b0));
+      o[2 * j + 1] = pk_bf16(fmaf(ub(lo, 2), a0, -b0), fmaf(ub(lo, 3), a0, -b0));
+      o[4 + 2 * j] = pk_bf16(fmaf(ub(hi, 0), a1, -b1), fmaf(ub(hi, 1), a1, -b1));
+      o[4 + 2 * j + 1] = pk_bf16(fmaf(ub(hi, 2), a1, -b1), fmaf(ub(hi, 3), a1, -b1));
+    }
+  }
+};
+
+// Q6_K (dequant_k.rs:87-111) on the split layout (208-byte records, f16 d
+// array).  Chunk ch of half hf: element l < 32 is y[l + 64ch] of the half,
+// code nibble ch of ql[l] | bits 4ch.. of qh[l]; element 32 + l is
+// y[l + 64ch + 32], nibble ch of ql[l + 32] | bits 4ch + 2.. of qh[l];
+// scales sc[l / 16 + 4ch] and sc[l / 16 + 4ch + 2].
+struct SmQ6K {
+  struct Chunk {
+    uint2 a, b, h;
+    uint32_t sc, d;
+    int ch;
+  };
+  __device__ static Chunk load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int64_t t,
+                               int g) {
+    const uint64_t e = (uint64_t)row * (uint64_t)k + 64u * (uint64_t)t;
+    const uint64_t blk = e >> 8;
+    const int hf = (int)((e >> 7) & 1u);
+    const uint8_t *rec = w + blk * 208u;
+    Chunk c;
+    c.ch = (int)((e >> 6) & 1u);
+    c.a = *reinterpret_cast<const uint2 *>(rec + 64 * hf + 8 * g);
+    c.b = *reinterpret_cast<const uint2 *>(rec + 64 * hf + 32 + 8 * g);
+    c.h = *reinterpret_cast<const uint2 *>(rec + 128 + 32 * hf + 8 * g);
+    c.sc = *reinterpret_cast<const uint32_t *>(rec + 192 + 8 * hf + 4 * c.ch);
+    c.d = reinterpret_cast<const uint16_t *>(aux)[blk];
+    return c;
+  }
+  __device__ static void decode(const Chunk &c, uint32_t (&o)[8], int g) {
+    const float d = h2f(c.d);
+    // l / 16 = g / 2 for both runs of this lane group
+    const int sb = g >> 1;
+    const float s0 = d * (float)(int8_t)((c.sc >> (8 * sb)) & 0xFFu);
+    const float s1 = d * (float)(int8_t)((c.sc >> (8 * (sb + 2))) & 0xFFu);
+    const float z0 = -32.0f * s0, z1 = -32.0f * s1;
+    const int sh = 4 * c.ch;
+    const uint32_t a[2] = {c.a.x, c.a.y}, b[2] = {c.b.x, c.b.y}, hh[2] = {c.h.x, c.h.y};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t h = hh[j] >> sh;
+      const uint32_t q0 = ((a[j] >> sh) & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
+      const uint32_t q1 = ((b[j] >> sh) & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
+      o[2 * j] = pk_bf16(fmaf(ub(q0, 0), s0, z0), fmaf(ub(q0, 1), s0, z0));
+      o[2 * j + 1] = pk_bf16(fmaf(ub(q0, 2), s0, z0), fmaf(ub(q0, 3), s0, z0));
+      o[4 + 2 * j] = pk_bf16(fmaf(ub(q1, 0), s1, z1), fmaf(ub(q1, 1), s1, z1));
+      o[4 + 2 * j + 1] = pk_bf16(fmaf(ub(q1, 2), s1, z1), fmaf(ub(q1, 3), s1, z1));
+    }
+  }
+};
+
+// Q8_0 (dequant.rs:40-47) on the split layout (int8 quants in element
+// order, f16 d per 32): the chunk's two blocks are its two runs.
+struct SmQ8 {
+  struct Chunk {
+    uint2 a, b;
+    uint32_t d;
+  };
+  __device__ static Chunk load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int64_t t, int g) {
+    const uint64_t e = (uint64_t)row * (uint64_t)k + 64u * (uint64_t)t;
+    Chunk c;
+    c.a = *reinterpret_cast<const uint2 *>(w + e + 8 * g);
+    c.b = *reinterpret_cast<const uint2 *>(w + e + 32 + 8 * g);
+    c.d = *reinterpret_cast<const uint32_t *>(aux + 2 * (e >> 5));
+    return c;
+  }
+  __device__ static void decode(const Chunk &c, uint32_t (&o)[8]) {
+    const float d0 = h2f(c.d), d1 = h2f(c.d >> 16);
+    const uint32_t a[2] = {c.a.x, c.a.y}, b[2] = {c.b.x, c.b.y};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      o[2 * j] = pk_bf16(d0 * (float)(int8_t)(a[j] & 0xFFu), d0 * (float)(int8_t)((a[j] >> 8) & 0xFFu));
+      o[2 * j + 1] = pk_bf16(d0 * (float)(int8_t)((a[j] >> 16) & 0xFFu), d0 * (float)(int8_t)(a[j] >> 24));
+      o[4 + 2 * j] = pk_bf16(d1 * (float)(int8_t)(b[j] & 0xFFu), d1 * (float)(int8_t)((b[j] >> 8) & 0xFFu));
+      o[4 + 2 * j + 1] = pk_bf16(d1 * (float)(int8_t)((b[j] >> 16) & 0xFFu), d1 * (float)(int8_t)(b[j] >> 24));
+    }
+  }
+};
+
+template <class C>
+__device__ __forceinline__ void decode_chunk(const typename C::Chunk &c, uint32_t (&o)[8], int g) {
+  if constexpr (__is_same(C, SmQ6K)) {
+    C::decode(c, o, g);
+  } else {
+    C::decode(c, o);
+  }
+}
+
+__device__ __forceinline__ bf16x8 pick(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1) {
+  return __builtin_bit_cast(bf16x8, (uint4){a0, a1, b0, b1});
+}
+
+// MT column tiles of 16 activation rows (M <= 16 MT).
+template <class C, int MT>
+__global__ __launch_bounds__(256) void k_smallm(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
+                                                const uint16_t *__restrict__ x, int64_t m,
+                                                void *__restrict__ y, int ytype, int64_t n, int64_t k) {
+  __shared__ f32x4 part[4][MT][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
+  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const int64_t row = n0 + (lane & 15) < n ? n0 + (lane & 15) : n - 1;
+  const int64_t nk = k / 64;
+
+  // Activation rows of this lane in each column tile (rows past m read row
+  // m - 1; their results are not stored).
+  const uint16_t *xr[MT];
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) {
+    const int64_t mr = 16 * ct + (lane & 15);
+    xr[ct] = x + (mr < m ? mr : m - 1) * k + 8 * g;
+  }
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) acc[ct] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+  typename C::Chunk cur = C::load(w, aux, row, k, wave < nk ? wave : 0, g);
+  for (int64_t t = wave; t < nk; t += 4) {
+    const typename C::Chunk c = cur;
+    if (t + 4 < nk) cur = C::load(w, aux, row, k, t + 4, g);
+    uint4 xa[MT], xb[MT];
+#pragma unroll
+    for (int ct = 0; ct < MT; ++ct) {
+      xa[ct] = *reinterpret_cast<const uint4 *>(xr[ct] + 64 * t);
+      xb[ct] = *reinterpret_cast<const uint4 *>(xr[ct] + 64 * t + 32);
+    }
+    uint32_t o[8];
+    decode_chunk<C>(c, o, g);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const bf16x8 fa = pick(o[2 * h], o[2 * h + 1], o[4 + 2 * h], o[4 + 2 * h + 1]);
+#pragma unroll
+      for (int ct = 0; ct < MT; ++ct) {
+        const uint32_t *pa = &xa[ct].x, *pb = &xb[ct].x;
+        const bf16x8 fb = pick(pa[2 * h], pa[2 * h + 1], pb[2 * h], pb[2 * h + 1]);
+        acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, fb, acc[ct], 0, 0, 0);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) part[wave][ct][lane] = acc[ct];
+  __syncthreads();
+  // 16 x 16 C layout: lane l holds column (activation row) l % 16 and weight
+  // rows 4 (l / 16) + i.  Thread t sums one lane slot of one column tile.
+  for (int slot = threadIdx.x; slot < MT * 64; slot += 256) {
+    const int ct = slot >> 6, l = slot & 63;
+    f32x4 v = part[0][ct][l];
+#pragma unroll
+    for (int q = 1; q < 4; ++q) v += part[q][ct][l];
+    const int64_t mr = 16 * ct + (l & 15);
+    if (mr < m) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t nr = n0 + 4 * (l >> 4) + i;
+        if (nr < n) store_one(y, ytype, mr * n + nr, v[i]);
+      }
+    }
+  }
+}
+
+template <class C>
+int run(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {
+  const dim3 grid((unsigned)((wt->n + 15) / 16));
+  const uint16_t *xb = static_cast<const uint16_t *>(x);
+  const uint8_t *aux = wt->data + wt->aux_off;
+  if (m <= 16)
+    hipLaunchKernelGGL((k_smallm<C, 1>), grid, dim3(256), 0, s, wt->data, aux, xb, m, y, ytype, wt->n, wt->k);
+  else if (m <= 32)
+    hipLaunchKernelGGL((k_smallm<C, 2>), grid, dim3(256), 0, s, wt->data, aux, xb, m, y, ytype, wt->n, wt->k);
+  else
+    hipLaunchKernelGGL((k_smallm<C, 4>), grid, dim3(256), 0, s, wt->data, aux, xb, m, y, ytype, wt->n, wt->k);
+  return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "small-M launch failed");
+}
+
+}  // namespace
+
+// bf16 activations, 2 <= m <= 64, k % 64 == 0, 16-byte aligned x.
+int launch_linear_smallm(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {
+  if (m < 2 || m > 64 || wt->k % 64 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
+  switch (wt->qtype) {
+    case RQ_Q4_K: return run<SmQ4K>(wt, x, m, y, ytype, s);
+    case RQ_Q6_K: return run<SmQ6K>(wt, x, m, y, ytype, s);
+    case RQ_Q8_0: return run<SmQ8>(wt, x, m, y, ytype, s);
+    default: return RQ_E_UNSUPPORTED;
+  }
+}
+
+}  // namespace rq

@@ -57,6 +57,21 @@ def test_verify_small_m_bf16(dev, qtype, m):
     assert norm_err(y, ref(xb.float().numpy(), wf)) <= TOL_BF16
 
 
+# The small-M matrix-core kernel (2 <= m <= 64): partial column tiles
+# (m = 3, 17, 33, 63), weight rows not a multiple of 16, fewer K-chunks than
+# waves (k = 64, 128), rows straddling super-blocks (k = 896), and bf16 / f16
+# outputs.
+@pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0])
+@pytest.mark.parametrize("m,n,k", [(3, 37, 256), (17, 130, 128), (33, 100, 896), (63, 200, 64), (5, 4864, 896)])
+def test_small_m_edges(dev, qtype, m, n, k):
+    w, wf = make(qtype, n, k, 31 + m + n)
+    xb = torch.from_numpy(synth.activations(6 + m, m, k)).to(torch.bfloat16)
+    r = ref(xb.float().numpy(), wf)
+    for ydt in (torch.float32, torch.bfloat16, torch.float16):
+        y = w.forward(xb.to(dev), out_dtype=ydt).float().cpu().numpy()
+        assert norm_err(y, r) <= TOL_BF16, (ydt, norm_err(y, r))
+
+
 @pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K])
 def test_prefill_bf16_out(dev, qtype):
     m, n, k = 128, 1024, 2048
