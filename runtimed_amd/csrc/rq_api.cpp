@@ -75,6 +75,23 @@ static void split_layout(int qtype, const uint8_t *src, uint64_t nblocks, std::v
       memcpy(&dst[b * 32], blk + 2, 32);
       memcpy(&dst[aux_off + b * 2], blk, 2);
     }
+  } else if (qtype == RQ_Q4_0) {
+    aux_off = align256(nblocks * 16);
+    dst.assign(aux_off + nblocks * 2, 0);
+    for (uint64_t b = 0; b < nblocks; ++b) {
+      const uint8_t *blk = src + b * 18;
+      memcpy(&dst[b * 16], blk + 2, 16);
+      memcpy(&dst[aux_off + b * 2], blk, 2);
+    }
+  } else if (qtype == RQ_Q5_0) {
+    aux_off = align256(nblocks * 16);
+    dst.assign(aux_off + nblocks * 8, 0);
+    for (uint64_t b = 0; b < nblocks; ++b) {
+      const uint8_t *blk = src + b * 22;
+      memcpy(&dst[b * 16], blk + 6, 16);
+      memcpy(&dst[aux_off + b * 8], blk + 2, 4);  // qh
+      memcpy(&dst[aux_off + b * 8 + 4], blk, 2);  // d
+    }
   } else {  // Q6_K
     aux_off = align256(nblocks * 208);
     dst.assign(aux_off + nblocks * 2, 0);
@@ -113,7 +130,7 @@ int rq_weight_create(int qtype, const void *host_blocks, size_t nbytes, int64_t 
   const uint8_t *src = static_cast<const uint8_t *>(host_blocks);
   std::vector<uint8_t> staged;
   uint64_t aux_off = 0, bytes = nblocks * (uint64_t)g.bytes;
-  if (qtype == RQ_Q8_0 || qtype == RQ_Q6_K) {
+  if (qtype == RQ_Q8_0 || qtype == RQ_Q6_K || qtype == RQ_Q4_0 || qtype == RQ_Q5_0) {
     split_layout(qtype, src, nblocks, staged, aux_off);
     src = staged.data();
     bytes = staged.size();

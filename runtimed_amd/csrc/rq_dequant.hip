@@ -171,6 +171,38 @@ __global__ __launch_bounds__(kThreads) void k_dequant_q6k(const uint8_t *__restr
   }
 }
 
+// Q4_0 / Q5_0 split layouts: one thread per 4 outputs; element i of a block
+// is nibble i / 16 of quant byte i % 16 (plus qh bit i for Q5_0), value
+// d * (q - 8) or d * (q - 16) (dequant.rs:50-77).
+template <bool Q5>
+__global__ __launch_bounds__(kThreads) void k_dequant_qx0(const uint8_t *__restrict__ qs,
+                                                         const uint8_t *__restrict__ aux,
+                                                         uint64_t quads, float4 *__restrict__ out) {
+  const uint64_t stride = (uint64_t)gridDim.x * kThreads;
+  for (uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x; t < quads; t += stride) {
+    const uint64_t blk = t >> 3;
+    const int i0 = (int)(t & 7) * 4;
+    const uint32_t v = *reinterpret_cast<const uint32_t *>(qs + 16 * blk + (i0 & 15));
+    uint32_t q = (v >> (4 * (i0 >> 4))) & 0x0F0F0F0Fu;
+    uint32_t dbits;
+    if (Q5) {
+      const uint2 rec = reinterpret_cast<const uint2 *>(aux)[blk];
+      const uint32_t hb = (rec.x >> i0) & 0xFu;
+      q |= (((hb & 1u) | ((hb & 2u) << 7) | ((hb & 4u) << 14) | ((hb & 8u) << 21)) << 4);
+      dbits = rec.y & 0xFFFFu;
+    } else {
+      dbits = reinterpret_cast<const uint16_t *>(aux)[blk];
+    }
+    const float d = f16_bits_to_f32(dbits), z = Q5 ? 16.0f : 8.0f;
+    float4 o;
+    o.x = d * ((float)(q & 0xFFu) - z);
+    o.y = d * ((float)((q >> 8) & 0xFFu) - z);
+    o.z = d * ((float)((q >> 16) & 0xFFu) - z);
+    o.w = d * ((float)(q >> 24) - z);
+    out[t] = o;
+  }
+}
+
 unsigned grid_for(uint64_t items) {
   const uint64_t want = (items + kThreads - 1) / kThreads;
   return (unsigned)(want < 65536 ? (want ? want : 1) : 65536);
@@ -208,6 +240,14 @@ int launch_dequant_weight(const rq_weight *w, float *out, hipStream_t s) {
       hipLaunchKernelGGL(k_dequant_q6k, dim3(grid_for(quads)), dim3(kThreads), 0, s, w->data,
                          reinterpret_cast<const uint16_t *>(w->data + w->aux_off), quads,
                          reinterpret_cast<float4 *>(out));
+      break;
+    case RQ_Q4_0:
+      hipLaunchKernelGGL(k_dequant_qx0<false>, dim3(grid_for(quads)), dim3(kThreads), 0, s, w->data,
+                         w->data + w->aux_off, quads, reinterpret_cast<float4 *>(out));
+      break;
+    case RQ_Q5_0:
+      hipLaunchKernelGGL(k_dequant_qx0<true>, dim3(grid_for(quads)), dim3(kThreads), 0, s, w->data,
+                         w->data + w->aux_off, quads, reinterpret_cast<float4 *>(out));
       break;
     default:
       return launch_dequant_raw(w->qtype, w->data, w->nblocks, out, s);

@@ -278,6 +278,182 @@ struct FmtQ8 {
   }
 };
 
+// Q5_K (dequant_k.rs:51-80) on the aligned GGUF stream (176-byte blocks:
+// d, dmin, 12 scale bytes, qh[32], qs[128]).  Same pieces as Q4_K; element
+// l of chunk c adds 16 when bit 2c (low nibbles) or 2c + 1 (high nibbles) of
+// qh[l] is set.
+struct FmtQ5K {
+  static constexpr int PE = 32;
+  static constexpr int RUNS = 2;
+  __device__ static int64_t run_off(int p, int r) { return 64 * (p >> 1) + 16 * (p & 1) + 32 * r; }
+
+  struct Piece {
+    uint4 hd, qv, hv;
+    int c;
+  };
+  __device__ static Piece load(const uint8_t *w, const uint8_t *, int64_t row, int64_t k, int p) {
+    const uint64_t e = (uint64_t)row * (uint64_t)k + 64u * (uint64_t)(p >> 1);
+    const uint8_t *bp = w + (e >> 8) * 176u;
+    Piece pc;
+    pc.c = (int)((e >> 6) & 3u);
+    pc.hd = *reinterpret_cast<const uint4 *>(bp);
+    pc.qv = *reinterpret_cast<const uint4 *>(bp + 48 + 32 * pc.c + 16 * (p & 1));
+    pc.hv = *reinterpret_cast<const uint4 *>(bp + 16 + 16 * (p & 1));
+    return pc;
+  }
+  __device__ static void scales(const Piece &pc, float &a0, float &b0, float &a1, float &b1) {
+    FmtQ4K::Piece q4;
+    q4.hd = pc.hd;
+    q4.c = pc.c;
+    FmtQ4K::scales(q4, a0, b0, a1, b1);
+  }
+  // 5-bit codes of dword j: run 0 (low nibbles | bit 2c), run 1 (high | bit 2c + 1).
+  __device__ static void codes(const Piece &pc, int j, uint32_t &c0, uint32_t &c1) {
+    const uint32_t q = (&pc.qv.x)[j], h = (&pc.hv.x)[j] >> (2 * pc.c);
+    c0 = (q & 0x0F0F0F0Fu) | ((h << 4) & 0x10101010u);
+    c1 = ((q >> 4) & 0x0F0F0F0Fu) | ((h << 3) & 0x10101010u);
+  }
+  __device__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
+    float a0, b0, a1, b1;
+    scales(pc, a0, b0, a1, b1);
+    float dl[4], dh[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t c0, c1;
+      codes(pc, j, c0, c1);
+      dl[j] = xv[0][4 * j] * ub(c0, 0);
+      dh[j] = xv[1][4 * j] * ub(c1, 0);
+#pragma unroll
+      for (int b = 1; b < 4; ++b) {
+        dl[j] = fmaf(xv[0][4 * j + b], ub(c0, b), dl[j]);
+        dh[j] = fmaf(xv[1][4 * j + b], ub(c1, b), dh[j]);
+      }
+    }
+    const float sl = (dl[0] + dl[1]) + (dl[2] + dl[3]);
+    const float shh = (dh[0] + dh[1]) + (dh[2] + dh[3]);
+    return (a0 * sl - b0 * sx[0]) + (a1 * shh - b1 * sx[1]);
+  }
+  __device__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
+    float a0, b0, a1, b1;
+    scales(pc, a0, b0, a1, b1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t c0, c1;
+      codes(pc, j, c0, c1);
+      o[2 * j] = pk_bf16(fmaf(ub(c0, 0), a0, -b0), fmaf(ub(c0, 1), a0, -b0));
+      o[2 * j + 1] = pk_bf16(fmaf(ub(c0, 2), a0, -b0), fmaf(ub(c0, 3), a0, -b0));
+      o[8 + 2 * j] = pk_bf16(fmaf(ub(c1, 0), a1, -b1), fmaf(ub(c1, 1), a1, -b1));
+      o[8 + 2 * j + 1] = pk_bf16(fmaf(ub(c1, 2), a1, -b1), fmaf(ub(c1, 3), a1, -b1));
+    }
+  }
+  // Exact weights: d1 * (q + hi) - m1 (dequant_k.rs:67-73).
+  __device__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
+    float a0, b0, a1, b1;
+    scales(pc, a0, b0, a1, b1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t c0, c1;
+      codes(pc, j, c0, c1);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        wv[0][4 * j + b] = a0 * ub(c0, b) - b0;
+        wv[1][4 * j + b] = a1 * ub(c1, b) - b1;
+      }
+    }
+  }
+};
+
+// Bits 0..3 of v spread to bit 0 of bytes 0..3.
+__device__ __forceinline__ uint32_t spread4(uint32_t v) { return ((v & 0xFu) * 0x00204081u) & 0x01010101u; }
+
+// Q4_0 (dequant.rs:50-61) and Q5_0 (dequant.rs:64-77) on their split
+// layouts: 16 quant bytes per 32-element block in block order, then at aux
+// one f16 d per block (Q4_0) or one 8-byte record {qh: u32, d: f16, 0} per
+// block (Q5_0).  A piece is the Q4_K run pattern: its two runs are elements
+// 16h .. 16h + 15 (h = p & 1) of two consecutive blocks -- the low (h = 0)
+// or high (h = 1) nibbles of the block's 16 bytes, and for Q5_0 bits
+// 16h .. 16h + 15 of its qh.
+template <bool Q5>
+struct FmtQx0 {
+  static constexpr int PE = 32;
+  static constexpr int RUNS = 2;
+  __device__ static int64_t run_off(int p, int r) { return 64 * (p >> 1) + 16 * (p & 1) + 32 * r; }
+
+  struct Piece {
+    uint4 q[2];
+    uint32_t qh[2];
+    uint32_t d[2];
+    int h;
+  };
+  __device__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
+    Piece pc;
+    pc.h = p & 1;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint64_t blk = ((uint64_t)row * (uint64_t)k + (uint64_t)run_off(p, r)) >> 5;
+      pc.q[r] = *reinterpret_cast<const uint4 *>(w + 16 * blk);
+      if (Q5) {
+        const uint2 rec = reinterpret_cast<const uint2 *>(aux)[blk];
+        pc.qh[r] = rec.x;
+        pc.d[r] = rec.y;
+      } else {
+        pc.qh[r] = 0;
+        pc.d[r] = reinterpret_cast<const uint16_t *>(aux)[blk];
+      }
+    }
+    return pc;
+  }
+  // Unsigned codes (q + 8, or q + 16 for Q5_0) of dword j of run r.
+  __device__ static uint32_t codes(const Piece &pc, int r, int j) {
+    const uint32_t q = ((&pc.q[r].x)[j] >> (4 * pc.h)) & 0x0F0F0F0Fu;
+    if (!Q5) return q;
+    return q | (spread4(pc.qh[r] >> (16 * pc.h + 4 * j)) << 4);
+  }
+  static constexpr float ZERO = Q5 ? 16.0f : 8.0f;
+  __device__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      float dd[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t c = codes(pc, r, j);
+        dd[j] = xv[r][4 * j] * ub(c, 0);
+#pragma unroll
+        for (int b = 1; b < 4; ++b) dd[j] = fmaf(xv[r][4 * j + b], ub(c, b), dd[j]);
+      }
+      const float dot = (dd[0] + dd[1]) + (dd[2] + dd[3]);
+      acc = fmaf(h2f(pc.d[r]), dot - ZERO * sx[r], acc);
+    }
+    return acc;
+  }
+  __device__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const float d = h2f(pc.d[r]), z = -ZERO * d;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t c = codes(pc, r, j);
+        o[8 * r + 2 * j] = pk_bf16(fmaf(ub(c, 0), d, z), fmaf(ub(c, 1), d, z));
+        o[8 * r + 2 * j + 1] = pk_bf16(fmaf(ub(c, 2), d, z), fmaf(ub(c, 3), d, z));
+      }
+    }
+  }
+  // Exact weights d * (q - 8) or d * (q - 16).
+  __device__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const float d = h2f(pc.d[r]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t c = codes(pc, r, j);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) wv[r][4 * j + b] = d * (ub(c, b) - ZERO);
+      }
+    }
+  }
+};
+
 // Q6_K in 32-element pieces for the GEMM: the 64 elements [64*ch, 64*ch+64)
 // of a 128-element half hf are y[l + 32*kk] for kk = 2ch, 2ch+1 (l < 32);
 // piece h takes l in [16h, 16h+16), i.e. the same run pattern as Q4_K.  Its

@@ -207,6 +207,9 @@ int launch_linear_mfma(const rq_weight *wt, const void *x, int64_t m, void *y, i
     case RQ_Q4_K: return by_m<FmtQ4K>(wt, x, m, y, ytype, s);
     case RQ_Q6_K: return by_m<FmtQ6KG>(wt, x, m, y, ytype, s);
     case RQ_Q8_0: return by_m<FmtQ8>(wt, x, m, y, ytype, s);
+    case RQ_Q5_K: return by_m<FmtQ5K>(wt, x, m, y, ytype, s);
+    case RQ_Q4_0: return by_m<FmtQx0<false>>(wt, x, m, y, ytype, s);
+    case RQ_Q5_0: return by_m<FmtQx0<true>>(wt, x, m, y, ytype, s);
     default: return RQ_E_UNSUPPORTED;
   }
 }

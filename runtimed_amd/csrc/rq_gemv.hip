@@ -286,6 +286,15 @@ int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m
     case RQ_Q8_0:
       if (wt->k % 64 != 0) return RQ_E_UNSUPPORTED;
       return dispatch_fmt<FmtQ8, 4>(wt, x, xtype, m, y, ytype, s);
+    case RQ_Q5_K:
+      if (wt->k % 64 != 0) return RQ_E_UNSUPPORTED;
+      return dispatch_fmt<FmtQ5K, 4>(wt, x, xtype, m, y, ytype, s);
+    case RQ_Q4_0:
+      if (wt->k % 64 != 0) return RQ_E_UNSUPPORTED;
+      return dispatch_fmt<FmtQx0<false>, 4>(wt, x, xtype, m, y, ytype, s);
+    case RQ_Q5_0:
+      if (wt->k % 64 != 0) return RQ_E_UNSUPPORTED;
+      return dispatch_fmt<FmtQx0<true>, 4>(wt, x, xtype, m, y, ytype, s);
     default:
       return RQ_E_UNSUPPORTED;
   }

@@ -1,11 +1,15 @@
 // rq_internal.h -- shared declarations for librq (gfx950).
 //
 // Device layouts held by a weight handle (all arrays 256-byte aligned):
-//   Q4_K, Q5_K, Q4_0, Q5_0  the GGUF block stream as uploaded.  A Q4_K block
-//                           is 144 = 9 x 16 bytes, so every block of a
-//                           16-aligned stream is 16-aligned.
+//   Q4_K, Q5_K              the GGUF block stream as uploaded.  Blocks are
+//                           144 = 9 x 16 and 176 = 11 x 16 bytes, so every
+//                           block of a 16-aligned stream is 16-aligned.
 //   Q8_0                    quants: n*k int8 in flat element order, then
 //                           scales: one f16 per 32-element block.
+//   Q4_0                    16 quant bytes per block in block order, then
+//                           one f16 d per block.
+//   Q5_0                    16 quant bytes per block, then one 8-byte record
+//                           {qh u32, d f16, 0} per block.
 //   Q6_K                    208-byte records [ql 128 | qh 64 | scales 16] per
 //                           block (13 x 16 bytes), then one f16 d per block.
 // The split layouts keep every element value and the flat element order of

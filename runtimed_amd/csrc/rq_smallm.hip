@@ -143,9 +143,93 @@ struct SmQ8 {
   }
 };
 
+// Q5_K (dequant_k.rs:51-80): as Q4_K, plus bit 2c / 2c + 1 of qh[j] -> 16.
+struct SmQ5K {
+  struct Chunk {
+    uint4 hd;
+    uint2 q, h;
+    int c;
+  };
+  __device__ static Chunk load(const uint8_t *w, const uint8_t *, int64_t row, int64_t k, int64_t t, int g) {
+    const uint64_t e = (uint64_t)row * (uint64_t)k + 64u * (uint64_t)t;
+    const uint8_t *bp = w + (e >> 8) * 176u;
+    Chunk ch;
+    ch.c = (int)((e >> 6) & 3u);
+    ch.hd = *reinterpret_cast<const uint4 *>(bp);
+    ch.q = *reinterpret_cast<const uint2 *>(bp + 48 + 32 * ch.c + 8 * g);
+    ch.h = *reinterpret_cast<const uint2 *>(bp + 16 + 8 * g);
+    return ch;
+  }
+  __device__ static void decode(const Chunk &ch, uint32_t (&o)[8]) {
+    FmtQ4K::Piece pc;
+    pc.hd = ch.hd;
+    pc.c = ch.c;
+    float a0, b0, a1, b1;
+    FmtQ4K::scales(pc, a0, b0, a1, b1);
+    const uint32_t q[2] = {ch.q.x, ch.q.y}, hh[2] = {ch.h.x, ch.h.y};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t h = hh[j] >> (2 * ch.c);
+      const uint32_t lo = (q[j] & 0x0F0F0F0Fu) | ((h << 4) & 0x10101010u);
+      const uint32_t hi = ((q[j] >> 4) & 0x0F0F0F0Fu) | ((h << 3) & 0x10101010u);
+      o[2 * j] = pk_bf16(fmaf(ub(lo, 0), a0, -b0), fmaf(ub(lo, 1), a0, -b0));
+      o[2 * j + 1] = pk_bf16(fmaf(ub(lo, 2), a0, -b0), fmaf(ub(lo, 3), a0, -b0));
+      o[4 + 2 * j] = pk_bf16(fmaf(ub(hi, 0), a1, -b1), fmaf(ub(hi, 1), a1, -b1));
+      o[4 + 2 * j + 1] = pk_bf16(fmaf(ub(hi, 2), a1, -b1), fmaf(ub(hi, 3), a1, -b1));
+    }
+  }
+};
+
+// Q4_0 / Q5_0 (dequant.rs:50-77) on their split layouts: the chunk's runs
+// are its two 32-element blocks; lane group g takes elements 8g .. 8g + 7 of
+// each: nibble g / 2 of quant bytes 8 (g % 2) .. + 7, and for Q5_0 bits
+// 8g .. 8g + 7 of qh.
+template <bool Q5>
+struct SmQx0 {
+  struct Chunk {
+    uint2 a, b;
+    uint32_t ha, hb, da, db;
+  };
+  __device__ static Chunk load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int64_t t, int g) {
+    const uint64_t b0 = ((uint64_t)row * (uint64_t)k + 64u * (uint64_t)t) >> 5;
+    Chunk c;
+    c.a = *reinterpret_cast<const uint2 *>(w + 16 * b0 + 8 * (g & 1));
+    c.b = *reinterpret_cast<const uint2 *>(w + 16 * (b0 + 1) + 8 * (g & 1));
+    if (Q5) {
+      const uint2 ra = reinterpret_cast<const uint2 *>(aux)[b0], rb = reinterpret_cast<const uint2 *>(aux)[b0 + 1];
+      c.ha = (ra.x >> (8 * g)) & 0xFFu;
+      c.hb = (rb.x >> (8 * g)) & 0xFFu;
+      c.da = ra.y;
+      c.db = rb.y;
+    } else {
+      c.ha = c.hb = 0;
+      c.da = reinterpret_cast<const uint16_t *>(aux)[b0];
+      c.db = reinterpret_cast<const uint16_t *>(aux)[b0 + 1];
+    }
+    return c;
+  }
+  __device__ static void decode(const Chunk &c, uint32_t (&o)[8], int g) {
+    const float z = Q5 ? 16.0f : 8.0f;
+    const int sh = 4 * (g >> 1);
+    const uint32_t qa[2] = {c.a.x, c.a.y}, qb[2] = {c.b.x, c.b.y};
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const float d = h2f(r ? c.db : c.da), nz = -z * d;
+      const uint32_t hbits = r ? c.hb : c.ha;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        uint32_t v = ((r ? qb[j] : qa[j]) >> sh) & 0x0F0F0F0Fu;
+        if (Q5) v |= spread4(hbits >> (4 * j)) << 4;
+        o[4 * r + 2 * j] = pk_bf16(fmaf(ub(v, 0), d, nz), fmaf(ub(v, 1), d, nz));
+        o[4 * r + 2 * j + 1] = pk_bf16(fmaf(ub(v, 2), d, nz), fmaf(ub(v, 3), d, nz));
+      }
+    }
+  }
+};
+
 template <class C>
 __device__ __forceinline__ void decode_chunk(const typename C::Chunk &c, uint32_t (&o)[8], int g) {
-  if constexpr (__is_same(C, SmQ6K)) {
+  if constexpr (__is_same(C, SmQ6K) || __is_same(C, SmQx0<false>) || __is_same(C, SmQx0<true>)) {
     C::decode(c, o, g);
   } else {
     C::decode(c, o);
@@ -248,6 +332,9 @@ int launch_linear_smallm(const rq_weight *wt, const void *x, int64_t m, void *y,
     case RQ_Q4_K: return run<SmQ4K>(wt, x, m, y, ytype, s);
     case RQ_Q6_K: return run<SmQ6K>(wt, x, m, y, ytype, s);
     case RQ_Q8_0: return run<SmQ8>(wt, x, m, y, ytype, s);
+    case RQ_Q5_K: return run<SmQ5K>(wt, x, m, y, ytype, s);
+    case RQ_Q4_0: return run<SmQx0<false>>(wt, x, m, y, ytype, s);
+    case RQ_Q5_0: return run<SmQx0<true>>(wt, x, m, y, ytype, s);
     default: return RQ_E_UNSUPPORTED;
   }
 }

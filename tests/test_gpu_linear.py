@@ -176,3 +176,30 @@ def test_large_gemm(dev, qtype, m, n, k):
     for ydt in (torch.bfloat16, torch.float32):
         y = w.forward(xb.to(dev), out_dtype=ydt).float().cpu().numpy()
         assert norm_err(y, r) <= TOL_BF16, (ydt, norm_err(y, r))
+
+
+# Q5_K, Q4_0 and Q5_0 on the fused paths: M = 1 (VALU GEMV, f32 gate),
+# small M and the tiled GEMM (bf16 gate); Q4_0 / Q5_0 are uploaded in split
+# layouts (16 quant bytes per block, then d / {qh, d} records).
+NEXT_FORMATS = [rq.Q5_K, rq.Q4_0, rq.Q5_0]
+
+
+@pytest.mark.parametrize("qtype", NEXT_FORMATS)
+@pytest.mark.parametrize("n,k", [(4864, 896), (896, 4864), (130, 256), (64, 2048)])
+def test_next_formats_gemv_f32(dev, qtype, n, k):
+    w, wf = make(qtype, n, k, 41 + n)
+    x = synth.activations(43, 1, k)
+    y = w.forward(torch.from_numpy(x).to(dev)).cpu().numpy()
+    assert norm_err(y, ref(x, wf)) <= TOL_F32
+
+
+@pytest.mark.parametrize("qtype", NEXT_FORMATS)
+@pytest.mark.parametrize("m,n,k", [(2, 896, 896), (17, 130, 256), (64, 200, 1024), (300, 256, 2048),
+                                   (512, 1024, 512)])
+def test_next_formats_matrix_cores(dev, qtype, m, n, k):
+    w, wf = make(qtype, n, k, 47 + m)
+    xb = torch.from_numpy(synth.activations(49 + m, m, k)).to(torch.bfloat16)
+    r = ref(xb.float().numpy(), wf)
+    for ydt in (torch.float32, torch.bfloat16):
+        y = w.forward(xb.to(dev), out_dtype=ydt).float().cpu().numpy()
+        assert norm_err(y, r) <= TOL_BF16, (ydt, norm_err(y, r))
