@@ -18,6 +18,9 @@
  *       `QTensor::dequantize` as called by `Weights::get` (store.rs:88-94),
  *       with runtimed-gguf's bit-exact semantics
  *       (crates/runtimed-gguf/src/quant/dequant.rs:83-146).
+ *   rq_embedding
+ *       `QMatMul::embedding` as called by `Weights::embed` and
+ *       `Weights::candidate_weights` (crates/runtimed-model/src/weights/embed_layer.rs:16-84).
  *   rq_dequant_tensor
  *       `dequant_tensor` (crates/runtimed-gguf/src/quant/dequant.rs:83-146) on
  *       GGUF bytes already in device memory, same error rules.
@@ -135,6 +138,14 @@ int rq_weight_info(const rq_weight *w, rq_weight_desc *out);
 /* Decode the whole weight to f32 (n*k values, row-major [n, k]) into device
  * memory.  Bit-identical to runtimed-gguf's dequant_tensor. */
 int rq_dequant_f32(const rq_weight *w, float *dev_out, void *stream);
+
+/* Rows ids[0 .. n_ids) of the weight, decoded bit-identically to
+ * rq_dequant_f32, as f32 [n_ids, k] in device memory: the quantized branch
+ * of Weights::embed / Weights::candidate_weights (embed_layer.rs:16-84,
+ * QMatMul::embedding).  ids are in host memory and may be reused when the
+ * call returns; an id >= n gives RQ_E_ARG and nothing is written; n_ids == 0
+ * is a no-op.  Requires k % 4 == 0 (RQ_E_UNSUPPORTED otherwise). */
+int rq_embedding(const rq_weight *w, const uint32_t *ids, int64_t n_ids, float *dev_out, void *stream);
 
 /* Decode a flat GGUF block stream that already sits in device memory, with
  * dequant_tensor's rules: RQ_E_UNSUPPORTED for a type without a decoder,

@@ -185,6 +185,33 @@ int rq_dequant_f32(const rq_weight *w, float *dev_out, void *stream) {
   return launch_dequant_weight(w, dev_out, as_stream(stream));
 }
 
+int rq_embedding(const rq_weight *w, const uint32_t *ids, int64_t n_ids, float *dev_out, void *stream) {
+  g_last_error.clear();
+  if (!w) return set_error(RQ_E_ARG, "weight is null");
+  if (n_ids < 0) return set_error(RQ_E_ARG, "n_ids %lld is negative", (long long)n_ids);
+  if (n_ids == 0) return RQ_OK;
+  if (!ids || !dev_out) return set_error(RQ_E_ARG, "null argument");
+  if (w->k % 4 != 0) return set_error(RQ_E_UNSUPPORTED, "row length %lld is not a multiple of 4", (long long)w->k);
+  for (int64_t i = 0; i < n_ids; ++i)
+    if ((int64_t)ids[i] >= w->n)
+      return set_error(RQ_E_ARG, "id %u at position %lld is out of range for %lld rows", ids[i], (long long)i,
+                       (long long)w->n);
+  int rc = hip_check(hipSetDevice(w->device), "hipSetDevice");
+  if (rc) return rc;
+  const hipStream_t s = as_stream(stream);
+  uint32_t *dids = nullptr;
+  rc = hip_check(hipMallocAsync(reinterpret_cast<void **>(&dids), (size_t)n_ids * sizeof(uint32_t), s),
+                 "hipMallocAsync");
+  if (rc) return rc;
+  // From pageable memory the copy returns once the ids are staged, so the
+  // caller's buffer may be reused on return.
+  rc = hip_check(hipMemcpyAsync(dids, ids, (size_t)n_ids * sizeof(uint32_t), hipMemcpyHostToDevice, s),
+                 "hipMemcpyAsync");
+  if (!rc) rc = launch_gather_rows(w, dids, n_ids, dev_out, s);
+  (void)hipFreeAsync(dids, s);
+  return rc;
+}
+
 int rq_dequant_tensor(int qtype, const void *dev_bytes, size_t nbytes, size_t n_elements,
                       float *dev_out, void *stream) {
   g_last_error.clear();

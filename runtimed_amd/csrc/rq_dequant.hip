@@ -102,104 +102,150 @@ __global__ __launch_bounds__(kThreads) void k_dequant_raw(int qtype, int elems, 
   }
 }
 
-// Q4_K handle layout (aligned GGUF blocks): one thread per 4 outputs.
-__global__ __launch_bounds__(kThreads) void k_dequant_q4k(const uint8_t *__restrict__ src,
-                                                         uint64_t quads, float4 *__restrict__ out) {
-  const uint64_t stride = (uint64_t)gridDim.x * kThreads;
-  for (uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x; t < quads; t += stride) {
-    const uint64_t blk = t >> 6;
-    const int i0 = (int)(t & 63) * 4;
-    const uint8_t *b = src + blk * 144;
-    const uint4 hd = *reinterpret_cast<const uint4 *>(b);
-    const int chunk = i0 >> 6, r = i0 & 63, j = 2 * chunk + (r >> 5);
-    const uint32_t qw = *reinterpret_cast<const uint32_t *>(b + 16 + 32 * chunk + (r & 31));
-    uint8_t s[12];
-    *reinterpret_cast<uint32_t *>(s) = hd.y;
-    *reinterpret_cast<uint32_t *>(s + 4) = hd.z;
-    *reinterpret_cast<uint32_t *>(s + 8) = hd.w;
-    uint32_t sc, m;
-    scale_min_k4(j, s, sc, m);
-    const float d1 = f16_bits_to_f32(hd.x & 0xFFFFu) * (float)sc;
-    const float m1 = f16_bits_to_f32(hd.x >> 16) * (float)m;
-    const uint32_t q4 = (r < 32) ? (qw & 0x0F0F0F0Fu) : ((qw >> 4) & 0x0F0F0F0Fu);
-    float4 o;
-    o.x = d1 * (float)(q4 & 0xFFu) - m1;
-    o.y = d1 * (float)((q4 >> 8) & 0xFFu) - m1;
-    o.z = d1 * (float)((q4 >> 16) & 0xFFu) - m1;
-    o.w = d1 * (float)(q4 >> 24) - m1;
-    out[t] = o;
-  }
+// ---- handle layouts: four consecutive outputs (flat quad t) per call ----
+
+// Q4_K (aligned GGUF blocks).
+__device__ float4 quad_q4k(const uint8_t *__restrict__ src, uint64_t t) {
+  const uint64_t blk = t >> 6;
+  const int i0 = (int)(t & 63) * 4;
+  const uint8_t *b = src + blk * 144;
+  const uint4 hd = *reinterpret_cast<const uint4 *>(b);
+  const int chunk = i0 >> 6, r = i0 & 63, j = 2 * chunk + (r >> 5);
+  const uint32_t qw = *reinterpret_cast<const uint32_t *>(b + 16 + 32 * chunk + (r & 31));
+  uint8_t s[12];
+  *reinterpret_cast<uint32_t *>(s) = hd.y;
+  *reinterpret_cast<uint32_t *>(s + 4) = hd.z;
+  *reinterpret_cast<uint32_t *>(s + 8) = hd.w;
+  uint32_t sc, m;
+  scale_min_k4(j, s, sc, m);
+  const float d1 = f16_bits_to_f32(hd.x & 0xFFFFu) * (float)sc;
+  const float m1 = f16_bits_to_f32(hd.x >> 16) * (float)m;
+  const uint32_t q4 = (r < 32) ? (qw & 0x0F0F0F0Fu) : ((qw >> 4) & 0x0F0F0F0Fu);
+  float4 o;
+  o.x = d1 * (float)(q4 & 0xFFu) - m1;
+  o.y = d1 * (float)((q4 >> 8) & 0xFFu) - m1;
+  o.z = d1 * (float)((q4 >> 16) & 0xFFu) - m1;
+  o.w = d1 * (float)(q4 >> 24) - m1;
+  return o;
 }
 
-// Q8_0 split layout: one thread per 4 outputs.
-__global__ __launch_bounds__(kThreads) void k_dequant_q8(const uint32_t *__restrict__ qs,
-                                                        const uint16_t *__restrict__ dsc,
-                                                        uint64_t quads, float4 *__restrict__ out) {
-  const uint64_t stride = (uint64_t)gridDim.x * kThreads;
-  for (uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x; t < quads; t += stride) {
-    const uint32_t v = qs[t];
-    const float d = f16_bits_to_f32(dsc[t >> 3]);
-    float4 o;
-    o.x = d * (float)(int8_t)(v & 0xFFu);
-    o.y = d * (float)(int8_t)((v >> 8) & 0xFFu);
-    o.z = d * (float)(int8_t)((v >> 16) & 0xFFu);
-    o.w = d * (float)(int8_t)(v >> 24);
-    out[t] = o;
-  }
+// Q5_K (aligned GGUF blocks): d1 * (q + hi) - m1 (dequant_k.rs:67-73).
+__device__ float4 quad_q5k(const uint8_t *__restrict__ src, uint64_t t) {
+  const uint64_t blk = t >> 6;
+  const int i0 = (int)(t & 63) * 4;
+  const uint8_t *b = src + blk * 176;
+  const uint4 hd = *reinterpret_cast<const uint4 *>(b);
+  const int chunk = i0 >> 6, r = i0 & 63, l = r & 31, j = 2 * chunk + (r >> 5);
+  const uint32_t qw = *reinterpret_cast<const uint32_t *>(b + 48 + 32 * chunk + l);
+  const uint32_t hw = *reinterpret_cast<const uint32_t *>(b + 16 + l);
+  uint8_t s[12];
+  *reinterpret_cast<uint32_t *>(s) = hd.y;
+  *reinterpret_cast<uint32_t *>(s + 4) = hd.z;
+  *reinterpret_cast<uint32_t *>(s + 8) = hd.w;
+  uint32_t sc, m;
+  scale_min_k4(j, s, sc, m);
+  const float d1 = f16_bits_to_f32(hd.x & 0xFFFFu) * (float)sc;
+  const float m1 = f16_bits_to_f32(hd.x >> 16) * (float)m;
+  const int bit = 2 * chunk + (r >> 5);
+  const uint32_t q = ((r < 32) ? (qw & 0x0F0F0F0Fu) : ((qw >> 4) & 0x0F0F0F0Fu)) |
+                     (((hw >> bit) & 0x01010101u) << 4);
+  float4 o;
+  o.x = d1 * (float)(q & 0xFFu) - m1;
+  o.y = d1 * (float)((q >> 8) & 0xFFu) - m1;
+  o.z = d1 * (float)((q >> 16) & 0xFFu) - m1;
+  o.w = d1 * (float)(q >> 24) - m1;
+  return o;
 }
 
-// Q6_K split layout: one thread per 4 outputs.
-__global__ __launch_bounds__(kThreads) void k_dequant_q6k(const uint8_t *__restrict__ rec,
-                                                         const uint16_t *__restrict__ dsc,
-                                                         uint64_t quads, float4 *__restrict__ out) {
-  const uint64_t stride = (uint64_t)gridDim.x * kThreads;
-  for (uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x; t < quads; t += stride) {
-    const uint64_t blk = t >> 6;
-    const int i0 = (int)(t & 63) * 4;
-    const int hf = i0 >> 7, r = i0 & 127, kk = r >> 5, l = r & 31;
-    const uint8_t *b = rec + blk * 208;
-    const uint32_t ql = *reinterpret_cast<const uint32_t *>(b + 64 * hf + 32 * (kk & 1) + l);
-    const uint32_t qh = *reinterpret_cast<const uint32_t *>(b + 128 + 32 * hf + l);
-    const float ds = f16_bits_to_f32(dsc[blk]) * (float)(int8_t)b[192 + 8 * hf + (l >> 4) + 2 * kk];
-    const uint32_t q = ((ql >> (4 * (kk >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * kk)) & 0x03030303u) << 4);
-    float4 o;
-    o.x = ds * ((float)(q & 0xFFu) - 32.0f);
-    o.y = ds * ((float)((q >> 8) & 0xFFu) - 32.0f);
-    o.z = ds * ((float)((q >> 16) & 0xFFu) - 32.0f);
-    o.w = ds * ((float)(q >> 24) - 32.0f);
-    out[t] = o;
-  }
+// Q8_0 split layout.
+__device__ float4 quad_q8(const uint8_t *__restrict__ qs, const uint8_t *__restrict__ aux, uint64_t t) {
+  const uint32_t v = reinterpret_cast<const uint32_t *>(qs)[t];
+  const float d = f16_bits_to_f32(reinterpret_cast<const uint16_t *>(aux)[t >> 3]);
+  float4 o;
+  o.x = d * (float)(int8_t)(v & 0xFFu);
+  o.y = d * (float)(int8_t)((v >> 8) & 0xFFu);
+  o.z = d * (float)(int8_t)((v >> 16) & 0xFFu);
+  o.w = d * (float)(int8_t)(v >> 24);
+  return o;
 }
 
-// Q4_0 / Q5_0 split layouts: one thread per 4 outputs; element i of a block
-// is nibble i / 16 of quant byte i % 16 (plus qh bit i for Q5_0), value
-// d * (q - 8) or d * (q - 16) (dequant.rs:50-77).
+// Q6_K split layout.
+__device__ float4 quad_q6k(const uint8_t *__restrict__ rec, const uint8_t *__restrict__ aux, uint64_t t) {
+  const uint64_t blk = t >> 6;
+  const int i0 = (int)(t & 63) * 4;
+  const int hf = i0 >> 7, r = i0 & 127, kk = r >> 5, l = r & 31;
+  const uint8_t *b = rec + blk * 208;
+  const uint32_t ql = *reinterpret_cast<const uint32_t *>(b + 64 * hf + 32 * (kk & 1) + l);
+  const uint32_t qh = *reinterpret_cast<const uint32_t *>(b + 128 + 32 * hf + l);
+  const float ds = f16_bits_to_f32(reinterpret_cast<const uint16_t *>(aux)[blk]) *
+                   (float)(int8_t)b[192 + 8 * hf + (l >> 4) + 2 * kk];
+  const uint32_t q = ((ql >> (4 * (kk >> 1))) & 0x0F0F0F0Fu) | (((qh >> (2 * kk)) & 0x03030303u) << 4);
+  float4 o;
+  o.x = ds * ((float)(q & 0xFFu) - 32.0f);
+  o.y = ds * ((float)((q >> 8) & 0xFFu) - 32.0f);
+  o.z = ds * ((float)((q >> 16) & 0xFFu) - 32.0f);
+  o.w = ds * ((float)(q >> 24) - 32.0f);
+  return o;
+}
+
+// Q4_0 / Q5_0 split layouts: element i of a block is nibble i / 16 of quant
+// byte i % 16 (plus qh bit i for Q5_0), value d * (q - 8) or d * (q - 16)
+// (dequant.rs:50-77).
 template <bool Q5>
-__global__ __launch_bounds__(kThreads) void k_dequant_qx0(const uint8_t *__restrict__ qs,
-                                                         const uint8_t *__restrict__ aux,
-                                                         uint64_t quads, float4 *__restrict__ out) {
+__device__ float4 quad_qx0(const uint8_t *__restrict__ qs, const uint8_t *__restrict__ aux, uint64_t t) {
+  const uint64_t blk = t >> 3;
+  const int i0 = (int)(t & 7) * 4;
+  const uint32_t v = *reinterpret_cast<const uint32_t *>(qs + 16 * blk + (i0 & 15));
+  uint32_t q = (v >> (4 * (i0 >> 4))) & 0x0F0F0F0Fu;
+  uint32_t dbits;
+  if (Q5) {
+    const uint2 rec = reinterpret_cast<const uint2 *>(aux)[blk];
+    const uint32_t hb = (rec.x >> i0) & 0xFu;
+    q |= (((hb & 1u) | ((hb & 2u) << 7) | ((hb & 4u) << 14) | ((hb & 8u) << 21)) << 4);
+    dbits = rec.y & 0xFFFFu;
+  } else {
+    dbits = reinterpret_cast<const uint16_t *>(aux)[blk];
+  }
+  const float d = f16_bits_to_f32(dbits), z = Q5 ? 16.0f : 8.0f;
+  float4 o;
+  o.x = d * ((float)(q & 0xFFu) - z);
+  o.y = d * ((float)((q >> 8) & 0xFFu) - z);
+  o.z = d * ((float)((q >> 16) & 0xFFu) - z);
+  o.w = d * ((float)(q >> 24) - z);
+  return o;
+}
+
+template <int QT>
+__device__ __forceinline__ float4 quad_handle(const uint8_t *data, const uint8_t *aux, uint64_t t) {
+  if constexpr (QT == RQ_Q4_K) return quad_q4k(data, t);
+  else if constexpr (QT == RQ_Q5_K) return quad_q5k(data, t);
+  else if constexpr (QT == RQ_Q8_0) return quad_q8(data, aux, t);
+  else if constexpr (QT == RQ_Q6_K) return quad_q6k(data, aux, t);
+  else if constexpr (QT == RQ_Q4_0) return quad_qx0<false>(data, aux, t);
+  else return quad_qx0<true>(data, aux, t);
+}
+
+// Whole handle: one thread per 4 outputs.
+template <int QT>
+__global__ __launch_bounds__(kThreads) void k_dequant_handle(const uint8_t *__restrict__ data,
+                                                            const uint8_t *__restrict__ aux, uint64_t quads,
+                                                            float4 *__restrict__ out) {
   const uint64_t stride = (uint64_t)gridDim.x * kThreads;
-  for (uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x; t < quads; t += stride) {
-    const uint64_t blk = t >> 3;
-    const int i0 = (int)(t & 7) * 4;
-    const uint32_t v = *reinterpret_cast<const uint32_t *>(qs + 16 * blk + (i0 & 15));
-    uint32_t q = (v >> (4 * (i0 >> 4))) & 0x0F0F0F0Fu;
-    uint32_t dbits;
-    if (Q5) {
-      const uint2 rec = reinterpret_cast<const uint2 *>(aux)[blk];
-      const uint32_t hb = (rec.x >> i0) & 0xFu;
-      q |= (((hb & 1u) | ((hb & 2u) << 7) | ((hb & 4u) << 14) | ((hb & 8u) << 21)) << 4);
-      dbits = rec.y & 0xFFFFu;
-    } else {
-      dbits = reinterpret_cast<const uint16_t *>(aux)[blk];
-    }
-    const float d = f16_bits_to_f32(dbits), z = Q5 ? 16.0f : 8.0f;
-    float4 o;
-    o.x = d * ((float)(q & 0xFFu) - z);
-    o.y = d * ((float)((q >> 8) & 0xFFu) - z);
-    o.z = d * ((float)((q >> 16) & 0xFFu) - z);
-    o.w = d * ((float)(q >> 24) - z);
-    out[t] = o;
+  for (uint64_t t = (uint64_t)blockIdx.x * kThreads + threadIdx.x; t < quads; t += stride)
+    out[t] = quad_handle<QT>(data, aux, t);
+}
+
+// Rows ids[0 .. nid) of an [n, k] handle (k % 4 == 0): output quad q of row
+// i is flat quad ids[i] * k / 4 + q.
+template <int QT>
+__global__ __launch_bounds__(kThreads) void k_gather_rows(const uint8_t *__restrict__ data,
+                                                         const uint8_t *__restrict__ aux,
+                                                         const uint32_t *__restrict__ ids, int64_t nid,
+                                                         int64_t kq, float4 *__restrict__ out) {
+  const uint64_t total = (uint64_t)nid * (uint64_t)kq, stride = (uint64_t)gridDim.x * kThreads;
+  for (uint64_t o = (uint64_t)blockIdx.x * kThreads + threadIdx.x; o < total; o += stride) {
+    const uint64_t i = o / (uint64_t)kq, q = o - i * (uint64_t)kq;
+    out[o] = quad_handle<QT>(data, aux, (uint64_t)ids[i] * (uint64_t)kq + q);
   }
 }
 
@@ -222,38 +268,42 @@ int launch_dequant_raw(int qtype, const uint8_t *src, uint64_t nblocks, float *o
                                          : set_error(RQ_E_DEVICE, "dequant launch failed");
 }
 
+template <template <int> class K, class... Args>
+int by_qtype(int qtype, dim3 grid, hipStream_t s, Args... args) {
+  switch (qtype) {
+    case RQ_Q4_K: hipLaunchKernelGGL(K<RQ_Q4_K>::fn, grid, dim3(kThreads), 0, s, args...); break;
+    case RQ_Q5_K: hipLaunchKernelGGL(K<RQ_Q5_K>::fn, grid, dim3(kThreads), 0, s, args...); break;
+    case RQ_Q8_0: hipLaunchKernelGGL(K<RQ_Q8_0>::fn, grid, dim3(kThreads), 0, s, args...); break;
+    case RQ_Q6_K: hipLaunchKernelGGL(K<RQ_Q6_K>::fn, grid, dim3(kThreads), 0, s, args...); break;
+    case RQ_Q4_0: hipLaunchKernelGGL(K<RQ_Q4_0>::fn, grid, dim3(kThreads), 0, s, args...); break;
+    case RQ_Q5_0: hipLaunchKernelGGL(K<RQ_Q5_0>::fn, grid, dim3(kThreads), 0, s, args...); break;
+    default: return set_error(RQ_E_UNSUPPORTED, "no decoder for qtype %d", qtype);
+  }
+  return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "dequant launch failed");
+}
+
+template <int QT>
+struct DequantK {
+  static constexpr auto fn = k_dequant_handle<QT>;
+};
+template <int QT>
+struct GatherK {
+  static constexpr auto fn = k_gather_rows<QT>;
+};
+
 int launch_dequant_weight(const rq_weight *w, float *out, hipStream_t s) {
   const uint64_t quads = (uint64_t)w->n * (uint64_t)w->k / 4;
   if (quads == 0) return RQ_OK;
-  switch (w->qtype) {
-    case RQ_Q4_K:
-      hipLaunchKernelGGL(k_dequant_q4k, dim3(grid_for(quads)), dim3(kThreads), 0, s, w->data,
-                         quads, reinterpret_cast<float4 *>(out));
-      break;
-    case RQ_Q8_0:
-      hipLaunchKernelGGL(k_dequant_q8, dim3(grid_for(quads)), dim3(kThreads), 0, s,
-                         reinterpret_cast<const uint32_t *>(w->data),
-                         reinterpret_cast<const uint16_t *>(w->data + w->aux_off), quads,
-                         reinterpret_cast<float4 *>(out));
-      break;
-    case RQ_Q6_K:
-      hipLaunchKernelGGL(k_dequant_q6k, dim3(grid_for(quads)), dim3(kThreads), 0, s, w->data,
-                         reinterpret_cast<const uint16_t *>(w->data + w->aux_off), quads,
-                         reinterpret_cast<float4 *>(out));
-      break;
-    case RQ_Q4_0:
-      hipLaunchKernelGGL(k_dequant_qx0<false>, dim3(grid_for(quads)), dim3(kThreads), 0, s, w->data,
-                         w->data + w->aux_off, quads, reinterpret_cast<float4 *>(out));
-      break;
-    case RQ_Q5_0:
-      hipLaunchKernelGGL(k_dequant_qx0<true>, dim3(grid_for(quads)), dim3(kThreads), 0, s, w->data,
-                         w->data + w->aux_off, quads, reinterpret_cast<float4 *>(out));
-      break;
-    default:
-      return launch_dequant_raw(w->qtype, w->data, w->nblocks, out, s);
-  }
-  return hipGetLastError() == hipSuccess ? RQ_OK
-                                         : set_error(RQ_E_DEVICE, "dequant launch failed");
+  return by_qtype<DequantK>(w->qtype, dim3(grid_for(quads)), s, (const uint8_t *)w->data,
+                            (const uint8_t *)(w->data + w->aux_off), quads, reinterpret_cast<float4 *>(out));
+}
+
+int launch_gather_rows(const rq_weight *w, const uint32_t *dev_ids, int64_t n_ids, float *out, hipStream_t s) {
+  if (n_ids == 0) return RQ_OK;
+  const int64_t kq = w->k / 4;
+  return by_qtype<GatherK>(w->qtype, dim3(grid_for((uint64_t)n_ids * (uint64_t)kq)), s, (const uint8_t *)w->data,
+                           (const uint8_t *)(w->data + w->aux_off), dev_ids, n_ids, kq,
+                           reinterpret_cast<float4 *>(out));
 }
 
 }  // namespace rq

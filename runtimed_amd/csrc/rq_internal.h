@@ -63,6 +63,9 @@ hipStream_t as_stream(void *s);
 
 // ---- launchers (each returns RQ_OK or an error code and message) ----
 int launch_dequant_weight(const rq_weight *w, float *out, hipStream_t s);
+// Rows dev_ids[0 .. n_ids) of a handle (every id < n, k % 4 == 0) as f32.
+int launch_gather_rows(const rq_weight *w, const uint32_t *dev_ids, int64_t n_ids, float *out,
+                       hipStream_t s);
 int launch_dequant_raw(int qtype, const uint8_t *src, uint64_t nblocks, float *out,
                        hipStream_t s);
 // Fused matmul on a handle; returns RQ_E_UNSUPPORTED when the handle's

@@ -128,6 +128,13 @@ ModelError ModelError::shape(const std::string &name, std::vector<size_t> expect
 
 size_t Tensor::elem_count() const { return product(dims_); }
 
+Tensor Tensor::reshaped(std::vector<size_t> dims) const {
+  if (product(dims) != elem_count()) throw ModelError::shape("reshape", dims, dims_);
+  Tensor r = *this;
+  r.dims_ = std::move(dims);
+  return r;
+}
+
 Tensor Tensor::zeros(std::vector<size_t> dims, DType t, int device) {
   Tensor r;
   r.dims_ = std::move(dims);
@@ -271,6 +278,15 @@ Tensor QMatMul::dequantize(void *stream) const {
   return out;
 }
 
+Tensor QMatMul::embedding(const std::vector<uint32_t> &ids, void *stream) const {
+  Tensor out = Tensor::zeros({ids.size(), k_}, DType::F32, device_);
+  if (ids.empty()) return out;
+  const int rc = rq_embedding(w_.get(), ids.data(), (int64_t)ids.size(), static_cast<float *>(out.data()), stream);
+  if (rc == RQ_E_ARG) throw ModelError(ModelError::Shape, std::string("embedding: ") + rq_last_error());
+  rq_ok(rc, "embedding");
+  return out;
+}
+
 size_t QMatMul::storage_size_in_bytes() const {
   rq_weight_desc d;
   rq_ok(rq_weight_info(w_.get(), &d), "rq_weight_info");
@@ -406,6 +422,32 @@ Tensor Weights::get(const std::string &name) const {
   auto q = q_map_.find(name);
   if (q != q_map_.end()) return q->second->dequantize();
   throw ModelError(ModelError::MissingWeight, "missing weight: " + name);
+}
+
+Tensor Weights::candidate_weights(const std::string &name, const std::vector<uint32_t> &ids) const {
+  auto q = q_map_.find(name);
+  if (q != q_map_.end()) return q->second->embedding(ids);
+  const Tensor &w = get_raw(name);
+  if (w.dims().size() != 2) throw ModelError::shape(name, {0, 0}, w.dims());
+  if (w.dtype() != DType::F32)
+    throw ModelError(ModelError::Config, "embedding rows: only f32 dense tables are served here: " + name);
+  const size_t hidden = w.dim(1), rows = w.dim(0);
+  Tensor out = Tensor::zeros({ids.size(), hidden}, DType::F32, w.device());
+  for (size_t i = 0; i < ids.size(); ++i) {
+    if (ids[i] >= rows)
+      throw ModelError(ModelError::Shape, "embedding: id " + std::to_string(ids[i]) + " out of range for " +
+                                              std::to_string(rows) + " rows of " + name);
+    hip_ok(hipMemcpyAsync(static_cast<float *>(out.data()) + i * hidden,
+                          static_cast<const float *>(w.data()) + (size_t)ids[i] * hidden, hidden * sizeof(float),
+                          hipMemcpyDeviceToDevice, nullptr),
+           "hipMemcpyAsync");
+  }
+  return out;
+}
+
+Tensor Weights::embed(const std::string &name, const std::vector<uint32_t> &ids) const {
+  Tensor rows = candidate_weights(name, ids);
+  return rows.reshaped({1, rows.dim(0), rows.dim(1)});
 }
 
 Tensor Weights::linear(const Tensor &x, const std::string &name) const {

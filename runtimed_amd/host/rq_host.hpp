@@ -75,6 +75,8 @@ class Tensor {
   int device() const { return device_; }
   void *data() const { return ptr_.get(); }
   bool has_storage() const { return ptr_ != nullptr; }
+  // Same storage, other dims (same element count).
+  Tensor reshaped(std::vector<size_t> dims) const;
 
  private:
   std::shared_ptr<void> ptr_;
@@ -114,6 +116,8 @@ class QMatMul {
   QMatMul(int qtype, const void *blocks, size_t nbytes, size_t n, size_t k, int device);
   Tensor forward(const Tensor &x, void *stream = nullptr) const;  // y = x W^T
   Tensor dequantize(void *stream = nullptr) const;                // [n, k] f32
+  // Rows ids of the dequantized matrix, [ids.size(), k] f32 (QMatMul::embedding).
+  Tensor embedding(const std::vector<uint32_t> &ids, void *stream = nullptr) const;
   size_t storage_size_in_bytes() const;
   size_t n() const { return n_; }
   size_t k() const { return k_; }
@@ -177,6 +181,10 @@ class Weights {
   Tensor linear(const Tensor &x, const std::string &name) const;        // linear_layer.rs:45-66
   Tensor linear_dense(const Tensor &x, const std::string &name) const;  // linear_layer.rs:68-105
   Tensor get(const std::string &name) const;                            // store.rs:78-101
+  // embed_layer.rs:16-57: rows ids as f32 [1, ids.size(), hidden].
+  Tensor embed(const std::string &name, const std::vector<uint32_t> &ids) const;
+  // embed_layer.rs:59-84: the same rows as [ids.size(), hidden].
+  Tensor candidate_weights(const std::string &name, const std::vector<uint32_t> &ids) const;
   const Tensor &get_raw(const std::string &name) const;                 // store.rs:103-107
   std::shared_ptr<QMatMul> q_matmul(const std::string &name) const;
   size_t resident_bytes() const;                                         // store.rs:57-76

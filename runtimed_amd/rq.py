@@ -65,6 +65,7 @@ def lib() -> ctypes.CDLL:
         L.rq_weight_info.argtypes = [vp, ctypes.POINTER(_Desc)]
         L.rq_dequant_f32.argtypes = [vp, vp, vp]
         L.rq_dequant_tensor.argtypes = [i32, vp, sz, sz, vp, vp]
+        L.rq_embedding.argtypes = [vp, vp, i64, vp, vp]
         L.rq_linear.argtypes = [vp, vp, i32, i64, vp, i32, vp]
         L.rq_fp8_quantize.argtypes = [vp, i32, i64, i64, i32, vp, vp, vp]
         L.rq_fp8_gemm.argtypes = [vp, i32, i64, vp, vp, i64, i64, vp, i32, i32, vp]
@@ -133,6 +134,14 @@ class QWeight:
     def dequantize(self) -> torch.Tensor:
         out = torch.empty((self.n, self.k), dtype=torch.float32, device=self.device)
         check(lib().rq_dequant_f32(self._h, _ptr(out), _stream(self.device)))
+        return out
+
+    def embedding(self, ids) -> torch.Tensor:
+        """Rows `ids` decoded exactly, f32 [len(ids), k] (embed_layer.rs:16-84)."""
+        ids = np.ascontiguousarray(np.asarray(ids, dtype=np.uint32).reshape(-1))
+        out = torch.empty((ids.size, self.k), dtype=torch.float32, device=self.device)
+        check(lib().rq_embedding(self._h, ids.ctypes.data_as(ctypes.c_void_p), ids.size, _ptr(out),
+                                 _stream(self.device)))
         return out
 
     def forward(self, x: torch.Tensor, out_dtype: Optional[torch.dtype] = None,

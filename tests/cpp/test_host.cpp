@@ -239,6 +239,33 @@ static void gpu_tests() {
     auto e = expect_throw<ModelError>([&] { w.linear(bad, "quant.weight"); });
     CHECK(e.kind == ModelError::Shape);
   });
+  run("embed_dense_and_quantized", [] {  // embed_layer.rs:92-125, rows 32 wide
+    std::vector<std::vector<int>> rows;
+    std::vector<float> dense;
+    for (int r = 0; r < 4; ++r) {
+      std::vector<int> q;
+      for (int i = 0; i < 32; ++i) q.push_back(3 * r + i);
+      rows.push_back(q);
+      for (int i = 0; i < 32; ++i) dense.push_back((float)(3 * r + i));
+    }
+    auto blocks = q8_rows(rows);
+    std::unordered_map<std::string, Tensor> map;
+    map["dense_embd"] = Tensor::from_host(dense.data(), {4, 32}, DType::F32, 0);
+    auto w = Weights::from_quantized(0, map, {{"quant_embd", std::make_shared<QMatMul>(8, blocks.data(), blocks.size(), 4, 32, 0)}});
+    const std::vector<uint32_t> ids = {1, 3};
+    auto od = w.embed("dense_embd", ids), oq = w.embed("quant_embd", ids);
+    CHECK((od.dims() == std::vector<size_t>{1, 2, 32}) && (oq.dims() == std::vector<size_t>{1, 2, 32}));
+    auto dv = od.to_vec<float>(), qv = oq.to_vec<float>();
+    CHECK(dv[0] == 3.0f && dv[1] == 4.0f && dv[2] == 5.0f && dv[32] == 9.0f && dv[33] == 10.0f && dv[34] == 11.0f);
+    CHECK(std::memcmp(dv.data(), qv.data(), dv.size() * 4) == 0);
+    auto cand = w.candidate_weights("quant_embd", ids);
+    CHECK((cand.dims() == std::vector<size_t>{2, 32}));
+    CHECK((w.embed("quant_embd", {}).dims() == std::vector<size_t>{1, 0, 32}));
+    auto e = expect_throw<ModelError>([&] { w.embed("quant_embd", {4}); });
+    CHECK(e.kind == ModelError::Shape);
+    auto m = expect_throw<ModelError>([&] { w.embed("nope", ids); });
+    CHECK(m.kind == ModelError::MissingWeight);
+  });
   run("weights_from_quantized_resident_bytes", [] {  // store.rs:231-243
     auto blocks = q8_rows({{1}, {2}, {3}, {4}});
     auto qm = std::make_shared<QMatMul>(8, blocks.data(), blocks.size(), 4, 32, 0);

@@ -68,6 +68,7 @@ def test_null_and_enum_checks():
     assert L.rq_weight_create(12, None, 0, 1, 256, 0, None) == -5
     assert L.rq_weight_info(None, None) == -5
     assert L.rq_dequant_f32(None, None, None) == -5
+    assert L.rq_embedding(None, None, 1, None, None) == -5
     assert L.rq_linear(None, None, 0, 1, None, 0, None) == -5
     assert L.rq_fp8_quantize(None, 0, 1, 16, 7, None, None, None) == -5  # bad mode
     assert L.rq_fp8_gemm(None, 99, 1, None, None, 16, 16, None, 0, 1, None) == -5
