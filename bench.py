@@ -176,6 +176,23 @@ def extra_q8_gemv(torch, rq, synth, dev, steps, warmup):
             "GB/s": round(b / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def extra_large_gemv(torch, rq, synth, dev, steps, warmup):
+    """The M=1 GEMV kernel where the launch cost is small next to the bytes:
+    Q4_K 14336x4096 (33 MB, a Llama-3-8B FFN shape), 16 copies (528 MB, more
+    than the 256 MB Infinity Cache) replayed in a HIP graph."""
+    n, k = 14336, 4096
+    blocks = synth.q4_k_blocks(9, n * k // 256)
+    copies = 16
+    W = [rq.QWeight(rq.Q4_K, blocks, n, k) for _ in range(copies)]
+    x = torch.from_numpy(synth.activations(4, 1, k)).to(dev)
+    y = torch.empty((1, n), device=dev)
+    g = capture(torch, lambda: [w.forward(x, out=y) for w in W])
+    ms = Timer(torch).replay(g, steps, warmup) / copies
+    b = n * k // 256 * Q4K_BLOCK + k * 4 + n * 4
+    return {"workload": "Q4_K GEMV 14336x4096 f32, M=1 (streaming shape)", "us_per_gemv": round(ms * 1e3, 3),
+            "GB/s": round(b / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def extra_verify(torch, rq, W, dev, steps, warmup):
     out = []
     for m in (1, 2, 4, 8, 16, 64):
@@ -365,6 +382,7 @@ def main():
     extra = {}
     if not args.no_extras:
         for name, fn in (("q8_0_gemv", lambda: extra_q8_gemv(torch, rq, synth, dev, args.steps, args.warmup)),
+                         ("q4_k_gemv_large", lambda: extra_large_gemv(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("verify", lambda: extra_verify(torch, rq, W[:32], dev, args.steps, args.warmup)),
                          ("prefill", lambda: extra_prefill(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("fp8_gemm", lambda: extra_fp8(torch, rq, synth, dev, args.steps, args.warmup))):

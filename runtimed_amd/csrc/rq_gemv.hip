@@ -128,6 +128,60 @@ __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
   }
 }
 
+// M = 1, long rows (P > 64 pieces): one wave per row, PPL pieces per lane
+// (piece lane + 64 i), activations in registers; the wave walks rows with a
+// grid stride and loads the next row's pieces before it computes the
+// current one, so about PPL x 2 pieces per lane are in flight.  No barriers:
+// the row total is a DPP sum over the wave.
+template <class F, int PPL>
+__global__ __launch_bounds__(256) void k_gemv_long(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
+                                                   const void *__restrict__ x, int xtype, void *__restrict__ y,
+                                                   int ytype, int64_t n, int64_t k) {
+  const int lane = threadIdx.x & 63;
+  const int P = (int)(k / F::PE);
+  const int64_t nw = (int64_t)gridDim.x * 4;
+  int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+
+  float xv[PPL][F::RUNS][16];
+  float sx[PPL][F::RUNS];
+#pragma unroll
+  for (int i = 0; i < PPL; ++i) {
+    const int p = lane + 64 * i;
+#pragma unroll
+    for (int r = 0; r < F::RUNS; ++r) {
+      sx[i][r] = 0.0f;
+      if (p < P) {
+        load_run<16>(x, xtype, F::run_off(p, r), xv[i][r]);
+#pragma unroll
+        for (int t = 0; t < 16; ++t) sx[i][r] += xv[i][r][t];
+      } else {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) xv[i][r][t] = 0.0f;
+      }
+    }
+  }
+
+  typename F::Piece cur[PPL];
+#pragma unroll
+  for (int i = 0; i < PPL; ++i)
+    if (row < n && lane + 64 * i < P) cur[i] = F::load(w, aux, row, k, lane + 64 * i);
+  for (; row < n; row += nw) {
+    const int64_t rn = row + nw;
+    typename F::Piece nxt[PPL];
+#pragma unroll
+    for (int i = 0; i < PPL; ++i)
+      if (rn < n && lane + 64 * i < P) nxt[i] = F::load(w, aux, rn, k, lane + 64 * i);
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PPL; ++i)
+      if (lane + 64 * i < P) acc += F::dot(cur[i], xv[i], sx[i]);
+    acc = seg_sum(acc, 64);
+    if (lane == 63) store_out(y, ytype, row, acc);
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) cur[i] = nxt[i];
+  }
+}
+
 // M > 1 (interim path): each piece is decoded once to exact f32 weights and
 // then dotted with every activation row, read from memory.
 template <class F, int PPL>
@@ -222,9 +276,31 @@ int run_multi(const rq_weight *wt, const void *x, int xtype, int64_t m, void *y,
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }
 
+template <class F, int PPL>
+int run_long(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s) {
+  // 16 waves per CU walking rows: enough weight bytes in flight to cover
+  // HBM latency, few enough that every wave sees several rows.
+  const int64_t waves = wt->n < 256 * 16 ? wt->n : 256 * 16;
+  const unsigned blocks = (unsigned)((waves + 3) / 4);
+  hipLaunchKernelGGL((k_gemv_long<F, PPL>), dim3(blocks), dim3(256), 0, s, wt->data, wt->data + wt->aux_off, x,
+                     xtype, y, ytype, wt->n, wt->k);
+  return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
+}
+
 template <class F>
 int run_m1(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s) {
   const int P = (int)(wt->k / F::PE);
+  // Long rows on many rows: one wave per row walking the rows.  Fewer rows
+  // (a decode-sized matrix) keep the team layout, which starts every row at
+  // once.
+  if (P > 64 && wt->n >= 4096) {
+    switch ((P + 63) / 64) {
+      case 2: return run_long<F, 2>(wt, x, xtype, y, ytype, s);
+      case 3: return run_long<F, 3>(wt, x, xtype, y, ytype, s);
+      case 4: return run_long<F, 4>(wt, x, xtype, y, ytype, s);
+      default: break;
+    }
+  }
   int seg_log2 = 6, team = 1, rows_per_wg, threads;
   if (P <= 64) {
     seg_log2 = ceil_log2(P < 16 ? 16 : P);
