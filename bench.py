@@ -273,6 +273,74 @@ def extra_fp8(torch, rq, synth, dev, steps, warmup):
             "quantize_ms": round(ms_q, 4)}
 
 
+def extra_marlin(torch, rq, dev, steps, warmup):
+    """Marlin INT4 GEMV, M=1, f32: the Qwen2-0.5B up-projection shape and the
+    streaming shape, enough distinct copies to exceed the Infinity Cache."""
+    res = []
+    for n, k, copies in ((4864, 896, 480), (14336, 4096, 32)):
+        kc = (k + 31) // 32
+        words = torch.randint(-2**31, 2**31 - 1, (kc, n, 4), dtype=torch.int32, device=dev)
+        scales = torch.rand(n, device=dev) * 0.02 + 0.001
+        W = [(words.clone(), scales.clone()) for _ in range(copies)]
+        x = torch.randn((1, k), device=dev)
+        y = torch.empty((1, n), device=dev)
+
+        def run():
+            st = rq._stream(dev)
+            for p, sc in W:
+                rq.check(rq.lib().rq_marlin_linear(rq._ptr(p), rq._ptr(sc), n, k, rq._ptr(x), rq.F32, 1,
+                                                   rq._ptr(y), rq.F32, st))
+
+        g = capture(torch, run)
+        ms = Timer(torch).replay(g, steps, warmup) / copies
+        b = kc * n * 16 + n * 4 + k * 4 + n * 4
+        res.append({"shape": f"{n}x{k}", "us_per_gemv": round(ms * 1e3, 3), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                    "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+        del W, g
+        torch.cuda.empty_cache()
+    return {"workload": "Marlin INT4 GEMV, M=1, f32 activations", "shapes": res}
+
+
+def extra_kv(torch, rq, dev, steps, warmup):
+    """Paged-KV quantizer: one layer's K for a 4096-token prompt with 8 KV
+    heads of 128 ([1, 8, 4096, 128] bf16, 8 MB), 64 distinct inputs; bytes
+    counted once each way (input read, codes and scales written)."""
+    shape = (1, 8, 4096, 128)
+    copies = 64
+    ins = [torch.randn(shape, device=dev).to(torch.bfloat16) for _ in range(copies)]
+    q = torch.empty(shape, dtype=torch.uint8, device=dev)
+    s = torch.empty(8, device=dev)
+    out = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    st = rq._stream(dev)
+    b, h, sd = 1, 8, 4096 * 128
+    res = {}
+    for mode, name in ((rq.KV_FP8, "fp8"), (rq.KV_INT8, "int8")):
+        def quant():
+            for t in ins:
+                rq.check(rq.lib().rq_kv_quantize(rq._ptr(t), rq.BF16, b, h, sd, mode, rq._ptr(q), rq._ptr(s), st))
+
+        def deq():
+            for _ in range(copies):
+                rq.check(rq.lib().rq_kv_dequantize(rq._ptr(q), mode, rq._ptr(s), b, h, sd, rq._ptr(out), rq.BF16, st))
+
+        for label, fn, nbytes in (("quantize", quant, b * h * sd * 3 + h * 4), ("dequantize", deq, b * h * sd * 3)):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            reps = max(2, steps // 4)
+            t0.record()
+            for _ in range(reps):
+                fn()
+            t1.record()
+            torch.cuda.synchronize()
+            ms = t0.elapsed_time(t1) / (reps * copies)
+            res[f"{name}_{label}"] = {"us": round(ms * 1e3, 3), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                      "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    return {"workload": "KV block quantizer [1, 8, 4096, 128] bf16 <-> fp8 / int8 codes, per-head scales", **res}
+
+
 def mode_gate(torch, rq, synth, dev, steps, warmup, eager=False):
     """Only the dominant kernel: R distinct 4864x896 Q4_K gate weights
     (R * 2.45 MB >= 1 GB), one GEMV each, in one HIP graph (or launched
@@ -385,7 +453,9 @@ def main():
                          ("q4_k_gemv_large", lambda: extra_large_gemv(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("verify", lambda: extra_verify(torch, rq, W[:32], dev, args.steps, args.warmup)),
                          ("prefill", lambda: extra_prefill(torch, rq, synth, dev, args.steps, args.warmup)),
-                         ("fp8_gemm", lambda: extra_fp8(torch, rq, synth, dev, args.steps, args.warmup))):
+                         ("fp8_gemm", lambda: extra_fp8(torch, rq, synth, dev, args.steps, args.warmup)),
+                         ("marlin_int4_gemv", lambda: extra_marlin(torch, rq, dev, args.steps, args.warmup)),
+                         ("kv_quantizer", lambda: extra_kv(torch, rq, dev, args.steps, args.warmup))):
             log(f"extra: {name}")
             try:
                 extra[name] = fn()

@@ -32,6 +32,17 @@
  *       -> `ops::fp8_gemm` (crates/runtimed-model/src/ops/fp8_gemm.rs:77-191),
  *       used by `Fp8Weight::forward` (crates/runtimed-model/src/weights/fp8_weight.rs:95-97)
  *       and by the F8E4M3 branch of `Weights::linear_dense` (linear_layer.rs:78-87).
+ *   rq_marlin_repack, rq_marlin_dequant, rq_marlin_linear
+ *       `repack_marlin_tiles`, `MarlinWeight::dequantize` and `marlin_gemv`
+ *       (crates/runtimed-model/src/ops/marlin_gemv.rs:42-202), reached through
+ *       `SubstratePort::marlin_gemv` (substrate/port.rs:76) from the Marlin
+ *       branch of `Weights::linear` (linear_layer.rs:53-63).
+ *   rq_kv_quantize, rq_kv_dequantize
+ *       `quantize_block_kv` / `quantize_fp8` / `quantize_int8` and
+ *       `dequantize_fp8` / `dequantize_int8`
+ *       (crates/runtimed-model/src/cache/paged/quantize.rs:12-123), called by
+ *       `allocate_block_with_offset` (cache/paged/table.rs:44) and
+ *       `QuantizedCacheBlock::dequantize_{k,v}` (cache/paged/block.rs:85-140).
  *   rq_last_error
  *       the message carried by `ModelError::{Shape, Config}`
  *       (crates/runtimed-model/src/error.rs:5-27).
@@ -104,6 +115,13 @@ typedef enum rq_fp8_mode {
    * e4m3_rne(x * (448 / max|x[m,:]|)); y is multiplied back by s[m]. */
   RQ_FP8_PER_TOKEN = 1
 } rq_fp8_mode;
+
+/* KV-cache block precision (CachePrecision, cache/paged/block.rs:23-27). */
+typedef enum rq_kv_mode {
+  RQ_KV_F16 = 0,  /* attention-sink / Fp16 blocks: a cast, scales 1 */
+  RQ_KV_FP8 = 1,  /* e4m3 codes, per-head scale max|t| / 448 */
+  RQ_KV_INT8 = 2  /* int8 codes, per-head scale max|t| / 127 */
+} rq_kv_mode;
 
 typedef struct rq_weight rq_weight;
 
@@ -180,6 +198,46 @@ int rq_fp8_gemm(const void *x, int xtype, int64_t m, const uint8_t *w, const flo
 int rq_fp8_gemm_q(const uint8_t *xq, const float *xscale, int64_t m, const uint8_t *w,
                   const float *w_scale, int64_t n, int64_t k, void *y, int ytype,
                   void *stream);
+
+/* ---- Marlin INT4 weights (marlin_gemv.rs) ----
+ * packed: u32 [ceil(k/32)][n][4] in device memory; record [c][r] carries row
+ * r, inputs 32c .. 32c+31, input 32c + 8j + i in bits 4i .. 4i+3 of word j;
+ * weight = (nibble - 8) * scales[r] (scales: n f32 in device memory). */
+
+/* repack_marlin_tiles (marlin_gemv.rs:66-97) on the device: w is [n, k] of
+ * type wtype (F32, F16 or BF16); nibble = clamp(round(w / s) + 8, 0, 15)
+ * with round half away from zero, computed as w * (1 / s) (1 when
+ * |s| <= 1e-12), NaN -> 0; inputs past k in the last record are 8. */
+int rq_marlin_repack(const void *w, int wtype, const float *scales, int64_t n, int64_t k,
+                     uint32_t *packed, void *stream);
+
+/* MarlinWeight::dequantize (marlin_gemv.rs:42-61): [n, k] f32, bit-exact. */
+int rq_marlin_dequant(const uint32_t *packed, const float *scales, int64_t n, int64_t k,
+                      float *dev_out, void *stream);
+
+/* marlin_gemv (marlin_gemv.rs:119-202): y[m, n] = scales[n] * sum_k x[m, k] *
+ * (q[n, k] - 8), f32 accumulation; x is m x k (F32, F16 or BF16), y is m x n
+ * of type ytype.  m = 0 is a no-op (the reference returns an empty tensor). */
+int rq_marlin_linear(const uint32_t *packed, const float *scales, int64_t n, int64_t k,
+                     const void *x, int xtype, int64_t m, void *y, int ytype, void *stream);
+
+/* ---- paged-KV block quantizer (cache/paged/quantize.rs) ----
+ * t is a K or V chunk viewed as [b, h, sd] (sd = tokens * head_dim; a tensor
+ * that is not 4-D is [1, 1, numel, 1], quantize.rs:14-18), type ttype in
+ * {F32, F16, BF16}.  RQ_KV_FP8 / RQ_KV_INT8: scales[h] =
+ * max(max|t[:, h, :]| / (448 | 127), 1e-8) (NaN elements ignored) and
+ * q (b*h*sd bytes) = f32_to_fp8_e4m3(t / s) or (i8)clamp(round(t / s),
+ * -128, 127) (NaN -> 0).  RQ_KV_F16: q holds b*h*sd f16 (t cast, round to
+ * nearest even) and every scale is 1.  Scratch for the per-head maxima is
+ * stream-ordered. */
+int rq_kv_quantize(const void *t, int ttype, int64_t b, int64_t h, int64_t sd, int mode, void *q,
+                   float *scales, void *stream);
+
+/* dequantize_fp8 / dequantize_int8 (quantize.rs:48-57, 98-107): out =
+ * decode(q) * scales[h] (f32 product) as otype (F32, F16 or BF16); RQ_KV_F16
+ * casts the f16 values (scales unused, may be NULL). */
+int rq_kv_dequantize(const void *q, int mode, const float *scales, int64_t b, int64_t h, int64_t sd,
+                     void *out, int otype, void *stream);
 
 #ifdef __cplusplus
 }

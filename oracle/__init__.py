@@ -54,6 +54,11 @@ def lib() -> ctypes.CDLL:
         L.rqo_fp8_quantize_rows.argtypes = [vp, i64, i64, vp, vp]
         L.rqo_fp8_encode_unscaled.argtypes = [vp, i64, vp]
         L.rqo_fp8_gemm_quantized_f64.argtypes = [vp, vp, i64, vp, vp, i64, i64, vp]
+        L.rqo_marlin_repack.argtypes = [vp, vp, i64, i64, vp]
+        L.rqo_marlin_dequant.argtypes = [vp, vp, i64, i64, vp]
+        L.rqo_marlin_gemv_f64.argtypes = [vp, i64, vp, vp, i64, i64, vp]
+        L.rqo_kv_quantize.argtypes = [vp, i64, i64, i64, i32, vp, vp]
+        L.rqo_kv_dequantize.argtypes = [vp, vp, i64, i64, i64, i32, vp]
         _lib = L
     return _lib
 
@@ -159,3 +164,59 @@ def fp8_gemm_quantized_f64(xq, xs, w_codes, ws) -> np.ndarray:
     y = np.empty((m, n), dtype=np.float64)
     lib().rqo_fp8_gemm_quantized_f64(_p(xq), _p(xs), m, _p(w_codes), _p(ws), n, k, _p(y))
     return y
+
+
+# ---- Marlin INT4 weights (marlin_gemv.rs) ----
+
+def marlin_repack(w: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """repack_marlin_tiles (marlin_gemv.rs:66-97): u32 [ceil(k/32), n, 4]."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    scales = np.ascontiguousarray(scales, dtype=np.float32).reshape(-1)
+    n, k = w.shape
+    packed = np.empty(((k + 31) // 32, n, 4), dtype=np.uint32)
+    lib().rqo_marlin_repack(_p(w), _p(scales), n, k, _p(packed))
+    return packed
+
+
+def marlin_dequant(packed: np.ndarray, scales: np.ndarray, k: int) -> np.ndarray:
+    """MarlinWeight::dequantize (marlin_gemv.rs:42-61): f32 [n, k]."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint32)
+    scales = np.ascontiguousarray(scales, dtype=np.float32).reshape(-1)
+    n = scales.size
+    out = np.empty((n, k), dtype=np.float32)
+    lib().rqo_marlin_dequant(_p(packed), _p(scales), n, k, _p(out))
+    return out
+
+
+def marlin_gemv_f64(x: np.ndarray, packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    packed = np.ascontiguousarray(packed, dtype=np.uint32)
+    scales = np.ascontiguousarray(scales, dtype=np.float32).reshape(-1)
+    m, k = x.shape
+    n = scales.size
+    y = np.empty((m, n), dtype=np.float64)
+    lib().rqo_marlin_gemv_f64(_p(x), m, _p(packed), _p(scales), n, k, _p(y))
+    return y
+
+
+# ---- paged-KV quantizer (cache/paged/quantize.rs) ----
+
+def kv_quantize(t: np.ndarray, int8: bool = False):
+    """quantize_fp8 / quantize_int8 (quantize.rs:12-46, 62-96): (codes u8 of
+    t's shape, scales f32 [h]); a tensor that is not 4-D counts as [1, 1, n, 1]."""
+    t = np.ascontiguousarray(t, dtype=np.float32)
+    b, h, sd = (t.shape[0], t.shape[1], t.shape[2] * t.shape[3]) if t.ndim == 4 else (1, 1, t.size)
+    q = np.empty(t.shape, dtype=np.uint8)
+    s = np.empty(h, dtype=np.float32)
+    lib().rqo_kv_quantize(_p(t), b, h, sd, int(int8), _p(q), _p(s))
+    return q, s
+
+
+def kv_dequantize(q: np.ndarray, scales: np.ndarray, int8: bool = False) -> np.ndarray:
+    """dequantize_fp8 / dequantize_int8 (quantize.rs:48-57, 98-107) in f32."""
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32).reshape(-1)
+    b, h, sd = (q.shape[0], q.shape[1], q.shape[2] * q.shape[3]) if q.ndim == 4 else (1, 1, q.size)
+    out = np.empty(q.shape, dtype=np.float32)
+    lib().rqo_kv_dequantize(_p(q), _p(scales), b, h, sd, int(int8), _p(out))
+    return out

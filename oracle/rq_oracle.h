@@ -91,6 +91,24 @@ void rqo_fp8_gemm_quantized_f64(const uint8_t *xq, const float *xs, int64_t m,
                                 const uint8_t *w, const float *ws, int64_t n,
                                 int64_t k, double *y);
 
+/* ---- Marlin INT4 weights (crates/runtimed-model/src/ops/marlin_gemv.rs) ----
+ * packed holds ceil(k/32) * n records of 4 u32: record [c][r] carries row r,
+ * inputs 32c .. 32c+31, input 32c + 8j + i in bits 4i..4i+3 of word j. */
+/* repack_marlin_tiles (marlin_gemv.rs:66-97). */
+void rqo_marlin_repack(const float *w, const float *s, int64_t n, int64_t k, uint32_t *packed);
+/* MarlinWeight::dequantize (marlin_gemv.rs:42-61): [n, k] f32. */
+void rqo_marlin_dequant(const uint32_t *packed, const float *s, int64_t n, int64_t k, float *out);
+/* cpu_marlin_gemv_fallback (marlin_gemv.rs:100-116) in double. */
+void rqo_marlin_gemv_f64(const float *x, int64_t m, const uint32_t *packed, const float *s, int64_t n,
+                         int64_t k, double *y);
+
+/* ---- paged-KV quantizer (crates/runtimed-model/src/cache/paged/quantize.rs) ----
+ * t is [b, h, sd] f32 (sd = tokens * head_dim); int8 selects quantize_int8. */
+void rqo_kv_quantize(const float *t, int64_t b, int64_t h, int64_t sd, int int8, uint8_t *q,
+                     float *scales);
+void rqo_kv_dequantize(const uint8_t *q, const float *scales, int64_t b, int64_t h, int64_t sd, int int8,
+                       float *out);
+
 #ifdef __cplusplus
 }
 #endif

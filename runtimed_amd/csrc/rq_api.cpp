@@ -296,4 +296,69 @@ int rq_fp8_gemm(const void *x, int xtype, int64_t m, const uint8_t *w, const flo
   return rc ? rc : rc2;
 }
 
+int rq_marlin_repack(const void *w, int wtype, const float *scales, int64_t n, int64_t k, uint32_t *packed,
+                     void *stream) {
+  g_last_error.clear();
+  if (!valid_ftype(wtype)) return set_error(RQ_E_ARG, "weight type %d not supported", wtype);
+  if (n < 0 || k <= 0) return set_error(RQ_E_SHAPE, "bad shape [%lld, %lld]", (long long)n, (long long)k);
+  if (n == 0) return RQ_OK;
+  if (!w || !scales || !packed) return set_error(RQ_E_ARG, "null argument");
+  return launch_marlin_repack(w, wtype, scales, n, k, packed, as_stream(stream));
+}
+
+int rq_marlin_dequant(const uint32_t *packed, const float *scales, int64_t n, int64_t k, float *dev_out,
+                      void *stream) {
+  g_last_error.clear();
+  if (n < 0 || k <= 0) return set_error(RQ_E_SHAPE, "bad shape [%lld, %lld]", (long long)n, (long long)k);
+  if (n == 0) return RQ_OK;
+  if (!packed || !scales || !dev_out) return set_error(RQ_E_ARG, "null argument");
+  return launch_marlin_dequant(packed, scales, n, k, dev_out, as_stream(stream));
+}
+
+int rq_marlin_linear(const uint32_t *packed, const float *scales, int64_t n, int64_t k, const void *x, int xtype,
+                     int64_t m, void *y, int ytype, void *stream) {
+  g_last_error.clear();
+  if (!valid_ftype(xtype)) return set_error(RQ_E_ARG, "activation type %d not supported", xtype);
+  if (!valid_ftype(ytype)) return set_error(RQ_E_ARG, "output type %d not supported", ytype);
+  if (m < 0 || n < 0 || k <= 0)
+    return set_error(RQ_E_SHAPE, "bad shape m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
+  if (m == 0 || n == 0) return RQ_OK;
+  if (!packed || !scales || !x || !y) return set_error(RQ_E_ARG, "null argument");
+  return launch_marlin_linear(packed, scales, n, k, x, xtype, m, y, ytype, as_stream(stream));
+}
+
+static bool valid_kv_mode(int mode) { return mode == RQ_KV_F16 || mode == RQ_KV_FP8 || mode == RQ_KV_INT8; }
+
+int rq_kv_quantize(const void *t, int ttype, int64_t b, int64_t h, int64_t sd, int mode, void *q, float *scales,
+                   void *stream) {
+  g_last_error.clear();
+  if (!valid_ftype(ttype)) return set_error(RQ_E_ARG, "input type %d not supported", ttype);
+  if (!valid_kv_mode(mode)) return set_error(RQ_E_ARG, "bad kv mode %d", mode);
+  if (b < 0 || h < 0 || sd < 0)
+    return set_error(RQ_E_SHAPE, "bad shape [%lld, %lld, %lld]", (long long)b, (long long)h, (long long)sd);
+  if (h == 0) return RQ_OK;
+  if (!scales) return set_error(RQ_E_ARG, "null scales");
+  if (b == 0 || sd == 0) {
+    // No elements: every head's maximum is 0, so its scale is the floor.
+    std::vector<float> fill((size_t)h, mode == RQ_KV_F16 ? 1.0f : 1e-8f);
+    const hipError_t e = hipMemcpyAsync(scales, fill.data(), (size_t)h * sizeof(float), hipMemcpyHostToDevice,
+                                        as_stream(stream));
+    return hip_check(e, "hipMemcpyAsync");
+  }
+  if (!t || !q) return set_error(RQ_E_ARG, "null argument");
+  return launch_kv_quantize(t, ttype, b, h, sd, mode, q, scales, as_stream(stream));
+}
+
+int rq_kv_dequantize(const void *q, int mode, const float *scales, int64_t b, int64_t h, int64_t sd, void *out,
+                     int otype, void *stream) {
+  g_last_error.clear();
+  if (!valid_ftype(otype)) return set_error(RQ_E_ARG, "output type %d not supported", otype);
+  if (!valid_kv_mode(mode)) return set_error(RQ_E_ARG, "bad kv mode %d", mode);
+  if (b < 0 || h < 0 || sd < 0)
+    return set_error(RQ_E_SHAPE, "bad shape [%lld, %lld, %lld]", (long long)b, (long long)h, (long long)sd);
+  if (b == 0 || h == 0 || sd == 0) return RQ_OK;
+  if (!q || !out || (mode != RQ_KV_F16 && !scales)) return set_error(RQ_E_ARG, "null argument");
+  return launch_kv_dequantize(q, mode, scales, b, h, sd, out, otype, as_stream(stream));
+}
+
 }  // extern "C"

@@ -22,6 +22,7 @@
 // Roofline: MFMA-bound (fp8 dense peak 5.0 PFLOP/s); flops = 2*m*n*k.
 #include <stdlib.h>
 
+#include "rq_e4m3.h"
 #include "rq_epilogue.h"
 #include "rq_internal.h"
 
@@ -30,56 +31,6 @@ namespace {
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-// FP8_E4M3_LUT value of a positive code 0..126 (load_safetensors.rs:14-29).
-__device__ __forceinline__ float e4m3_pos_value(int c) {
-  const int e = c >> 3, m = c & 7;
-  return e == 0 ? (float)m * 0.001953125f : ldexpf(1.0f + (float)m * 0.125f, e - 7);
-}
-
-// f32_to_fp8_e4m3 (load_safetensors.rs:53-69), bit-exact.
-__device__ uint32_t enc_e4m3_ref(float f) {
-  if (f != f) return 0x7Fu;
-  const uint32_t sign = (__float_as_uint(f) >> 24) & 0x80u;
-  const float a = fabsf(f);
-  if (a <= 0.0f) return sign;
-  if (a >= 448.0f) return sign | 0x7Eu;
-  int lo = 0, hi = 127;
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (e4m3_pos_value(mid) < a) lo = mid + 1;
-    else hi = mid;
-  }
-  const float above = e4m3_pos_value(lo);
-  if (above == a) return sign | (uint32_t)lo;
-  const float below = e4m3_pos_value(lo - 1);
-  return sign | (uint32_t)((a - below <= above - a) ? lo - 1 : lo);
-}
-
-// Clamp to +-448 then OCP e4m3fn round-to-nearest-even.
-__device__ uint32_t enc_e4m3_rne(float f) {
-  if (f != f) return 0x7Fu;
-  const uint32_t sign = (__float_as_uint(f) >> 24) & 0x80u;
-  float a = fminf(fabsf(f), 448.0f);
-  if (a < 0.015625f) return sign | (uint32_t)__builtin_rintf(a * 512.0f);
-  const uint32_t u = __float_as_uint(a);
-  int e = (int)((u >> 23) & 0xFFu) - 127;
-  const uint32_t man = u & 0x7FFFFFu;
-  uint32_t r = man >> 20;
-  const uint32_t rem = man & 0xFFFFFu;
-  if (rem > 0x80000u || (rem == 0x80000u && (r & 1u))) r += 1;
-  if (r == 8) {
-    r = 0;
-    e += 1;
-  }
-  return sign | (((uint32_t)(e + 7) << 3) | r);
-}
-
-__device__ __forceinline__ float load_x1(const void *x, int xtype, int64_t i) {
-  if (xtype == RQ_F32) return static_cast<const float *>(x)[i];
-  if (xtype == RQ_BF16) return bf16_bits_to_f32(static_cast<const uint16_t *>(x)[i]);
-  return (float)static_cast<const _Float16 *>(x)[i];
-}
 
 // One workgroup per activation row.
 __global__ __launch_bounds__(256) void k_fp8_quant_rows(const void *__restrict__ x, int xtype,
@@ -109,15 +60,6 @@ __global__ __launch_bounds__(256) void k_fp8_quant_rows(const void *__restrict__
   if (tid == 0) xs[row] = amax / 448.0f;
 }
 
-// e4m3 decode for the scalar path (LUT formula of load_safetensors.rs:14-29).
-__device__ __forceinline__ float dec_e4m3(uint32_t b) {
-  const int e = (b >> 3) & 0xF, m = b & 7;
-  float v;
-  if (e == 0) v = (float)m * 0.001953125f;
-  else if (e == 15 && m == 7) v = __uint_as_float(0x7FC00000u);
-  else v = ldexpf(1.0f + (float)m * 0.125f, e - 7);
-  return (b & 0x80u) ? -v : v;
-}
 
 // Scalar fallback for shapes the tiled kernel does not take (k % 128 != 0).
 __global__ __launch_bounds__(256) void k_fp8_gemm_scalar(const uint8_t *__restrict__ xq,

@@ -88,6 +88,19 @@ int launch_fp8_quantize(const void *x, int xtype, int64_t m, int64_t k, int mode
 int launch_fp8_gemm(const uint8_t *xq, const float *xs, int64_t m, const uint8_t *w,
                     const float *ws, int64_t n, int64_t k, void *y, int ytype, hipStream_t s);
 
+// Marlin INT4 weights (arguments validated by the caller).
+int launch_marlin_repack(const void *w, int wtype, const float *s, int64_t n, int64_t k, uint32_t *packed,
+                         hipStream_t st);
+int launch_marlin_dequant(const uint32_t *packed, const float *s, int64_t n, int64_t k, float *out,
+                          hipStream_t st);
+int launch_marlin_linear(const uint32_t *packed, const float *s, int64_t n, int64_t k, const void *x, int xtype,
+                         int64_t m, void *y, int ytype, hipStream_t st);
+// Paged-KV block quantizer (arguments validated by the caller).
+int launch_kv_quantize(const void *t, int ttype, int64_t b, int64_t h, int64_t sd, int mode, void *q,
+                       float *scales, hipStream_t s);
+int launch_kv_dequantize(const void *q, int mode, const float *scales, int64_t b, int64_t h, int64_t sd, void *out,
+                         int otype, hipStream_t s);
+
 // ---- exact scalar conversions shared by device code ----
 
 // f16 bit pattern -> f32 bit pattern, integer-exact including subnormals and

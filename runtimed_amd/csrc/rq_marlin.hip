@@ -1,0 +1,221 @@
+// rq_marlin.hip -- Marlin INT4 weights on gfx950: repack, dequant and the
+// fused GEMV (crates/runtimed-model/src/ops/marlin_gemv.rs).
+//
+// Layout (the reference's, marlin_gemv.rs:66-97): u32 packed[ceil(k/32)][n][4];
+// record [c][r] holds row r, inputs 32c .. 32c+31, input 32c + 8j + i in bits
+// 4i .. 4i+3 of word j; value (nibble - 8) * scale[r].  Records of one chunk
+// are contiguous over rows, so lanes on consecutive rows read one contiguous
+// run with 128-bit loads.
+//
+// GEMV (marlin_gemv.rs:119-202 launches one thread per output over all of
+// k): here a 512-thread workgroup owns R rows and splits the k chunks over
+// 8 waves x (64 / R) lane groups, so a decode-sized matrix still spreads
+// over the whole chip; partial sums meet through lane exchanges and LDS,
+// scale[r] is applied once at the end as in the reference (acc * scale).
+// Bound: HBM, 0.5 byte per weight + 4 bytes of scale per row.
+#include "rq_e4m3.h"
+#include "rq_internal.h"
+
+namespace rq {
+namespace {
+
+// repack_marlin_tiles (marlin_gemv.rs:66-97): one thread per (row, chunk),
+// chunk fastest so that a wave reads one row's inputs contiguously.
+__global__ __launch_bounds__(256) void k_marlin_repack(const void *__restrict__ w, int wtype,
+                                                       const float *__restrict__ s, int64_t n,
+                                                       int64_t k, int64_t kc, uint4 *__restrict__ packed) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= n * kc) return;
+  const int64_t r = idx / kc, c = idx - r * kc;
+  const float sr = s[r];
+  const float inv_s = fabsf(sr) > 1e-12f ? 1.0f / sr : 1.0f;
+  uint32_t words[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t kk = c * 32 + 8 * j + i;
+      uint32_t q = 8;
+      if (kk < k) {
+        const float t = roundf(load_x1(w, wtype, r * k + kk) * inv_s) + 8.0f;
+        q = (t != t) ? 0u : (uint32_t)fminf(fmaxf(t, 0.0f), 15.0f);
+      }
+      word |= q << (4 * i);
+    }
+    words[j] = word;
+  }
+  packed[c * n + r] = make_uint4(words[0], words[1], words[2], words[3]);
+}
+
+// MarlinWeight::dequantize (marlin_gemv.rs:42-61): one thread per (row, chunk).
+__global__ __launch_bounds__(256) void k_marlin_dequant(const uint4 *__restrict__ packed,
+                                                        const float *__restrict__ s, int64_t n, int64_t k,
+                                                        int64_t kc, float *__restrict__ out, bool vec) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= n * kc) return;
+  const int64_t r = idx / kc, c = idx - r * kc;
+  const uint4 q = packed[c * n + r];
+  const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+  const float sr = s[r];
+  float *o = out + r * k + c * 32;
+  if (vec && c * 32 + 32 <= k) {
+#pragma unroll
+    for (int j4 = 0; j4 < 8; ++j4) {
+      const uint32_t v = wd[j4 >> 1] >> (16 * (j4 & 1));
+      reinterpret_cast<float4 *>(o)[j4] =
+          make_float4((float)((int)(v & 15u) - 8) * sr, (float)((int)((v >> 4) & 15u) - 8) * sr,
+                      (float)((int)((v >> 8) & 15u) - 8) * sr, (float)((int)((v >> 12) & 15u) - 8) * sr);
+    }
+  } else {
+    for (int e = 0; e < 32 && c * 32 + e < k; ++e)
+      o[e] = (float)((int)((wd[e >> 3] >> (4 * (e & 7))) & 15u) - 8) * sr;
+  }
+}
+
+// Sum over the 32 inputs of one record of x[base .. base+32) * (q - 8).
+__device__ __forceinline__ float record_dot(const uint32_t (&wd)[4], const void *x, int xtype, int64_t base,
+                                            int valid, bool vec) {
+  float a = 0.0f;
+  if (vec && valid == 32) {
+#pragma unroll
+    for (int j4 = 0; j4 < 8; ++j4) {
+      const float4 xv = load_x4(x, xtype, base + 4 * j4);
+      const uint32_t v = wd[j4 >> 1] >> (16 * (j4 & 1));
+      a = fmaf(xv.x, (float)(v & 15u) - 8.0f, a);
+      a = fmaf(xv.y, (float)((v >> 4) & 15u) - 8.0f, a);
+      a = fmaf(xv.z, (float)((v >> 8) & 15u) - 8.0f, a);
+      a = fmaf(xv.w, (float)((v >> 12) & 15u) - 8.0f, a);
+    }
+  } else {
+    for (int e = 0; e < valid; ++e)
+      a = fmaf(load_x1(x, xtype, base + e), (float)((wd[e >> 3] >> (4 * (e & 7))) & 15u) - 8.0f, a);
+  }
+  return a;
+}
+
+// y[m0 .. m0+MT) x [R rows of this workgroup].
+template <int R, int MT>
+__global__ __launch_bounds__(512) void k_marlin_gemv(const uint4 *__restrict__ packed, const float *__restrict__ s,
+                                                     const void *__restrict__ x, int xtype, int64_t m, int64_t n,
+                                                     int64_t k, int64_t kc, void *__restrict__ y, int ytype,
+                                                     bool vec) {
+  constexpr int GROUPS = 64 / R;      // lane groups per wave
+  constexpr int SLOTS = 8 * GROUPS;   // chunk slots per workgroup
+  __shared__ float red[8][MT][R];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rl = lane % R;
+  const int64_t row = (int64_t)blockIdx.x * R + rl;
+  const int slot = wave * GROUPS + lane / R;
+  const int64_t m0 = (int64_t)blockIdx.y * MT;
+  float acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
+  if (row < n) {
+    // Batches of 4 records per lane, all loads issued before the first use.
+    for (int64_t c0 = slot; c0 < kc; c0 += 4 * SLOTS) {
+      uint4 q[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t c = c0 + j * SLOTS;
+        q[j] = c < kc ? packed[c * n + row] : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t c = c0 + j * SLOTS;
+        if (c < kc) {
+          const uint32_t wd[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+          const int64_t kb = c * 32;
+          const int valid = (int)(k - kb < 32 ? k - kb : 32);
+#pragma unroll
+          for (int t = 0; t < MT; ++t)
+            if (m0 + t < m) acc[t] += record_dot(wd, x, xtype, (m0 + t) * k + kb, valid, vec);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int off = R; off < 64; off <<= 1)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] += __shfl_xor(acc[t], off);
+  if (lane < R) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) red[wave][t][rl] = acc[t];
+  }
+  __syncthreads();
+  if (threadIdx.x < R * MT) {
+    const int t = threadIdx.x / R, l = threadIdx.x % R;
+    const int64_t orow = (int64_t)blockIdx.x * R + l, xr = m0 + t;
+    if (orow < n && xr < m) {
+      float v = 0.0f;
+#pragma unroll
+      for (int wv = 0; wv < 8; ++wv) v += red[wv][t][l];
+      store_out(y, ytype, xr * n + orow, v * s[orow]);
+    }
+  }
+}
+
+template <int R, int MT>
+void launch_gemv(const uint4 *packed, const float *s, const void *x, int xtype, int64_t m, int64_t n, int64_t k,
+                 int64_t kc, void *y, int ytype, bool vec, hipStream_t st) {
+  const dim3 grid((unsigned)((n + R - 1) / R), (unsigned)((m + MT - 1) / MT));
+  hipLaunchKernelGGL((k_marlin_gemv<R, MT>), grid, dim3(512), 0, st, packed, s, x, xtype, m, n, k, kc, y, ytype,
+                     vec);
+}
+
+template <int R>
+void launch_gemv_r(const uint4 *packed, const float *s, const void *x, int xtype, int64_t m, int64_t n, int64_t k,
+                   int64_t kc, void *y, int ytype, bool vec, hipStream_t st) {
+  if (m == 1) launch_gemv<R, 1>(packed, s, x, xtype, m, n, k, kc, y, ytype, vec, st);
+  else if (m == 2) launch_gemv<R, 2>(packed, s, x, xtype, m, n, k, kc, y, ytype, vec, st);
+  else launch_gemv<R, 4>(packed, s, x, xtype, m, n, k, kc, y, ytype, vec, st);
+}
+
+int last_launch(const char *what) {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "%s launch: %s", what, hipGetErrorString(e));
+}
+
+}  // namespace
+
+int launch_marlin_repack(const void *w, int wtype, const float *s, int64_t n, int64_t k, uint32_t *packed,
+                         hipStream_t st) {
+  const int64_t kc = (k + 31) / 32;
+  const int64_t threads = n * kc;
+  hipLaunchKernelGGL(k_marlin_repack, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, w, wtype, s, n,
+                     k, kc, reinterpret_cast<uint4 *>(packed));
+  return last_launch("marlin repack");
+}
+
+int launch_marlin_dequant(const uint32_t *packed, const float *s, int64_t n, int64_t k, float *out,
+                          hipStream_t st) {
+  const int64_t kc = (k + 31) / 32;
+  const int64_t threads = n * kc;
+  const bool vec = (k % 4 == 0) && (reinterpret_cast<uintptr_t>(out) % 16 == 0);
+  hipLaunchKernelGGL(k_marlin_dequant, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                     reinterpret_cast<const uint4 *>(packed), s, n, k, kc, out, vec);
+  return last_launch("marlin dequant");
+}
+
+int launch_marlin_linear(const uint32_t *packed, const float *s, int64_t n, int64_t k, const void *x, int xtype,
+                         int64_t m, void *y, int ytype, hipStream_t st) {
+  const int64_t kc = (k + 31) / 32;
+  const uint4 *p = reinterpret_cast<const uint4 *>(packed);
+  const bool vec = (k % 4 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0);
+  const int xsize = xtype == RQ_F32 ? 4 : 2, ysize = ytype == RQ_F32 ? 4 : 2;
+  // grid.y holds at most 65535 row groups of 4: longer activations go in parts.
+  constexpr int64_t PART = 65535 * 4;
+  for (int64_t r0 = 0; r0 < m; r0 += PART) {
+    const int64_t mp = m - r0 < PART ? m - r0 : PART;
+    const void *xp = static_cast<const uint8_t *>(x) + r0 * k * xsize;
+    void *yp = static_cast<uint8_t *>(y) + r0 * n * ysize;
+    if (n <= 8192) launch_gemv_r<16>(p, s, xp, xtype, mp, n, k, kc, yp, ytype, vec, st);
+    else if (n <= 32768) launch_gemv_r<32>(p, s, xp, xtype, mp, n, k, kc, yp, ytype, vec, st);
+    else launch_gemv_r<64>(p, s, xp, xtype, mp, n, k, kc, yp, ytype, vec, st);
+    const int rc = last_launch("marlin gemv");
+    if (rc) return rc;
+  }
+  return RQ_OK;
+}
+
+}  // namespace rq

@@ -24,6 +24,9 @@ GEOMETRY = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q5
 
 F32, F16, BF16, F8E4M3 = 0, 1, 30, 128
 FP8_UNSCALED, FP8_PER_TOKEN = 0, 1
+# rq_kv_mode: CachePrecision (cache/paged/block.rs:23-27)
+KV_F16, KV_FP8, KV_INT8 = 0, 1, 2
+SINK_TOKENS_COUNT = 16  # quantize.rs:9
 _FTYPE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.float8_e4m3fn: F8E4M3,
           torch.uint8: F8E4M3}
 
@@ -70,6 +73,11 @@ def lib() -> ctypes.CDLL:
         L.rq_fp8_quantize.argtypes = [vp, i32, i64, i64, i32, vp, vp, vp]
         L.rq_fp8_gemm.argtypes = [vp, i32, i64, vp, vp, i64, i64, vp, i32, i32, vp]
         L.rq_fp8_gemm_q.argtypes = [vp, vp, i64, vp, vp, i64, i64, vp, i32, vp]
+        L.rq_marlin_repack.argtypes = [vp, i32, vp, i64, i64, vp, vp]
+        L.rq_marlin_dequant.argtypes = [vp, vp, i64, i64, vp, vp]
+        L.rq_marlin_linear.argtypes = [vp, vp, i64, i64, vp, i32, i64, vp, i32, vp]
+        L.rq_kv_quantize.argtypes = [vp, i32, i64, i64, i64, i32, vp, vp, vp]
+        L.rq_kv_dequantize.argtypes = [vp, i32, vp, i64, i64, i64, vp, i32, vp]
         for f in ("rq_weight_create", "rq_weight_info", "rq_dequant_f32", "rq_dequant_tensor",
                   "rq_linear", "rq_fp8_quantize", "rq_fp8_gemm", "rq_fp8_gemm_q"):
             getattr(L, f).restype = i32
@@ -200,3 +208,156 @@ def fp8_gemm_q(xq: torch.Tensor, xs: Optional[torch.Tensor], w: torch.Tensor,
     check(lib().rq_fp8_gemm_q(_ptr(xq), _ptr(xs), m, _ptr(w), _ptr(w_scale), n, k, _ptr(out),
                               ftype(out.dtype), _stream(xq.device)))
     return out
+
+
+# ---- Marlin INT4 weights (crates/runtimed-model/src/ops/marlin_gemv.rs) ----
+
+class MarlinWeight:
+    """Packed INT4 weights (marlin_gemv.rs:11-63): `packed` holds the u32 words
+    [ceil(in_dim/32), out_dim, 4] (as torch.int32 bits), `scales` f32 [out_dim]."""
+
+    def __init__(self, packed: torch.Tensor, scales: torch.Tensor, in_dim: int, out_dim: int):
+        if packed.dtype not in (torch.int32, torch.uint32):
+            raise RqError(-5, f"marlin packed must be U32, got {packed.dtype}")
+        if tuple(scales.shape) not in ((out_dim,), (out_dim, 1)):
+            raise RqError(-4, f"marlin_scales: expected [{out_dim}], got {list(scales.shape)}")
+        if packed.device != scales.device:
+            raise RqError(-5, "packed and scales must be on the same device")
+        k_chunks = (in_dim + 31) // 32
+        if packed.numel() < k_chunks * out_dim * 4:
+            raise RqError(-4, f"marlin_packed: expected [{k_chunks}, {out_dim}, 4], got {list(packed.shape)}")
+        self.packed, self.scales, self.in_dim, self.out_dim = packed, scales, in_dim, out_dim
+
+    @property
+    def device(self) -> torch.device:
+        return self.packed.device
+
+    def resident_bytes(self) -> int:
+        return self.packed.numel() * self.packed.element_size() + self.scales.numel() * self.scales.element_size()
+
+    def _scales_f32(self) -> torch.Tensor:
+        return self.scales.reshape(-1).to(torch.float32).contiguous()
+
+    def dequantize(self) -> torch.Tensor:
+        """f32 [out_dim, in_dim], bit-exact (marlin_gemv.rs:42-61)."""
+        out = torch.empty((self.out_dim, self.in_dim), dtype=torch.float32, device=self.device)
+        check(lib().rq_marlin_dequant(_ptr(self.packed.contiguous()), _ptr(self._scales_f32()), self.out_dim,
+                                      self.in_dim, _ptr(out), _stream(self.device)))
+        return out
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return marlin_gemv(x, self)
+
+
+def repack_marlin_tiles(weight: torch.Tensor, scales: torch.Tensor) -> MarlinWeight:
+    """repack_marlin_tiles (marlin_gemv.rs:66-97), run on the device."""
+    if weight.dim() != 2:
+        raise RqError(-5, f"weight must be 2D, got {list(weight.shape)}")
+    out_dim, in_dim = weight.shape
+    s32 = scales.reshape(-1).to(torch.float32).contiguous()
+    if s32.numel() != out_dim:
+        raise RqError(-4, f"scales: expected [{out_dim}], got [{s32.numel()}]")
+    w = weight.contiguous()
+    packed = torch.empty(((in_dim + 31) // 32, out_dim, 4), dtype=torch.int32, device=w.device)
+    if weight.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        w = w.to(torch.float32)
+    check(lib().rq_marlin_repack(_ptr(w), ftype(w.dtype), _ptr(s32), out_dim, in_dim, _ptr(packed),
+                                 _stream(w.device)))
+    return MarlinWeight(packed, scales, in_dim, out_dim)
+
+
+def marlin_gemv(x: torch.Tensor, w: MarlinWeight) -> torch.Tensor:
+    """x @ (w * scale)^T over the last dimension of x, result in x's dtype
+    (marlin_gemv.rs:119-202)."""
+    in_dim = x.shape[-1] if x.dim() else 0
+    if in_dim != w.in_dim:
+        raise RqError(-4, f"marlin_gemv: expected [{w.in_dim}], got {list(x.shape)}")
+    rows = x.numel() // in_dim if in_dim else 0
+    out = torch.empty((*x.shape[:-1], w.out_dim), dtype=x.dtype, device=x.device)
+    if rows == 0 or w.out_dim == 0:
+        return out.zero_()
+    xc = x.contiguous()
+    if xc.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        xc = xc.to(torch.float32)
+        out = out.to(torch.float32)
+    check(lib().rq_marlin_linear(_ptr(w.packed.contiguous()), _ptr(w._scales_f32()), w.out_dim, w.in_dim,
+                                 _ptr(xc), ftype(xc.dtype), rows, _ptr(out), ftype(out.dtype), _stream(x.device)))
+    return out.to(x.dtype)
+
+
+# ---- paged-KV block quantizer (crates/runtimed-model/src/cache/paged/quantize.rs) ----
+
+def _kv_dims(t: torch.Tensor):
+    if t.dim() == 4:
+        return t.shape[0], t.shape[1], t.shape[2] * t.shape[3]
+    return 1, 1, t.numel()
+
+
+def _kv_input(t: torch.Tensor) -> torch.Tensor:
+    t = t.contiguous()
+    return t if t.dtype in (torch.float32, torch.float16, torch.bfloat16) else t.to(torch.float32)
+
+
+def _kv_quantize(t: torch.Tensor, mode: int):
+    b, h, sd = _kv_dims(t)
+    src = _kv_input(t)
+    qdt = {KV_FP8: torch.float8_e4m3fn, KV_INT8: torch.uint8, KV_F16: torch.float16}[mode]
+    q = torch.empty(t.shape, dtype=qdt, device=t.device)
+    s = torch.empty(h, dtype=torch.float32, device=t.device)
+    check(lib().rq_kv_quantize(_ptr(src), ftype(src.dtype), b, h, sd, mode, _ptr(q), _ptr(s),
+                               _stream(t.device)))
+    return q, s.reshape(1, h, 1, 1)
+
+
+def quantize_fp8(t: torch.Tensor):
+    """quantize_fp8 (quantize.rs:12-46): (e4m3 codes of t's shape, scales [1, h, 1, 1])."""
+    return _kv_quantize(t, KV_FP8)
+
+
+def quantize_int8(t: torch.Tensor):
+    """quantize_int8 (quantize.rs:62-96): (int8 codes as uint8 of t's shape, scales [1, h, 1, 1])."""
+    return _kv_quantize(t, KV_INT8)
+
+
+def _kv_dequantize(q: torch.Tensor, scale: Optional[torch.Tensor], mode: int, target_dtype: torch.dtype):
+    b, h, sd = _kv_dims(q)
+    out = torch.empty(q.shape, dtype=target_dtype, device=q.device)
+    s = scale.reshape(-1).to(torch.float32).contiguous() if scale is not None else None
+    if s is not None and s.numel() != h:
+        raise RqError(-4, f"scale: expected {h} entries, got {s.numel()}")
+    check(lib().rq_kv_dequantize(_ptr(q.contiguous()), mode, _ptr(s), b, h, sd, _ptr(out), ftype(target_dtype),
+                                 _stream(q.device)))
+    return out
+
+
+def dequantize_fp8(t: torch.Tensor, scale: torch.Tensor, target_dtype: torch.dtype) -> torch.Tensor:
+    """dequantize_fp8 (quantize.rs:48-57)."""
+    return _kv_dequantize(t, scale, KV_FP8, target_dtype)
+
+
+def dequantize_int8(t: torch.Tensor, scale: torch.Tensor, target_dtype: torch.dtype) -> torch.Tensor:
+    """dequantize_int8 (quantize.rs:98-107)."""
+    return _kv_dequantize(t, scale, KV_INT8, target_dtype)
+
+
+def quantize_block_kv(token_offset: int, k: torch.Tensor, v: torch.Tensor, requested_precision: int):
+    """quantize_block_kv (quantize.rs:109-135): the first SINK_TOKENS_COUNT
+    tokens, and Fp16 caches, stay f16 with scale 1."""
+    if token_offset < SINK_TOKENS_COUNT or requested_precision == KV_F16:
+        kf, _ = _kv_quantize(k, KV_F16)
+        vf, _ = _kv_quantize(v, KV_F16)
+        one_k = torch.ones(1, dtype=torch.float32, device=k.device)
+        one_v = torch.ones(1, dtype=torch.float32, device=v.device)
+        return kf, vf, one_k, one_v, KV_F16
+    mode = KV_INT8 if requested_precision == KV_INT8 else KV_FP8
+    kq, ks = _kv_quantize(k, mode)
+    vq, vs = _kv_quantize(v, mode)
+    return kq, vq, ks, vs, mode
+
+
+def dequantize_block(q: torch.Tensor, scale: Optional[torch.Tensor], precision: int,
+                     target_dtype: torch.dtype) -> torch.Tensor:
+    """QuantizedCacheBlock::dequantize_k / dequantize_v (block.rs:85-140)."""
+    if precision == KV_F16:
+        return _kv_dequantize(q, None, KV_F16, target_dtype)
+    return _kv_dequantize(q, scale, precision, target_dtype)

@@ -22,7 +22,9 @@ def declared_symbols():
 def test_header_declares_the_boundary():
     syms = declared_symbols()
     for s in ("rq_weight_create", "rq_weight_destroy", "rq_dequant_f32", "rq_dequant_tensor",
-              "rq_linear", "rq_fp8_gemm", "rq_fp8_quantize", "rq_last_error"):
+              "rq_linear", "rq_fp8_gemm", "rq_fp8_quantize", "rq_last_error", "rq_embedding",
+              "rq_marlin_repack", "rq_marlin_dequant", "rq_marlin_linear", "rq_kv_quantize",
+              "rq_kv_dequantize"):
         assert s in syms
 
 
@@ -76,6 +78,19 @@ def test_null_and_enum_checks():
     assert L.rq_dequant_tensor(12, None, 0, 100, None, None) == -2
     assert L.rq_dequant_tensor(12, None, 10, 256, None, None) == -3
     assert L.rq_dequant_tensor(12, None, 0, 0, None, None) == 0  # empty stream is a no-op
+    # Marlin INT4 and the KV quantizer: enum, shape and null checks
+    assert L.rq_marlin_repack(None, 99, None, 4, 32, None, None) == -5
+    assert L.rq_marlin_repack(None, 0, None, 4, 0, None, None) == -4
+    assert L.rq_marlin_repack(None, 0, None, 0, 32, None, None) == 0      # no rows: no-op
+    assert L.rq_marlin_dequant(None, None, 4, 32, None, None) == -5
+    assert L.rq_marlin_linear(None, None, 4, 32, None, 0, 0, None, 0, None) == 0  # m = 0
+    assert L.rq_marlin_linear(None, None, 4, 32, None, 0, 1, None, 0, None) == -5
+    assert L.rq_marlin_linear(None, None, 4, 32, None, 0, -1, None, 0, None) == -4
+    assert L.rq_kv_quantize(None, 0, 1, 2, 16, 9, None, None, None) == -5   # bad mode
+    assert L.rq_kv_quantize(None, 0, -1, 2, 16, 1, None, None, None) == -4
+    assert L.rq_kv_quantize(None, 0, 1, 2, 16, 1, None, None, None) == -5  # null scales
+    assert L.rq_kv_dequantize(None, 1, None, 1, 2, 0, None, 0, None) == 0  # empty
+    assert L.rq_kv_dequantize(None, 2, None, 1, 2, 16, None, 0, None) == -5
     L.rq_weight_destroy(None)
 
 

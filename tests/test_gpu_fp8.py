@@ -64,6 +64,26 @@ def test_unscaled_encoder_bit_exact(dev):
     assert xs.cpu().numpy()[0] == 1.0
 
 
+def test_unscaled_encoder_ties_and_boundaries(dev):
+    # every e4m3 value, every midpoint between neighbours (exact ties, which
+    # the reference breaks towards the lower magnitude) and the floats one ulp
+    # either side of each, in both signs; the 2^-9 grid below 2^-6; values
+    # around 448 and tiny or subnormal inputs
+    pos = np.array([oracle.fp8_decode(c) for c in range(127)], np.float32)
+    mids = ((pos[:-1].astype(np.float64) + pos[1:]) / 2).astype(np.float32)
+    assert np.array_equal(mids.astype(np.float64), (pos[:-1].astype(np.float64) + pos[1:]) / 2)
+    near = np.concatenate([np.nextafter(mids, np.float32(0)), np.nextafter(mids, np.float32(np.inf)),
+                           np.nextafter(pos, np.float32(0)), np.nextafter(pos, np.float32(np.inf))])
+    grid = (np.arange(0, 8.01, 0.125, dtype=np.float32) / np.float32(512))
+    extra = np.array([447.9, 448.0, 464.0, 479.9, 480.0, 1e-30, 1e-40, 2.0 ** -10, 2.0 ** -11, 3e-3],
+                     np.float32)
+    vals = np.concatenate([pos, mids, near, grid, extra]).astype(np.float32)
+    vals = np.concatenate([vals, -vals])
+    t = torch.from_numpy(vals.reshape(1, -1)).to(dev)
+    xq, _ = rq.fp8_quantize(t, rq.FP8_UNSCALED)
+    assert np.array_equal(xq.cpu().numpy()[0], oracle.fp8_encode_array(vals))
+
+
 def _fp8_problem(m, n, k, seed):
     wv = synth.fp8_weight_values(seed, n, k)
     w = torch.from_numpy(wv).to("cuda")
