@@ -324,6 +324,71 @@ Tensor HipSubstrate::fp8_gemm(const Tensor &x, const Tensor &w, const Tensor *sc
   return y;
 }
 
+Tensor HipSubstrate::marlin_gemv(const Tensor &x, const MarlinWeight &w) const {
+  const size_t in_dim = x.dims().empty() ? 0 : x.dims().back();
+  if (in_dim != w.in_dim()) throw ModelError::shape("marlin_gemv", {w.in_dim()}, x.dims());
+  const size_t rows = in_dim ? x.elem_count() / in_dim : 0;
+  auto dims = leading(x.dims());
+  dims.push_back(w.out_dim());
+  Tensor y = Tensor::zeros(dims, x.dtype(), w.packed().device());
+  if (rows == 0 || w.out_dim() == 0) return y;
+  const int xt = dtype_rq(x.dtype());
+  if (xt != RQ_F32 && xt != RQ_F16 && xt != RQ_BF16) throw ModelError(ModelError::Config, "marlin: activation dtype");
+  rq_ok(rq_marlin_linear(static_cast<const uint32_t *>(w.packed().data()), static_cast<const float *>(w.scales().data()),
+                         (int64_t)w.out_dim(), (int64_t)in_dim, x.data(), xt, (int64_t)rows, y.data(), xt, stream_),
+        "marlin_gemv", {w.in_dim()}, x.dims());
+  return y;
+}
+
+// ------------------------------------------------------------ MarlinWeight --
+
+MarlinWeight MarlinWeight::create(Tensor packed, Tensor scales, size_t in_dim, size_t out_dim) {
+  if (packed.dtype() != DType::U32) throw ModelError(ModelError::Config, "marlin packed must be U32");
+  if (scales.dims() != std::vector<size_t>{out_dim} && scales.dims() != std::vector<size_t>{out_dim, 1})
+    throw ModelError::shape("marlin_scales", {out_dim}, scales.dims());
+  if (scales.dtype() != DType::F32) throw ModelError(ModelError::Config, "marlin scales must be F32");
+  if (packed.device() != scales.device())
+    throw ModelError(ModelError::Config, "packed and scales must be on the same device");
+  const size_t k_chunks = (in_dim + 31) / 32;
+  if (packed.elem_count() < k_chunks * out_dim * 4)
+    throw ModelError::shape("marlin_packed", {k_chunks, out_dim, 4}, packed.dims());
+  MarlinWeight mw;
+  mw.packed_ = std::move(packed);
+  mw.scales_ = std::move(scales);
+  mw.in_dim_ = in_dim;
+  mw.out_dim_ = out_dim;
+  return mw;
+}
+
+size_t MarlinWeight::resident_bytes() const {
+  return packed_.elem_count() * dtype_size(packed_.dtype()) + scales_.elem_count() * dtype_size(scales_.dtype());
+}
+
+Tensor MarlinWeight::dequantize(void *stream) const {
+  Tensor out = Tensor::zeros({out_dim_, in_dim_}, DType::F32, packed_.device());
+  if (out_dim_ == 0 || in_dim_ == 0) return out;
+  rq_ok(rq_marlin_dequant(static_cast<const uint32_t *>(packed_.data()), static_cast<const float *>(scales_.data()),
+                          (int64_t)out_dim_, (int64_t)in_dim_, static_cast<float *>(out.data()), stream),
+        "marlin_dequant");
+  return out;
+}
+
+MarlinWeight repack_marlin_tiles(const Tensor &weight, const Tensor &scales, void *stream) {
+  if (weight.dims().size() != 2) throw ModelError(ModelError::Config, "weight must be 2D");
+  const size_t out_dim = weight.dim(0), in_dim = weight.dim(1);
+  if (scales.elem_count() != out_dim) throw ModelError::shape("scales", {out_dim}, {scales.elem_count()});
+  if (scales.dtype() != DType::F32) throw ModelError(ModelError::Config, "marlin scales must be F32");
+  const int wt = dtype_rq(weight.dtype());
+  if (wt != RQ_F32 && wt != RQ_F16 && wt != RQ_BF16) throw ModelError(ModelError::Config, "marlin: weight dtype");
+  const size_t k_chunks = (in_dim + 31) / 32;
+  Tensor packed = Tensor::zeros({k_chunks, out_dim, 4}, DType::U32, weight.device());
+  if (out_dim && in_dim)
+    rq_ok(rq_marlin_repack(weight.data(), wt, static_cast<const float *>(scales.data()), (int64_t)out_dim,
+                           (int64_t)in_dim, static_cast<uint32_t *>(packed.data()), stream),
+          "repack_marlin_tiles");
+  return MarlinWeight::create(std::move(packed), scales, in_dim, out_dim);
+}
+
 // --------------------------------------------------------------- Fp8Weight --
 
 Fp8Weight Fp8Weight::create(Tensor weight, Tensor scale, size_t in_dim, size_t out_dim) {
@@ -450,13 +515,63 @@ Tensor Weights::embed(const std::string &name, const std::vector<uint32_t> &ids)
   return rows.reshaped({1, rows.dim(0), rows.dim(1)});
 }
 
+void Weights::insert_marlin(const std::string &name, const MarlinWeight &mw) {
+  const std::string suffix = ".weight";
+  const bool has = name.size() >= suffix.size() && name.compare(name.size() - suffix.size(), suffix.size(), suffix) == 0;
+  const std::string stem = has ? name.substr(0, name.size() - suffix.size()) : name;
+  map_[name] = mw.packed();
+  map_[stem + ".marlin_packed"] = mw.packed();
+  map_[stem + ".marlin_scales"] = mw.scales();
+}
+
+bool Weights::find_marlin(const std::string &name, const Tensor **packed, const Tensor **scales) const {
+  const std::string suffix = ".weight";
+  const bool has = name.size() >= suffix.size() && name.compare(name.size() - suffix.size(), suffix.size(), suffix) == 0;
+  const std::string stem = has ? name.substr(0, name.size() - suffix.size()) : name;
+  auto get = [&](const std::string &key, bool want_u32) -> const Tensor * {
+    auto it = map_.find(key);
+    if (it == map_.end() || (want_u32 && it->second.dtype() != DType::U32)) return nullptr;
+    return &it->second;
+  };
+  const Tensor *p = nullptr;
+  for (const std::string &key : {name + ".marlin_packed", stem + ".marlin_packed", name + ".packed", stem + ".packed"})
+    if (!p) p = get(key, false);
+  if (!p) p = get(name, true);
+  if (!p) p = get(stem, true);
+  if (!p) return false;
+  const Tensor *sc = nullptr;
+  for (const std::string &key : {name + ".marlin_scales", stem + ".marlin_scales", name + ".scales", stem + ".scales",
+                                 name + ".scale", stem + ".scale", name + ".weight.scale", stem + ".weight.scale"})
+    if (!sc) sc = get(key, false);
+  if (!sc) return false;
+  *packed = p;
+  *scales = sc;
+  return true;
+}
+
 Tensor Weights::linear(const Tensor &x, const std::string &name) const {
   auto q = q_map_.find(name);
   if (q != q_map_.end()) return q->second->forward(x);
+  const Tensor *packed = nullptr, *scales = nullptr;
+  if (find_marlin(name, &packed, &scales)) {
+    // linear_layer.rs:53-63: in_dim comes from x, checked against the
+    // number of packed chunks.
+    const size_t x_in = x.dims().empty() ? 0 : x.dims().back();
+    const size_t out_dim = scales->elem_count();
+    const size_t k_chunks = packed->dims().size() >= 2 ? packed->dim(0) : (x_in + 31) / 32;
+    const size_t max_k = k_chunks * 32, min_k = k_chunks > 1 ? (k_chunks - 1) * 32 : 0;
+    if (x_in > max_k || (k_chunks > 1 && x_in <= min_k)) throw ModelError::shape(name, {max_k}, x.dims());
+    return substrate_->marlin_gemv(x, MarlinWeight::create(*packed, *scales, x_in, out_dim));
+  }
   return linear_dense(x, name);
 }
 
 Tensor Weights::linear_dense(const Tensor &x, const std::string &name) const {
+  const Tensor *packed = nullptr, *scales = nullptr;
+  if (find_marlin(name, &packed, &scales)) {  // linear_layer.rs:69-74
+    const size_t x_in = x.dims().empty() ? 0 : x.dims().back();
+    return substrate_->marlin_gemv(x, MarlinWeight::create(*packed, *scales, x_in, scales->elem_count()));
+  }
   const Tensor &w = get_raw(name);
   if (w.dtype() == DType::F8E4M3 || w.dtype() == DType::U8) {
     // scale lookup order of linear_layer.rs:79-85; absent = ones

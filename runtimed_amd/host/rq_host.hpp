@@ -7,8 +7,10 @@
 //   Weights             crates/runtimed-model/src/weights/store.rs:12-166,
 //                       linear_layer.rs:45-105, load_gguf.rs:40-120
 //   Fp8Weight           crates/runtimed-model/src/weights/fp8_weight.rs:9-97
+//   MarlinWeight        crates/runtimed-model/src/ops/marlin_gemv.rs:11-202
 //   SubstratePort /
-//   HipSubstrate        crates/runtimed-model/src/substrate/port.rs:14-77 (fp8_gemm)
+//   HipSubstrate        crates/runtimed-model/src/substrate/port.rs:14-77 (fp8_gemm,
+//                       marlin_gemv)
 //   ModelError/GgufError crates/runtimed-model/src/error.rs:5-27,
 //                       crates/runtimed-gguf/src/error.rs:3-37
 //
@@ -130,11 +132,33 @@ class QMatMul {
   int device_, qtype_;
 };
 
-// SubstratePort (port.rs:14-77), the FP8 entry only.
+// MarlinWeight (marlin_gemv.rs:11-63): packed U32 [ceil(in_dim/32), out_dim, 4],
+// scales [out_dim] or [out_dim, 1] (F32 here).
+class MarlinWeight {
+ public:
+  static MarlinWeight create(Tensor packed, Tensor scales, size_t in_dim, size_t out_dim);
+  size_t resident_bytes() const;
+  Tensor dequantize(void *stream = nullptr) const;  // [out_dim, in_dim] f32
+  const Tensor &packed() const { return packed_; }
+  const Tensor &scales() const { return scales_; }
+  size_t in_dim() const { return in_dim_; }
+  size_t out_dim() const { return out_dim_; }
+
+ private:
+  Tensor packed_, scales_;
+  size_t in_dim_ = 0, out_dim_ = 0;
+};
+
+// repack_marlin_tiles (marlin_gemv.rs:66-97), run on the weight's device.
+MarlinWeight repack_marlin_tiles(const Tensor &weight, const Tensor &scales, void *stream = nullptr);
+
+// SubstratePort (port.rs:14-77): the FP8 and Marlin entries.
 class SubstratePort {
  public:
   virtual ~SubstratePort() = default;
   virtual Tensor fp8_gemm(const Tensor &x, const Tensor &w, const Tensor *scale) const = 0;
+  // marlin_gemv (marlin_gemv.rs:119-202): x @ (w * scale)^T in x's dtype.
+  virtual Tensor marlin_gemv(const Tensor &x, const MarlinWeight &w) const = 0;
 };
 
 // librq behind the port: x is encoded with the reference's unscaled e4m3
@@ -145,6 +169,7 @@ class HipSubstrate : public SubstratePort {
   explicit HipSubstrate(bool per_token = false, void *stream = nullptr)
       : per_token_(per_token), stream_(stream) {}
   Tensor fp8_gemm(const Tensor &x, const Tensor &w, const Tensor *scale) const override;
+  Tensor marlin_gemv(const Tensor &x, const MarlinWeight &w) const override;
 
  private:
   bool per_token_;
@@ -186,6 +211,8 @@ class Weights {
   // embed_layer.rs:59-84: the same rows as [ids.size(), hidden].
   Tensor candidate_weights(const std::string &name, const std::vector<uint32_t> &ids) const;
   const Tensor &get_raw(const std::string &name) const;                 // store.rs:103-107
+  // linear_layer.rs:17-22: registers packed and scales under the name's stem.
+  void insert_marlin(const std::string &name, const MarlinWeight &mw);
   std::shared_ptr<QMatMul> q_matmul(const std::string &name) const;
   size_t resident_bytes() const;                                         // store.rs:57-76
   bool contains_key(const std::string &name) const;
@@ -193,6 +220,9 @@ class Weights {
   void set_substrate(std::shared_ptr<SubstratePort> s) { substrate_ = std::move(s); }
 
  private:
+  // linear_layer.rs:24-42: the packed / scales pair under any of the
+  // reference's key spellings, or null.
+  bool find_marlin(const std::string &name, const Tensor **packed, const Tensor **scales) const;
   int device_ = 0;
   std::unordered_map<std::string, Tensor> map_;
   std::unordered_map<std::string, std::shared_ptr<QMatMul>> q_map_;

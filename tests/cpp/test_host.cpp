@@ -347,6 +347,45 @@ static void gpu_tests() {
     auto vals = weights2.linear(x, "w").to_vec<float>();
     for (int i = 0; i < 16; ++i) CHECK(std::fabs(vals[i] - 16.0f * sv[i]) < 1e-1f);
   });
+  run("marlin_gemv_matches_dequant", [] {  // marlin_gemv.rs:209-222
+    const float wv[8] = {1.0f, -2.0f, 3.0f, 0.0f, 0.5f, 1.5f, -0.5f, 2.0f};
+    const float sv[2] = {0.5f, 0.25f};
+    auto w = Tensor::from_host(wv, {2, 4}, DType::F32, 0);
+    auto sc = Tensor::from_host(sv, {2}, DType::F32, 0);
+    auto mw = repack_marlin_tiles(w, sc);
+    CHECK(mw.resident_bytes() == (2 * 4) * 4 + 2 * 4);
+    uint32_t want[8];
+    rqo_marlin_repack(wv, sv, 2, 4, want);
+    auto got = mw.packed().to_vec<uint32_t>();
+    CHECK(got.size() == 8 && std::memcmp(got.data(), want, sizeof(want)) == 0);
+    const float xv[4] = {2.0f, 1.0f, -1.0f, 3.0f};
+    auto x = Tensor::from_host(xv, {1, 4}, DType::F32, 0);
+    auto y = HipSubstrate().marlin_gemv(x, mw).to_vec<float>();
+    auto deq = mw.dequantize().to_vec<float>();
+    for (int r = 0; r < 2; ++r) {
+      float e = 0.0f;
+      for (int k = 0; k < 4; ++k) e += xv[k] * deq[r * 4 + k];
+      CHECK(std::fabs(y[r] - e) < 1e-4f);
+    }
+    CHECK(y[0] == -3.0f && y[1] == 8.25f);
+  });
+  run("linear_marlin", [] {  // linear_layer.rs:143-160
+    const float wv[8] = {1, 2, 3, 4, 2, 3, 4, 5};
+    const float ones[80] = {1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1,
+                            1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1,
+                            1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1};
+    auto mw = repack_marlin_tiles(Tensor::from_host(wv, {2, 4}, DType::F32, 0),
+                                  Tensor::from_host(ones, {2}, DType::F32, 0));
+    auto weights = Weights::from_parts(0, {});
+    weights.insert_marlin("blk.0.attn_q", mw);
+    auto y = weights.linear(Tensor::from_host(ones, {1, 4}, DType::F32, 0), "blk.0.attn_q.weight");
+    CHECK((y.dims() == std::vector<size_t>{1, 2}));
+    auto v = y.to_vec<float>();
+    CHECK(v[0] == 10.0f && v[1] == 14.0f);
+    auto bad = Tensor::from_host(ones, {1, 80}, DType::F32, 0);
+    auto e = expect_throw<ModelError>([&] { weights.linear(bad, "blk.0.attn_q.weight"); });
+    CHECK(e.kind == ModelError::Shape);
+  });
   run("cuda_fp8_gemm_runs_or_skips", [] {  // fp8_gemm.rs:209-230
     std::vector<uint8_t> xb(16 * 16, 0x38), wb(16 * 16, 0x38);
     std::vector<float> sv(16);
