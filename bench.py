@@ -341,6 +341,54 @@ def extra_kv(torch, rq, dev, steps, warmup):
     return {"workload": "KV block quantizer [1, 8, 4096, 128] bf16 <-> fp8 / int8 codes, per-head scales", **res}
 
 
+def extra_upload(torch, rq, synth, dev):
+    """GGUF upload: the tensors of 8 Q4_K_M layers of the prefill model
+    (hidden 2048, FFN 8192; q/k/o/gate/up Q4_K, v/down Q6_K) and its Q6_K
+    262144x2048 output head, written back to back into a file, memory-mapped
+    (pages populated), and turned into device handles with rq_weight_create
+    (pinned double-buffered DMA, Q6_K split on the device).  The file is in the page cache (just written), as after a warm
+    start; disk read time is not part of the figure."""
+    import mmap
+    import tempfile
+    import time
+
+    import numpy as np
+
+    layer = [(rq.Q4_K, 2048, 2048)] * 3 + [(rq.Q6_K, 2048, 2048), (rq.Q4_K, 8192, 2048),
+                                           (rq.Q4_K, 8192, 2048), (rq.Q6_K, 2048, 8192)]
+    tensors = layer * 8 + [(rq.Q6_K, 262144, 2048)]
+    tmpdir = "/dev/shm" if os.path.isdir("/dev/shm") else tempfile.gettempdir()
+    fd, path = tempfile.mkstemp(suffix=".gguf.bin", dir=tmpdir)
+    try:
+        offs, total = [], 0
+        cache = {}
+        with os.fdopen(fd, "wb") as f:
+            for qt, n, k in tensors:
+                key = (qt, n, k)
+                if key not in cache:
+                    cache[key] = synth.weight_blocks(qt, 21, n, k)
+                f.write(cache[key].tobytes())
+                offs.append(total)
+                total += cache[key].nbytes
+        del cache
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        # mapped read-only with populated pages, as GgufFile::open maps a model
+        with open(path, "rb") as f:
+            mapping = mmap.mmap(f.fileno(), 0, flags=mmap.MAP_PRIVATE | mmap.MAP_POPULATE, prot=mmap.PROT_READ)
+        mm = np.frombuffer(mapping, dtype=np.uint8)
+        W = [rq.QWeight(qt, mm[o:o + n * k // rq.GEOMETRY[qt][0] * rq.GEOMETRY[qt][1]], n, k)
+             for (qt, n, k), o in zip(tensors, offs)]
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        del W, mm
+        mapping.close()
+    finally:
+        os.unlink(path)
+    return {"workload": "GGUF upload, 8 Q4_K_M layers (2048/8192) + Q6_K 262144x2048 head, page-cache file",
+            "bytes": total, "tensors": len(tensors), "s": round(dt, 4), "GB/s": round(total / dt / 1e9, 2)}
+
+
 def mode_gate(torch, rq, synth, dev, steps, warmup, eager=False):
     """Only the dominant kernel: R distinct 4864x896 Q4_K gate weights
     (R * 2.45 MB >= 1 GB), one GEMV each, in one HIP graph (or launched
@@ -455,7 +503,8 @@ def main():
                          ("prefill", lambda: extra_prefill(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("fp8_gemm", lambda: extra_fp8(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("marlin_int4_gemv", lambda: extra_marlin(torch, rq, dev, args.steps, args.warmup)),
-                         ("kv_quantizer", lambda: extra_kv(torch, rq, dev, args.steps, args.warmup))):
+                         ("kv_quantizer", lambda: extra_kv(torch, rq, dev, args.steps, args.warmup)),
+                         ("gguf_upload", lambda: extra_upload(torch, rq, synth, dev))):
             log(f"extra: {name}")
             try:
                 extra[name] = fn()

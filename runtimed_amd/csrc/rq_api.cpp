@@ -63,8 +63,17 @@ static int stream_checks(int qtype, uint64_t nbytes, uint64_t n_elements, Geomet
 
 static uint64_t align256(uint64_t v) { return (v + 255) & ~(uint64_t)255; }
 
+// Device bytes of the split layout (rq_internal.h) for nblocks blocks, and
+// the offset of its scale array.
+static uint64_t split_size(int qtype, uint64_t nblocks, uint64_t *aux_off) {
+  const uint64_t qbytes = qtype == RQ_Q8_0 ? 32 : qtype == RQ_Q6_K ? 208 : 16;
+  const uint64_t abytes = qtype == RQ_Q5_0 ? 8 : 2;
+  *aux_off = align256(nblocks * qbytes);
+  return *aux_off + nblocks * abytes;
+}
+
 // Host-side split of Q8_0 / Q6_K streams into the aligned device layout
-// described in rq_internal.h.
+// described in rq_internal.h (small tensors; large ones split on the device).
 static void split_layout(int qtype, const uint8_t *src, uint64_t nblocks, std::vector<uint8_t> &dst,
                          uint64_t &aux_off) {
   if (qtype == RQ_Q8_0) {
@@ -128,17 +137,28 @@ int rq_weight_create(int qtype, const void *host_blocks, size_t nbytes, int64_t 
   if (rc) return rc;
   const uint64_t nblocks = count / (uint64_t)g.elems;
   const uint8_t *src = static_cast<const uint8_t *>(host_blocks);
-  std::vector<uint8_t> staged;
-  uint64_t aux_off = 0, bytes = nblocks * (uint64_t)g.bytes;
-  if (qtype == RQ_Q8_0 || qtype == RQ_Q6_K || qtype == RQ_Q4_0 || qtype == RQ_Q5_0) {
-    split_layout(qtype, src, nblocks, staged, aux_off);
-    src = staged.data();
-    bytes = staged.size();
-  }
+  const bool split = qtype == RQ_Q8_0 || qtype == RQ_Q6_K || qtype == RQ_Q4_0 || qtype == RQ_Q5_0;
+  const uint64_t raw_bytes = nblocks * (uint64_t)g.bytes;
+  uint64_t aux_off = 0, bytes = raw_bytes;
   uint8_t *dptr = nullptr;
-  rc = hip_check(hipMalloc(reinterpret_cast<void **>(&dptr), bytes), "hipMalloc");
-  if (rc) return rc;
-  rc = hip_check(hipMemcpy(dptr, src, bytes, hipMemcpyHostToDevice), "hipMemcpy");
+  if (raw_bytes >= (4ull << 20)) {
+    // Large tensors: pinned double-buffered DMA, split on the device.
+    if (split) bytes = split_size(qtype, nblocks, &aux_off);
+    rc = hip_check(hipMalloc(reinterpret_cast<void **>(&dptr), bytes), "hipMalloc");
+    if (rc) return rc;
+    if (split) rc = hip_check(hipMemset(dptr, 0, bytes), "hipMemset");
+    if (!rc) rc = upload_blocks(qtype, src, nblocks, g.bytes, dptr, aux_off, device);
+  } else {
+    std::vector<uint8_t> staged;
+    if (split) {
+      split_layout(qtype, src, nblocks, staged, aux_off);
+      src = staged.data();
+      bytes = staged.size();
+    }
+    rc = hip_check(hipMalloc(reinterpret_cast<void **>(&dptr), bytes), "hipMalloc");
+    if (rc) return rc;
+    rc = hip_check(hipMemcpy(dptr, src, bytes, hipMemcpyHostToDevice), "hipMemcpy");
+  }
   if (rc) {
     (void)hipFree(dptr);
     return rc;

@@ -61,6 +61,11 @@ bool geometry(int qtype, Geometry *g);
 int set_error(int code, const char *fmt, ...);
 hipStream_t as_stream(void *s);
 
+// Host-to-device upload of nblocks GGUF blocks into a handle's layout
+// (pinned double-buffered DMA; split layouts scattered on the device).
+int upload_blocks(int qtype, const uint8_t *src, uint64_t nblocks, int bbytes, uint8_t *dptr, uint64_t aux_off,
+                  int device);
+
 // ---- launchers (each returns RQ_OK or an error code and message) ----
 int launch_dequant_weight(const rq_weight *w, float *out, hipStream_t s);
 // Rows dev_ids[0 .. n_ids) of a handle (every id < n, k % 4 == 0) as f32.

@@ -3,6 +3,11 @@
 
 #include <hip/hip_runtime.h>
 
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
 #include <cstring>
 #include <fstream>
 #include <iterator>
@@ -54,11 +59,12 @@ bool librq_decodes(uint32_t t) { return t == 2 || t == 6 || t == 8 || t == 12 ||
 
 // Cursor over the mapped bytes (header.rs:41-107).
 struct Cursor {
-  const std::vector<uint8_t> &b;
+  const uint8_t *data;
+  size_t size;
   size_t pos = 0;
   const uint8_t *take(size_t n) {
-    if (n > b.size() - pos || pos > b.size()) throw GgufError(GgufError::Truncated, "truncated file at offset " + std::to_string(pos));
-    const uint8_t *p = b.data() + pos;
+    if (n > size - pos || pos > size) throw GgufError(GgufError::Truncated, "truncated file at offset " + std::to_string(pos));
+    const uint8_t *p = data + pos;
     pos += n;
     return p;
   }
@@ -179,17 +185,41 @@ std::vector<uint8_t> Tensor::to_host() const {
 
 // ---------------------------------------------------------------- GgufFile --
 
+// The file is memory-mapped read-only (as header.rs maps it) with its pages
+// populated up front, so tensor bytes go to the upload without a copy.
 GgufFile GgufFile::open(const std::string &path) {
-  std::ifstream f(path, std::ios::binary);
-  if (!f) throw GgufError(GgufError::Io, "io: cannot open " + path);
-  std::vector<uint8_t> b((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
-  return parse(std::move(b));
+  const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+  if (fd < 0) throw GgufError(GgufError::Io, "io: cannot open " + path);
+  struct stat st;
+  if (fstat(fd, &st) != 0) {
+    ::close(fd);
+    throw GgufError(GgufError::Io, "io: cannot stat " + path);
+  }
+  const size_t size = (size_t)st.st_size;
+  if (size == 0) {
+    ::close(fd);
+    return parse(std::vector<uint8_t>());
+  }
+  void *p = mmap(nullptr, size, PROT_READ, MAP_PRIVATE | MAP_POPULATE, fd, 0);
+  ::close(fd);
+  if (p == MAP_FAILED) throw GgufError(GgufError::Io, "io: cannot map " + path);
+  std::shared_ptr<const uint8_t> data(static_cast<const uint8_t *>(p), [size](const uint8_t *q) {
+    munmap(const_cast<uint8_t *>(q), size);
+  });
+  return parse_view(std::move(data), size);
 }
 
 GgufFile GgufFile::parse(std::vector<uint8_t> bytes) {
+  auto owned = std::make_shared<std::vector<uint8_t>>(std::move(bytes));
+  std::shared_ptr<const uint8_t> data(owned, owned->data());
+  return parse_view(std::move(data), owned->size());
+}
+
+GgufFile GgufFile::parse_view(std::shared_ptr<const uint8_t> data, size_t size) {
   GgufFile g;
-  g.bytes_ = std::move(bytes);
-  Cursor cur{g.bytes_};
+  g.data_ = std::move(data);
+  g.size_ = size;
+  Cursor cur{g.data_.get(), g.size_};
   if (std::memcmp(cur.take(4), "GGUF", 4) != 0) throw GgufError(GgufError::BadMagic, "bad magic: not a GGUF file");
   const uint32_t version = cur.get<uint32_t>();
   if (version != 3) throw GgufError(GgufError::Version, "unsupported GGUF version: " + std::to_string(version) + " (want 3)");
@@ -227,7 +257,7 @@ GgufFile GgufFile::parse(std::vector<uint8_t> bytes) {
       n *= d;
     }
     const uint64_t off = data_start + r.off;
-    if (off < data_start || off > g.bytes_.size()) throw GgufError(GgufError::Range, "tensor '" + r.name + "': byte range out of bounds");
+    if (off < data_start || off > g.size_) throw GgufError(GgufError::Range, "tensor '" + r.name + "': byte range out of bounds");
     g.tensors.push_back(TensorInfo{r.name, r.dims, r.dtype, off, n});
   }
   return g;
@@ -245,9 +275,9 @@ const uint8_t *GgufFile::tensor_bytes(const TensorInfo &info, size_t *len) const
   const size_t blocks = (info.n_elements + elems - 1) / elems;
   if (blocks > SIZE_MAX / bb) throw GgufError(GgufError::Overflow, "tensor '" + info.name + "': element count overflows");
   const size_t n = blocks * bb;
-  if (info.offset > bytes_.size() || n > bytes_.size() - info.offset) throw GgufError(GgufError::Range, "tensor '" + info.name + "': byte range out of bounds");
+  if (info.offset > size_ || n > size_ - info.offset) throw GgufError(GgufError::Range, "tensor '" + info.name + "': byte range out of bounds");
   *len = n;
-  return bytes_.data() + info.offset;
+  return data_.get() + info.offset;
 }
 
 // ----------------------------------------------------------------- QMatMul --

@@ -108,7 +108,9 @@ class GgufFile {
   uint64_t alignment = 32;
 
  private:
-  std::vector<uint8_t> bytes_;
+  static GgufFile parse_view(std::shared_ptr<const uint8_t> data, size_t size);
+  std::shared_ptr<const uint8_t> data_;  // the mapped file (or parsed buffer)
+  size_t size_ = 0;
 };
 
 // The quantized q_map value: a librq weight handle behind shared ownership

@@ -31,6 +31,24 @@ def test_handle_dequant_bit_exact(dev, qtype, n, k):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("qtype,mbytes", [(q, 5) for q in ALL] + [(rq.Q8_0, 140), (rq.Q4_K, 140), (rq.Q6_K, 140),
+                                                                   (rq.Q5_0, 70)])
+def test_large_upload_bit_exact(dev, qtype, mbytes):
+    # at least 4 MB of blocks take the staged upload (pinned double-buffered
+    # DMA, split on the device); more than 64 MB spans several staging chunks
+    elems, bb = rq.GEOMETRY[qtype]
+    k = 4096
+    n = (mbytes << 20) // (k // elems * bb) + 1
+    print(f"upload qtype={qtype} n={n} k={k} bytes={n * k // elems * bb}", flush=True)
+    data = synth.random_bytes(91 + qtype + mbytes, n * k // elems * bb)
+    w = rq.QWeight(qtype, data, n, k)
+    got = w.dequantize().cpu().numpy().reshape(-1)
+    rc, want = oracle.dequant_tensor(qtype, data, n * k, threads=8)
+    assert rc == 0
+    bits_equal(got, want)
+    assert w.info()["gguf_bytes"] == n * k // elems * bb
+
+
 @pytest.mark.parametrize("qtype", ALL)
 def test_handle_dequant_random_bytes(dev, qtype):
     # every byte random: f16 scales include subnormals, infinities and NaNs
