@@ -48,13 +48,13 @@ __device__ __forceinline__ void load_run(const void *x, int xtype, int64_t idx, 
 struct FmtQ4K {
   static constexpr int PE = 32;    // elements per piece
   static constexpr int RUNS = 2;   // runs of 16 activations
-  __device__ static int64_t run_off(int p, int r) { return 64 * (p >> 1) + 16 * (p & 1) + 32 * r; }
+  __device__ __forceinline__ static int64_t run_off(int p, int r) { return 64 * (p >> 1) + 16 * (p & 1) + 32 * r; }
 
   struct Piece {
     uint4 hd, qv;
     int c;
   };
-  __device__ static Piece load(const uint8_t *w, const uint8_t *, int64_t row, int64_t k, int p) {
+  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *, int64_t row, int64_t k, int p) {
     const uint64_t e = (uint64_t)row * (uint64_t)k + 64u * (uint64_t)(p >> 1);
     const uint8_t *bp = w + (e >> 8) * 144u;
     Piece pc;
@@ -65,7 +65,7 @@ struct FmtQ4K {
   }
   // (d*sc, dmin*m) for sub-blocks 2c (low nibbles) and 2c+1 (high nibbles):
   // scale_min_k4 (dequant_k.rs:8-16) on the packed bytes in hd.y/z/w.
-  __device__ static void scales(const Piece &pc, float &a0, float &b0, float &a1, float &b1) {
+  __device__ __forceinline__ static void scales(const Piece &pc, float &a0, float &b0, float &a1, float &b1) {
     const int sh = 16 * (pc.c & 1);
     const uint32_t Y = pc.hd.y >> sh, Z = pc.hd.z >> sh, W = pc.hd.w >> sh;
     uint32_t sc0, m0, sc1, m1;
@@ -87,7 +87,7 @@ struct FmtQ4K {
     b1 = dmin * (float)m1;
   }
   // M=1: sum over the piece of W*x with the activations in registers.
-  __device__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
+  __device__ __forceinline__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
     float a0, b0, a1, b1;
     scales(pc, a0, b0, a1, b1);
     const uint32_t q[4] = {pc.qv.x, pc.qv.y, pc.qv.z, pc.qv.w};
@@ -111,7 +111,7 @@ struct FmtQ4K {
   // 2j, 2j + 1 of run r) for the MFMA GEMM: one fused multiply-add per
   // weight (a single rounding, then the bf16 rounding), not the exact
   // two-rounding value of decode().
-  __device__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
+  __device__ __forceinline__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
     float a0, b0, a1, b1;
     scales(pc, a0, b0, a1, b1);
     const uint32_t q[4] = {pc.qv.x, pc.qv.y, pc.qv.z, pc.qv.w};
@@ -125,7 +125,7 @@ struct FmtQ4K {
     }
   }
   // Exact dequantized weights of the piece, in run order.
-  __device__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
+  __device__ __forceinline__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
     float a0, b0, a1, b1;
     scales(pc, a0, b0, a1, b1);
     const uint32_t q[4] = {pc.qv.x, pc.qv.y, pc.qv.z, pc.qv.w};
@@ -143,7 +143,7 @@ struct FmtQ4K {
 struct FmtQ6K {
   static constexpr int PE = 64;
   static constexpr int RUNS = 4;
-  __device__ static int64_t run_off(int p, int r) { return 128 * (p >> 1) + 16 * (p & 1) + 32 * r; }
+  __device__ __forceinline__ static int64_t run_off(int p, int r) { return 128 * (p >> 1) + 16 * (p & 1) + 32 * r; }
 
   struct Piece {
     uint4 a, b, h;
@@ -151,7 +151,7 @@ struct FmtQ6K {
     uint32_t d;
     int s;
   };
-  __device__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
+  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
     const uint64_t e = (uint64_t)row * (uint64_t)k + 128u * (uint64_t)(p >> 1);
     const uint64_t blk = e >> 8;
     const int hf = (int)((e >> 7) & 1u), s = p & 1;
@@ -166,7 +166,7 @@ struct FmtQ6K {
     return pc;
   }
   // Unsigned 6-bit codes (q + 32) of run r for dword j.
-  __device__ static uint32_t codes(const Piece &pc, int r, int j) {
+  __device__ __forceinline__ static uint32_t codes(const Piece &pc, int r, int j) {
     const uint32_t a = (&pc.a.x)[j], b = (&pc.b.x)[j], h = (&pc.h.x)[j];
     switch (r) {
       case 0: return (a & 0x0F0F0F0Fu) | ((h & 0x03030303u) << 4);
@@ -176,12 +176,12 @@ struct FmtQ6K {
     }
   }
   // int8 scale of run r: scales[8*hf + s + 2r] (dequant_k.rs:107).
-  __device__ static float scale(const Piece &pc, int r) {
+  __device__ __forceinline__ static float scale(const Piece &pc, int r) {
     const int byte = pc.s + 2 * r;
     const uint32_t word = byte < 4 ? pc.sc.x : pc.sc.y;
     return (float)(int8_t)((word >> (8 * (byte & 3))) & 0xFFu);
   }
-  __device__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
+  __device__ __forceinline__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
     float acc = 0.0f;
 #pragma unroll
     for (int r = 0; r < RUNS; ++r) {
@@ -198,7 +198,7 @@ struct FmtQ6K {
     }
     return h2f(pc.d) * acc;
   }
-  __device__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
+  __device__ __forceinline__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
     const float d = h2f(pc.d);
 #pragma unroll
     for (int r = 0; r < RUNS; ++r) {
@@ -219,13 +219,13 @@ struct FmtQ6K {
 struct FmtQ8 {
   static constexpr int PE = 32;
   static constexpr int RUNS = 2;
-  __device__ static int64_t run_off(int p, int r) { return 64 * (p >> 1) + 16 * (p & 1) + 32 * r; }
+  __device__ __forceinline__ static int64_t run_off(int p, int r) { return 64 * (p >> 1) + 16 * (p & 1) + 32 * r; }
 
   struct Piece {
     uint4 q[2];
     uint32_t d[2];
   };
-  __device__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
+  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
     Piece pc;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
@@ -235,7 +235,7 @@ struct FmtQ8 {
     }
     return pc;
   }
-  __device__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
+  __device__ __forceinline__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
     float acc = 0.0f;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
@@ -253,7 +253,7 @@ struct FmtQ8 {
     }
     return acc;
   }
-  __device__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
+  __device__ __forceinline__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const float d = h2f(pc.d[r]);
@@ -265,7 +265,7 @@ struct FmtQ8 {
       }
     }
   }
-  __device__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
+  __device__ __forceinline__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const float d = h2f(pc.d[r]);
@@ -285,13 +285,13 @@ struct FmtQ8 {
 struct FmtQ5K {
   static constexpr int PE = 32;
   static constexpr int RUNS = 2;
-  __device__ static int64_t run_off(int p, int r) { return 64 * (p >> 1) + 16 * (p & 1) + 32 * r; }
+  __device__ __forceinline__ static int64_t run_off(int p, int r) { return 64 * (p >> 1) + 16 * (p & 1) + 32 * r; }
 
   struct Piece {
     uint4 hd, qv, hv;
     int c;
   };
-  __device__ static Piece load(const uint8_t *w, const uint8_t *, int64_t row, int64_t k, int p) {
+  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *, int64_t row, int64_t k, int p) {
     const uint64_t e = (uint64_t)row * (uint64_t)k + 64u * (uint64_t)(p >> 1);
     const uint8_t *bp = w + (e >> 8) * 176u;
     Piece pc;
@@ -301,19 +301,19 @@ struct FmtQ5K {
     pc.hv = *reinterpret_cast<const uint4 *>(bp + 16 + 16 * (p & 1));
     return pc;
   }
-  __device__ static void scales(const Piece &pc, float &a0, float &b0, float &a1, float &b1) {
+  __device__ __forceinline__ static void scales(const Piece &pc, float &a0, float &b0, float &a1, float &b1) {
     FmtQ4K::Piece q4;
     q4.hd = pc.hd;
     q4.c = pc.c;
     FmtQ4K::scales(q4, a0, b0, a1, b1);
   }
   // 5-bit codes of dword j: run 0 (low nibbles | bit 2c), run 1 (high | bit 2c + 1).
-  __device__ static void codes(const Piece &pc, int j, uint32_t &c0, uint32_t &c1) {
+  __device__ __forceinline__ static void codes(const Piece &pc, int j, uint32_t &c0, uint32_t &c1) {
     const uint32_t q = (&pc.qv.x)[j], h = (&pc.hv.x)[j] >> (2 * pc.c);
     c0 = (q & 0x0F0F0F0Fu) | ((h << 4) & 0x10101010u);
     c1 = ((q >> 4) & 0x0F0F0F0Fu) | ((h << 3) & 0x10101010u);
   }
-  __device__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
+  __device__ __forceinline__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
     float a0, b0, a1, b1;
     scales(pc, a0, b0, a1, b1);
     float dl[4], dh[4];
@@ -333,7 +333,7 @@ struct FmtQ5K {
     const float shh = (dh[0] + dh[1]) + (dh[2] + dh[3]);
     return (a0 * sl - b0 * sx[0]) + (a1 * shh - b1 * sx[1]);
   }
-  __device__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
+  __device__ __forceinline__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
     float a0, b0, a1, b1;
     scales(pc, a0, b0, a1, b1);
 #pragma unroll
@@ -347,7 +347,7 @@ struct FmtQ5K {
     }
   }
   // Exact weights: d1 * (q + hi) - m1 (dequant_k.rs:67-73).
-  __device__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
+  __device__ __forceinline__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
     float a0, b0, a1, b1;
     scales(pc, a0, b0, a1, b1);
 #pragma unroll
@@ -377,7 +377,7 @@ template <bool Q5>
 struct FmtQx0 {
   static constexpr int PE = 32;
   static constexpr int RUNS = 2;
-  __device__ static int64_t run_off(int p, int r) { return 64 * (p >> 1) + 16 * (p & 1) + 32 * r; }
+  __device__ __forceinline__ static int64_t run_off(int p, int r) { return 64 * (p >> 1) + 16 * (p & 1) + 32 * r; }
 
   struct Piece {
     uint4 q[2];
@@ -385,7 +385,7 @@ struct FmtQx0 {
     uint32_t d[2];
     int h;
   };
-  __device__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
+  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
     Piece pc;
     pc.h = p & 1;
 #pragma unroll
@@ -404,13 +404,13 @@ struct FmtQx0 {
     return pc;
   }
   // Unsigned codes (q + 8, or q + 16 for Q5_0) of dword j of run r.
-  __device__ static uint32_t codes(const Piece &pc, int r, int j) {
+  __device__ __forceinline__ static uint32_t codes(const Piece &pc, int r, int j) {
     const uint32_t q = ((&pc.q[r].x)[j] >> (4 * pc.h)) & 0x0F0F0F0Fu;
     if (!Q5) return q;
     return q | (spread4(pc.qh[r] >> (16 * pc.h + 4 * j)) << 4);
   }
   static constexpr float ZERO = Q5 ? 16.0f : 8.0f;
-  __device__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
+  __device__ __forceinline__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
     float acc = 0.0f;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
@@ -427,7 +427,7 @@ struct FmtQx0 {
     }
     return acc;
   }
-  __device__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
+  __device__ __forceinline__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const float d = h2f(pc.d[r]), z = -ZERO * d;
@@ -440,7 +440,7 @@ struct FmtQx0 {
     }
   }
   // Exact weights d * (q - 8) or d * (q - 16).
-  __device__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
+  __device__ __forceinline__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const float d = h2f(pc.d[r]);
@@ -462,7 +462,7 @@ struct FmtQx0 {
 struct FmtQ6KG {
   static constexpr int PE = 32;
   static constexpr int RUNS = 2;
-  __device__ static int64_t run_off(int p, int r) { return 64 * (p >> 1) + 16 * (p & 1) + 32 * r; }
+  __device__ __forceinline__ static int64_t run_off(int p, int r) { return 64 * (p >> 1) + 16 * (p & 1) + 32 * r; }
 
   struct Piece {
     uint4 a, b, h;
@@ -470,7 +470,7 @@ struct FmtQ6KG {
     uint32_t d;
     int ch;
   };
-  __device__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
+  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
     const uint64_t e = (uint64_t)row * (uint64_t)k + 64u * (uint64_t)(p >> 1);
     const uint64_t blk = e >> 8;
     const int hf = (int)((e >> 7) & 1u), hh = p & 1;
@@ -485,7 +485,7 @@ struct FmtQ6KG {
     pc.d = reinterpret_cast<const uint16_t *>(aux)[blk];
     return pc;
   }
-  __device__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
+  __device__ __forceinline__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
     const float d = h2f(pc.d);
     const float ds0 = d * (float)(int8_t)(pc.sc & 0xFFu);
     const float ds1 = d * (float)(int8_t)((pc.sc >> 16) & 0xFFu);
@@ -502,7 +502,7 @@ struct FmtQ6KG {
       o[8 + 2 * j + 1] = pk_bf16(fmaf(ub(q1, 2), ds1, z1), fmaf(ub(q1, 3), ds1, z1));
     }
   }
-  __device__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
+  __device__ __forceinline__ static void decode(const Piece &pc, float (&wv)[RUNS][16]) {
     const float d = h2f(pc.d);
     const float ds0 = d * (float)(int8_t)(pc.sc & 0xFFu);
     const float ds1 = d * (float)(int8_t)((pc.sc >> 16) & 0xFFu);
