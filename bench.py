@@ -413,6 +413,21 @@ def mode_gate(torch, rq, synth, dev, steps, warmup, eager=False):
                       "GB/s": round(b / (ms * 1e-3) / 1e9, 1)}), flush=True)
 
 
+def mode_gemv_large(torch, rq, synth, dev, steps):
+    """Only the Q4_K 14336x4096 M=1 GEMV over 16 distinct copies (eager, for
+    counters)."""
+    n, k, copies = 14336, 4096, 16
+    blocks = synth.q4_k_blocks(9, n * k // 256)
+    W = [rq.QWeight(rq.Q4_K, blocks, n, k) for _ in range(copies)]
+    x = torch.from_numpy(synth.activations(4, 1, k)).to(dev)
+    y = torch.empty((1, n), device=dev)
+    for _ in range(steps):
+        for w in W:
+            w.forward(x, out=y)
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "gemv-large", "launches": steps * copies}), flush=True)
+
+
 def mode_copy(torch, dev, steps):
     """A plain device copy of 512 MiB: the calibration kernel for HBM byte
     counters (FETCH_SIZE / WRITE_SIZE per dispatch vs. 512 MiB moved)."""
@@ -463,7 +478,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
-    ap.add_argument("--mode", choices=["full", "gate", "copy", "fp8", "prefill-head"], default="full",
+    ap.add_argument("--mode", choices=["full", "gate", "copy", "fp8", "prefill-head", "gemv-large"], default="full",
                     help="gate: only the dominant GEMV; copy: counter calibration copy")
     ap.add_argument("--eager", action="store_true", help="gate mode without a HIP graph")
     args = ap.parse_args()
@@ -487,6 +502,8 @@ def main():
         return mode_fp8(torch, rq, synth, dev, args.steps)
     if args.mode == "prefill-head":
         return mode_prefill_head(torch, rq, synth, dev, args.steps)
+    if args.mode == "gemv-large":
+        return mode_gemv_large(torch, rq, synth, dev, args.steps)
     log(f"decode workload: {args.layers} layer copies, steps={args.steps} warmup={args.warmup}")
     W, ms, gate_ms = decode_workload(torch, rq, synth, args.layers, args.steps, args.warmup, dev)
     step_bytes = layer_bytes() * args.layers

@@ -21,6 +21,15 @@ __device__ __forceinline__ float h2f(uint32_t bits) {
 
 __device__ __forceinline__ float ub(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xFFu); }
 
+// Returns v unchanged but hides how it was computed.  A word of four masked
+// codes (e.g. q & 0x0F0F0F0F) fed to ub() should become one
+// v_cvt_f32_ubyte{0..3} per code; seeing the mask, the optimizer instead
+// folds it into each extraction (a v_bfe_u32 plus a conversion per code).
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
 typedef __bf16 fmt_bf16x2 __attribute__((ext_vector_type(2)));
 typedef float fmt_f32x2 __attribute__((ext_vector_type(2)));
 
@@ -66,25 +75,19 @@ struct FmtQ4K {
   // (d*sc, dmin*m) for sub-blocks 2c (low nibbles) and 2c+1 (high nibbles):
   // scale_min_k4 (dequant_k.rs:8-16) on the packed bytes in hd.y/z/w.
   __device__ __forceinline__ static void scales(const Piece &pc, float &a0, float &b0, float &a1, float &b1) {
+    // Both sub-blocks at once, one per byte of a 16-bit pair; the two
+    // scale_min_k4 cases are computed side by side and selected (lanes of a
+    // wave usually hold different chunks c, and a branch would run both).
     const int sh = 16 * (pc.c & 1);
     const uint32_t Y = pc.hd.y >> sh, Z = pc.hd.z >> sh, W = pc.hd.w >> sh;
-    uint32_t sc0, m0, sc1, m1;
-    if (pc.c < 2) {
-      sc0 = Y & 63u;
-      m0 = Z & 63u;
-      sc1 = (Y >> 8) & 63u;
-      m1 = (Z >> 8) & 63u;
-    } else {
-      sc0 = (W & 0xFu) | ((Y >> 2) & 0x30u);
-      m0 = ((W >> 4) & 0xFu) | ((Z >> 2) & 0x30u);
-      sc1 = ((W >> 8) & 0xFu) | ((Y >> 10) & 0x30u);
-      m1 = ((W >> 12) & 0xFu) | ((Z >> 10) & 0x30u);
-    }
+    const bool low = pc.c < 2;
+    const uint32_t sc = opaque(low ? (Y & 0x3F3Fu) : ((W & 0x0F0Fu) | ((Y >> 2) & 0x3030u)));
+    const uint32_t mn = opaque(low ? (Z & 0x3F3Fu) : (((W >> 4) & 0x0F0Fu) | ((Z >> 2) & 0x3030u)));
     const float d = h2f(pc.hd.x), dmin = h2f(pc.hd.x >> 16);
-    a0 = d * (float)sc0;
-    b0 = dmin * (float)m0;
-    a1 = d * (float)sc1;
-    b1 = dmin * (float)m1;
+    a0 = d * ub(sc, 0);
+    b0 = dmin * ub(mn, 0);
+    a1 = d * ub(sc, 1);
+    b1 = dmin * ub(mn, 1);
   }
   // M=1: sum over the piece of W*x with the activations in registers.
   __device__ __forceinline__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
@@ -94,7 +97,7 @@ struct FmtQ4K {
     float dl[4], dh[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t lo = q[j] & 0x0F0F0F0Fu, hi = q[j] & 0xF0F0F0F0u;
+      const uint32_t lo = opaque(q[j] & 0x0F0F0F0Fu), hi = opaque(q[j] & 0xF0F0F0F0u);
       dl[j] = xv[0][4 * j] * ub(lo, 0);
       dh[j] = xv[1][4 * j] * ub(hi, 0);
 #pragma unroll
@@ -117,7 +120,7 @@ struct FmtQ4K {
     const uint32_t q[4] = {pc.qv.x, pc.qv.y, pc.qv.z, pc.qv.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t lo = q[j] & 0x0F0F0F0Fu, hi = (q[j] >> 4) & 0x0F0F0F0Fu;
+      const uint32_t lo = opaque(q[j] & 0x0F0F0F0Fu), hi = opaque((q[j] >> 4) & 0x0F0F0F0Fu);
       o[2 * j] = pk_bf16(fmaf(ub(lo, 0), a0, -b0), fmaf(ub(lo, 1), a0, -b0));
       o[2 * j + 1] = pk_bf16(fmaf(ub(lo, 2), a0, -b0), fmaf(ub(lo, 3), a0, -b0));
       o[8 + 2 * j] = pk_bf16(fmaf(ub(hi, 0), a1, -b1), fmaf(ub(hi, 1), a1, -b1));
@@ -188,7 +191,7 @@ struct FmtQ6K {
       float dd[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t q = codes(pc, r, j);
+        const uint32_t q = opaque(codes(pc, r, j));
         dd[j] = xv[r][4 * j] * ub(q, 0);
 #pragma unroll
         for (int b = 1; b < 4; ++b) dd[j] = fmaf(xv[r][4 * j + b], ub(q, b), dd[j]);
@@ -205,7 +208,7 @@ struct FmtQ6K {
       const float ds = d * scale(pc, r);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t q = codes(pc, r, j);
+        const uint32_t q = opaque(codes(pc, r, j));
 #pragma unroll
         for (int b = 0; b < 4; ++b) wv[r][4 * j + b] = ds * (ub(q, b) - 32.0f);
       }
@@ -243,7 +246,7 @@ struct FmtQ8 {
       float dd[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t u = q[j] ^ 0x80808080u;  // q + 128 as unsigned bytes
+        const uint32_t u = opaque(q[j] ^ 0x80808080u);  // q + 128 as unsigned bytes
         dd[j] = xv[r][4 * j] * ub(u, 0);
 #pragma unroll
         for (int b = 1; b < 4; ++b) dd[j] = fmaf(xv[r][4 * j + b], ub(u, b), dd[j]);
@@ -321,6 +324,8 @@ struct FmtQ5K {
     for (int j = 0; j < 4; ++j) {
       uint32_t c0, c1;
       codes(pc, j, c0, c1);
+      c0 = opaque(c0);
+      c1 = opaque(c1);
       dl[j] = xv[0][4 * j] * ub(c0, 0);
       dh[j] = xv[1][4 * j] * ub(c1, 0);
 #pragma unroll
@@ -340,6 +345,8 @@ struct FmtQ5K {
     for (int j = 0; j < 4; ++j) {
       uint32_t c0, c1;
       codes(pc, j, c0, c1);
+      c0 = opaque(c0);
+      c1 = opaque(c1);
       o[2 * j] = pk_bf16(fmaf(ub(c0, 0), a0, -b0), fmaf(ub(c0, 1), a0, -b0));
       o[2 * j + 1] = pk_bf16(fmaf(ub(c0, 2), a0, -b0), fmaf(ub(c0, 3), a0, -b0));
       o[8 + 2 * j] = pk_bf16(fmaf(ub(c1, 0), a1, -b1), fmaf(ub(c1, 1), a1, -b1));
@@ -354,6 +361,8 @@ struct FmtQ5K {
     for (int j = 0; j < 4; ++j) {
       uint32_t c0, c1;
       codes(pc, j, c0, c1);
+      c0 = opaque(c0);
+      c1 = opaque(c1);
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         wv[0][4 * j + b] = a0 * ub(c0, b) - b0;
@@ -417,7 +426,7 @@ struct FmtQx0 {
       float dd[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t c = codes(pc, r, j);
+        const uint32_t c = opaque(codes(pc, r, j));
         dd[j] = xv[r][4 * j] * ub(c, 0);
 #pragma unroll
         for (int b = 1; b < 4; ++b) dd[j] = fmaf(xv[r][4 * j + b], ub(c, b), dd[j]);
@@ -433,7 +442,7 @@ struct FmtQx0 {
       const float d = h2f(pc.d[r]), z = -ZERO * d;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t c = codes(pc, r, j);
+        const uint32_t c = opaque(codes(pc, r, j));
         o[8 * r + 2 * j] = pk_bf16(fmaf(ub(c, 0), d, z), fmaf(ub(c, 1), d, z));
         o[8 * r + 2 * j + 1] = pk_bf16(fmaf(ub(c, 2), d, z), fmaf(ub(c, 3), d, z));
       }
@@ -446,7 +455,7 @@ struct FmtQx0 {
       const float d = h2f(pc.d[r]);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t c = codes(pc, r, j);
+        const uint32_t c = opaque(codes(pc, r, j));
 #pragma unroll
         for (int b = 0; b < 4; ++b) wv[r][4 * j + b] = d * (ub(c, b) - ZERO);
       }
@@ -494,8 +503,8 @@ struct FmtQ6KG {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t a = (&pc.a.x)[j], b = (&pc.b.x)[j], h = (&pc.h.x)[j] >> nsh;
-      const uint32_t q0 = ((a >> nsh) & 0x0F0F0F0Fu) | ((h & 0x03030303u) << 4);
-      const uint32_t q1 = ((b >> nsh) & 0x0F0F0F0Fu) | ((h & 0x0C0C0C0Cu) << 2);
+      const uint32_t q0 = opaque(((a >> nsh) & 0x0F0F0F0Fu) | ((h & 0x03030303u) << 4));
+      const uint32_t q1 = opaque(((b >> nsh) & 0x0F0F0F0Fu) | ((h & 0x0C0C0C0Cu) << 2));
       o[2 * j] = pk_bf16(fmaf(ub(q0, 0), ds0, z0), fmaf(ub(q0, 1), ds0, z0));
       o[2 * j + 1] = pk_bf16(fmaf(ub(q0, 2), ds0, z0), fmaf(ub(q0, 3), ds0, z0));
       o[8 + 2 * j] = pk_bf16(fmaf(ub(q1, 0), ds1, z1), fmaf(ub(q1, 1), ds1, z1));
@@ -510,8 +519,8 @@ struct FmtQ6KG {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t a = (&pc.a.x)[j], b = (&pc.b.x)[j], h = (&pc.h.x)[j] >> hsh;
-      const uint32_t q0 = ((a >> nsh) & 0x0F0F0F0Fu) | ((h & 0x03030303u) << 4);
-      const uint32_t q1 = ((b >> nsh) & 0x0F0F0F0Fu) | ((h & 0x0C0C0C0Cu) << 2);
+      const uint32_t q0 = opaque(((a >> nsh) & 0x0F0F0F0Fu) | ((h & 0x03030303u) << 4));
+      const uint32_t q1 = opaque(((b >> nsh) & 0x0F0F0F0Fu) | ((h & 0x0C0C0C0Cu) << 2));
 #pragma unroll
       for (int bb = 0; bb < 4; ++bb) {
         wv[0][4 * j + bb] = ds0 * (ub(q0, bb) - 32.0f);

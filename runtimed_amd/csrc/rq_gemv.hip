@@ -77,11 +77,15 @@ __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
     p = 64 * tm + lane;
   }
   const bool live = p < P;
+  // Loads use a piece and row clamped into the matrix, unconditionally:
+  // a load under a branch makes the compiler drain every outstanding load
+  // (the prefetched row too) before the next use.  Dead lanes and rows past
+  // n contribute nothing (the dot product is selected away).
+  const int pl = live ? p : P - 1;
   const int64_t groups = (n + rows_per_wg - 1) / rows_per_wg;
   int64_t g = blockIdx.x;
   int64_t row = g * rows_per_wg + row_in_wg;
-  typename F::Piece cur;
-  if (live && row < n) cur = F::load(w, aux, row, k, p);
+  typename F::Piece cur = F::load(w, aux, row < n ? row : n - 1, k, pl);
 
   float xv[F::RUNS][16];
   float sx[F::RUNS];
@@ -101,9 +105,9 @@ __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
   for (; g < groups; g += gridDim.x) {
     const int64_t gn = g + gridDim.x;
     const int64_t row_n = gn * rows_per_wg + row_in_wg;
-    typename F::Piece nxt;
-    if (live && gn < groups && row_n < n) nxt = F::load(w, aux, row_n, k, p);
-    float acc = (live && row < n) ? F::dot(cur, xv, sx) : 0.0f;
+    const typename F::Piece nxt = F::load(w, aux, (gn < groups && row_n < n) ? row_n : (row < n ? row : n - 1), k, pl);
+    const float d = F::dot(cur, xv, sx);
+    float acc = (live && row < n) ? d : 0.0f;
     if (team == 1) {
       const int seg = 1 << seg_log2;
       if (seg >= 16) {
@@ -161,20 +165,27 @@ __global__ __launch_bounds__(256) void k_gemv_long(const uint8_t *__restrict__ w
     }
   }
 
+  // Unconditional loads of clamped pieces and rows (see k_gemv_m1): the
+  // next row's loads stay in flight while the current row is computed.
+  if (row >= n) return;
+  int pc[PPL];
+#pragma unroll
+  for (int i = 0; i < PPL; ++i) pc[i] = lane + 64 * i < P ? lane + 64 * i : P - 1;
   typename F::Piece cur[PPL];
 #pragma unroll
-  for (int i = 0; i < PPL; ++i)
-    if (row < n && lane + 64 * i < P) cur[i] = F::load(w, aux, row, k, lane + 64 * i);
+  for (int i = 0; i < PPL; ++i) cur[i] = F::load(w, aux, row, k, pc[i]);
   for (; row < n; row += nw) {
     const int64_t rn = row + nw;
+    const int64_t rl = rn < n ? rn : row;
     typename F::Piece nxt[PPL];
 #pragma unroll
-    for (int i = 0; i < PPL; ++i)
-      if (rn < n && lane + 64 * i < P) nxt[i] = F::load(w, aux, rn, k, lane + 64 * i);
+    for (int i = 0; i < PPL; ++i) nxt[i] = F::load(w, aux, rl, k, pc[i]);
     float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < PPL; ++i)
-      if (lane + 64 * i < P) acc += F::dot(cur[i], xv[i], sx[i]);
+    for (int i = 0; i < PPL; ++i) {
+      const float d = F::dot(cur[i], xv[i], sx[i]);
+      acc += lane + 64 * i < P ? d : 0.0f;
+    }
     acc = seg_sum(acc, 64);
     if (lane == 63) store_out(y, ytype, row, acc);
 #pragma unroll
