@@ -63,14 +63,19 @@ struct FmtQ4K {
     uint4 hd, qv;
     int c;
   };
-  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *, int64_t row, int64_t k, int p) {
-    const uint64_t e = (uint64_t)row * (uint64_t)k + 64u * (uint64_t)(p >> 1);
+  // The piece of the row whose first element is element rk of the flat
+  // stream (rk = row * k).
+  __device__ __forceinline__ static Piece load_e(const uint8_t *w, const uint8_t *, uint64_t rk, int p) {
+    const uint64_t e = rk + 64u * (uint64_t)(p >> 1);
     const uint8_t *bp = w + (e >> 8) * 144u;
     Piece pc;
     pc.c = (int)((e >> 6) & 3u);
     pc.hd = *reinterpret_cast<const uint4 *>(bp);
     pc.qv = *reinterpret_cast<const uint4 *>(bp + 16 + 32 * pc.c + 16 * (p & 1));
     return pc;
+  }
+  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
+    return load_e(w, aux, (uint64_t)row * (uint64_t)k, p);
   }
   // (d*sc, dmin*m) for sub-blocks 2c (low nibbles) and 2c+1 (high nibbles):
   // scale_min_k4 (dequant_k.rs:8-16) on the packed bytes in hd.y/z/w.
@@ -154,8 +159,10 @@ struct FmtQ6K {
     uint32_t d;
     int s;
   };
-  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
-    const uint64_t e = (uint64_t)row * (uint64_t)k + 128u * (uint64_t)(p >> 1);
+  // The piece of the row whose first element is element rk of the flat
+  // stream (rk = row * k).
+  __device__ __forceinline__ static Piece load_e(const uint8_t *w, const uint8_t *aux, uint64_t rk, int p) {
+    const uint64_t e = rk + 128u * (uint64_t)(p >> 1);
     const uint64_t blk = e >> 8;
     const int hf = (int)((e >> 7) & 1u), s = p & 1;
     const uint8_t *rec = w + blk * 208u;
@@ -167,6 +174,9 @@ struct FmtQ6K {
     pc.sc = *reinterpret_cast<const uint2 *>(rec + 192 + 8 * hf);
     pc.d = reinterpret_cast<const uint16_t *>(aux)[blk];
     return pc;
+  }
+  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
+    return load_e(w, aux, (uint64_t)row * (uint64_t)k, p);
   }
   // Unsigned 6-bit codes (q + 32) of run r for dword j.
   __device__ __forceinline__ static uint32_t codes(const Piece &pc, int r, int j) {
@@ -228,15 +238,20 @@ struct FmtQ8 {
     uint4 q[2];
     uint32_t d[2];
   };
-  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
+  // The piece of the row whose first element is element rk of the flat
+  // stream (rk = row * k).
+  __device__ __forceinline__ static Piece load_e(const uint8_t *w, const uint8_t *aux, uint64_t rk, int p) {
     Piece pc;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const uint64_t e = (uint64_t)row * (uint64_t)k + (uint64_t)run_off(p, r);
+      const uint64_t e = rk + (uint64_t)run_off(p, r);
       pc.q[r] = *reinterpret_cast<const uint4 *>(w + e);
       pc.d[r] = reinterpret_cast<const uint16_t *>(aux)[e >> 5];
     }
     return pc;
+  }
+  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
+    return load_e(w, aux, (uint64_t)row * (uint64_t)k, p);
   }
   __device__ __forceinline__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
     float acc = 0.0f;
@@ -294,8 +309,10 @@ struct FmtQ5K {
     uint4 hd, qv, hv;
     int c;
   };
-  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *, int64_t row, int64_t k, int p) {
-    const uint64_t e = (uint64_t)row * (uint64_t)k + 64u * (uint64_t)(p >> 1);
+  // The piece of the row whose first element is element rk of the flat
+  // stream (rk = row * k).
+  __device__ __forceinline__ static Piece load_e(const uint8_t *w, const uint8_t *, uint64_t rk, int p) {
+    const uint64_t e = rk + 64u * (uint64_t)(p >> 1);
     const uint8_t *bp = w + (e >> 8) * 176u;
     Piece pc;
     pc.c = (int)((e >> 6) & 3u);
@@ -303,6 +320,9 @@ struct FmtQ5K {
     pc.qv = *reinterpret_cast<const uint4 *>(bp + 48 + 32 * pc.c + 16 * (p & 1));
     pc.hv = *reinterpret_cast<const uint4 *>(bp + 16 + 16 * (p & 1));
     return pc;
+  }
+  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
+    return load_e(w, aux, (uint64_t)row * (uint64_t)k, p);
   }
   __device__ __forceinline__ static void scales(const Piece &pc, float &a0, float &b0, float &a1, float &b1) {
     FmtQ4K::Piece q4;
@@ -394,12 +414,14 @@ struct FmtQx0 {
     uint32_t d[2];
     int h;
   };
-  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
+  // The piece of the row whose first element is element rk of the flat
+  // stream (rk = row * k).
+  __device__ __forceinline__ static Piece load_e(const uint8_t *w, const uint8_t *aux, uint64_t rk, int p) {
     Piece pc;
     pc.h = p & 1;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const uint64_t blk = ((uint64_t)row * (uint64_t)k + (uint64_t)run_off(p, r)) >> 5;
+      const uint64_t blk = (rk + (uint64_t)run_off(p, r)) >> 5;
       pc.q[r] = *reinterpret_cast<const uint4 *>(w + 16 * blk);
       if (Q5) {
         const uint2 rec = reinterpret_cast<const uint2 *>(aux)[blk];
@@ -411,6 +433,9 @@ struct FmtQx0 {
       }
     }
     return pc;
+  }
+  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
+    return load_e(w, aux, (uint64_t)row * (uint64_t)k, p);
   }
   // Unsigned codes (q + 8, or q + 16 for Q5_0) of dword j of run r.
   __device__ __forceinline__ static uint32_t codes(const Piece &pc, int r, int j) {
@@ -479,8 +504,10 @@ struct FmtQ6KG {
     uint32_t d;
     int ch;
   };
-  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
-    const uint64_t e = (uint64_t)row * (uint64_t)k + 64u * (uint64_t)(p >> 1);
+  // The piece of the row whose first element is element rk of the flat
+  // stream (rk = row * k).
+  __device__ __forceinline__ static Piece load_e(const uint8_t *w, const uint8_t *aux, uint64_t rk, int p) {
+    const uint64_t e = rk + 64u * (uint64_t)(p >> 1);
     const uint64_t blk = e >> 8;
     const int hf = (int)((e >> 7) & 1u), hh = p & 1;
     const uint8_t *rec = w + blk * 208u;
@@ -493,6 +520,9 @@ struct FmtQ6KG {
     pc.sc = *reinterpret_cast<const uint32_t *>(rec + 192 + 8 * hf + 4 * pc.ch) >> (8 * hh);
     pc.d = reinterpret_cast<const uint16_t *>(aux)[blk];
     return pc;
+  }
+  __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
+    return load_e(w, aux, (uint64_t)row * (uint64_t)k, p);
   }
   __device__ __forceinline__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
     const float d = h2f(pc.d);
