@@ -389,6 +389,45 @@ def extra_upload(torch, rq, synth, dev):
             "bytes": total, "tensors": len(tensors), "s": round(dt, 4), "GB/s": round(total / dt / 1e9, 2)}
 
 
+def extra_library(torch, dev, steps):
+    """Context, not a result of this library: the vendor BLAS (hipBLASLt via
+    torch) on the same problem sizes with the weights already dense -- bf16
+    GEMMs for the M=512 prefill shapes, and the FP8 workload through
+    torch._scaled_mm with per-row / per-column scales."""
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        reps = max(5, steps)
+        t0.record()
+        for _ in range(reps):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / reps
+
+    out = []
+    for name, n, k in (("q/k/o 2048x2048", 2048, 2048), ("gate/up 8192x2048", 8192, 2048),
+                       ("down 2048x8192", 2048, 8192), ("lm_head 262144x2048", 262144, 2048)):
+        a = torch.randn((512, k), device=dev).to(torch.bfloat16)
+        w = torch.randn((n, k), device=dev).to(torch.bfloat16)
+        ms = timed(lambda: a @ w.t())
+        out.append({"shape": f"bf16 M=512 {name}", "ms": round(ms, 4), "TFLOP/s": round(2 * 512 * n * k / ms / 1e9, 1)})
+        del a, w
+        torch.cuda.empty_cache()
+    m, n, k = 2048, 14336, 4096
+    a = torch.randn((m, k), device=dev).to(torch.float8_e4m3fn)
+    w = torch.randn((n, k), device=dev).to(torch.float8_e4m3fn)
+    sa = torch.ones((m, 1), device=dev)
+    sw = torch.ones((1, n), device=dev)
+    ms = timed(lambda: torch._scaled_mm(a, w.t(), scale_a=sa, scale_b=sw, out_dtype=torch.bfloat16))
+    out.append({"shape": "fp8 e4m3 2048x14336x4096, row/column scales", "ms": round(ms, 4),
+                "TFLOP/s": round(2 * m * n * k / ms / 1e9, 1)})
+    return {"workload": "vendor BLAS on dense weights (reference point)", "shapes": out}
+
+
 def mode_gate(torch, rq, synth, dev, steps, warmup, eager=False):
     """Only the dominant kernel: R distinct 4864x896 Q4_K gate weights
     (R * 2.45 MB >= 1 GB), one GEMV each, in one HIP graph (or launched
@@ -521,7 +560,8 @@ def main():
                          ("fp8_gemm", lambda: extra_fp8(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("marlin_int4_gemv", lambda: extra_marlin(torch, rq, dev, args.steps, args.warmup)),
                          ("kv_quantizer", lambda: extra_kv(torch, rq, dev, args.steps, args.warmup)),
-                         ("gguf_upload", lambda: extra_upload(torch, rq, synth, dev))):
+                         ("gguf_upload", lambda: extra_upload(torch, rq, synth, dev)),
+                         ("library_reference", lambda: extra_library(torch, dev, args.steps))):
             log(f"extra: {name}")
             try:
                 extra[name] = fn()
