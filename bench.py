@@ -121,6 +121,35 @@ def decode_workload(torch, rq, synth, layers, steps, warmup, dev):
     return W, ms, gate_ms
 
 
+def extra_decode_fused(torch, rq, synth, layers, steps, warmup, dev):
+    """The same layer set with the usual load-time weight fusion: q/k/v
+    concatenated into one 1152x896 weight and gate/up into one 9728x896 (the
+    GGUF streams concatenate exactly: every matrix holds a whole number of
+    Q4_K blocks), so a token is 4 GEMVs per layer over the same bytes."""
+    blocks = {name: synth.q4_k_blocks(100 + i, n * k // 256) for i, (name, n, k) in enumerate(LAYER)}
+    qkv = np.concatenate([blocks["q"], blocks["k"], blocks["v"]])
+    gu = np.concatenate([blocks["gate"], blocks["up"]])
+    fused = [("qkv", qkv, 1152, 896), ("o", blocks["o"], 896, 896), ("gate_up", gu, 9728, 896),
+             ("down", blocks["down"], 896, 4864)]
+    W = [[(rq.QWeight(rq.Q4_K, b, n, k), n, k) for _, b, n, k in fused] for _ in range(layers)]
+    x896 = torch.from_numpy(synth.activations(1, 1, 896)).to(dev)
+    x4864 = torch.from_numpy(synth.activations(2, 1, 4864)).to(dev)
+    ys = {n: torch.empty((1, n), dtype=torch.float32, device=dev) for _, _, n, _ in fused}
+
+    def token():
+        for lw in W:
+            for w, n, k in lw:
+                w.forward(x4864 if k == 4864 else x896, out=ys[n])
+
+    g = capture(torch, token)
+    ms = Timer(torch).replay(g, steps, warmup)
+    del g, W
+    value = layer_bytes() * layers / (ms * 1e-3) / 1e9
+    return {"workload": "decode layer set with fused q/k/v and gate/up weights (4 GEMVs per layer, same bytes)",
+            "GB/s": round(value, 1), "frac_hbm": round(value / HBM_PEAK_GBS, 4),
+            "us_per_layer": round(ms * 1e3 / layers, 2)}
+
+
 def cpu_baseline(oracle, synth, budget_s):
     """Oracle dequant (load time) + f32 GEMV over the dequantized layer."""
     threads = cpu_threads()
@@ -553,7 +582,9 @@ def main():
 
     extra = {}
     if not args.no_extras:
-        for name, fn in (("q8_0_gemv", lambda: extra_q8_gemv(torch, rq, synth, dev, args.steps, args.warmup)),
+        for name, fn in (("decode_fused_weights", lambda: extra_decode_fused(torch, rq, synth, args.layers, args.steps,
+                                                                               args.warmup, dev)),
+                         ("q8_0_gemv", lambda: extra_q8_gemv(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("q4_k_gemv_large", lambda: extra_large_gemv(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("verify", lambda: extra_verify(torch, rq, W[:32], dev, args.steps, args.warmup)),
                          ("prefill", lambda: extra_prefill(torch, rq, synth, dev, args.steps, args.warmup)),

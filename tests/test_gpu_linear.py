@@ -205,3 +205,16 @@ def test_next_formats_matrix_cores(dev, qtype, m, n, k):
     for ydt in (torch.float32, torch.bfloat16):
         y = w.forward(xb.to(dev), out_dtype=ydt).float().cpu().numpy()
         assert norm_err(y, r) <= TOL_BF16, (ydt, norm_err(y, r))
+
+
+@pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q8_0, rq.Q6_K])
+def test_fused_weights_concatenate(dev, qtype):
+    # q/k/v (and gate/up) each hold a whole number of blocks, so their GGUF
+    # streams concatenate into one weight whose rows are the stacked rows;
+    # each output row is computed the same way, so the results are identical.
+    parts = [(896, 896), (128, 896), (128, 896)]
+    data = [synth.weight_blocks(qtype, 300 + i, n, 896) for i, (n, _) in enumerate(parts)]
+    x = torch.from_numpy(synth.activations(9, 1, 896)).to(dev)
+    sep = [rq.QWeight(qtype, d, n, 896).forward(x) for d, (n, _) in zip(data, parts)]
+    fused = rq.QWeight(qtype, np.concatenate(data), 1152, 896).forward(x)
+    assert torch.equal(fused, torch.cat(sep, dim=1))
