@@ -49,6 +49,43 @@ __device__ __forceinline__ float seg_sum(float v, int seg) {
   return v;
 }
 
+// Activations of an M = 1 call, staged once per workgroup in LDS as f32.
+// Loading each lane's 32-64 activations straight from global memory made
+// every wave pull a full copy of x through the L1/TA path (x is small, but it
+// is read 8-16x more often than the weights): on a 4864 x 896 GEMV that cost
+// 1.6 of 4.7 us.  Layout: 16 bytes of padding after every 256 bytes, so the
+// 8 lanes served by one ds_read_b128 (pieces 64 floats apart) hit distinct
+// banks.  A run of 16 activations never crosses a padding gap.
+constexpr int64_t kXldsMaxK = 12288;
+__device__ __forceinline__ int xpad(int e) { return e + 4 * (e >> 6); }
+inline size_t xlds_bytes(int64_t k) { return k <= kXldsMaxK ? (size_t)(k + 4 * (k >> 6) + 4) * sizeof(float) : 0; }
+
+__device__ __forceinline__ void stage_x(const void *x, int xtype, int k, float *xs) {
+  for (int e = 4 * (int)threadIdx.x; e < k; e += 4 * (int)blockDim.x)
+    *reinterpret_cast<float4 *>(xs + xpad(e)) = load_x4(x, xtype, e);
+  __syncthreads();
+}
+
+template <int LEN>
+__device__ __forceinline__ void load_run_lds(const float *xs, int e0, float *dst) {
+  const float4 *src = reinterpret_cast<const float4 *>(xs + xpad(e0));
+#pragma unroll
+  for (int j = 0; j < LEN / 4; ++j) {
+    const float4 a = src[j];
+    dst[4 * j + 0] = a.x;
+    dst[4 * j + 1] = a.y;
+    dst[4 * j + 2] = a.z;
+    dst[4 * j + 3] = a.w;
+  }
+}
+
+// Loads run r of piece p: from the LDS copy when there is one (xs != null).
+template <class F>
+__device__ __forceinline__ void load_piece_x(const void *x, int xtype, const float *xs, int p, int r, float *dst) {
+  if (xs) load_run_lds<16>(xs, (int)F::run_off(p, r), dst);
+  else load_run<16>(x, xtype, F::run_off(p, r), dst);
+}
+
 // M = 1: every lane owns one piece position; its activations are loaded once
 // into registers and reused for every row it visits.  Rows with P <= 64
 // pieces sit on an aligned segment of seg = max(16, next_pow2(P)) lanes
@@ -62,7 +99,7 @@ __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
                                                 const void *__restrict__ x, int xtype,
                                                 void *__restrict__ y, int ytype, int64_t n,
                                                 int64_t k, int seg_log2, int team,
-                                                int rows_per_wg) {
+                                                int rows_per_wg, bool xlds) {
   __shared__ float red[8][8];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int P = (int)(k / F::PE);
@@ -87,13 +124,19 @@ __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
   int64_t row = g * rows_per_wg + row_in_wg;
   typename F::Piece cur = F::load(w, aux, row < n ? row : n - 1, k, pl);
 
+  extern __shared__ float xs_dyn[];
+  const float *xs = nullptr;
+  if (xlds) {  // uniform: the whole workgroup stages x once
+    stage_x(x, xtype, (int)k, xs_dyn);
+    xs = xs_dyn;
+  }
   float xv[F::RUNS][16];
   float sx[F::RUNS];
 #pragma unroll
   for (int r = 0; r < F::RUNS; ++r) {
     sx[r] = 0.0f;
     if (live) {
-      load_run<16>(x, xtype, F::run_off(p, r), xv[r]);
+      load_piece_x<F>(x, xtype, xs, p, r, xv[r]);
 #pragma unroll
       for (int t = 0; t < 16; ++t) sx[r] += xv[r][t];
     } else {
@@ -140,12 +183,18 @@ __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
 template <class F, int PPL>
 __global__ __launch_bounds__(256) void k_gemv_long(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
                                                    const void *__restrict__ x, int xtype, void *__restrict__ y,
-                                                   int ytype, int64_t n, int64_t k) {
+                                                   int ytype, int64_t n, int64_t k, bool xlds) {
   const int lane = threadIdx.x & 63;
   const int P = (int)(k / F::PE);
   const int64_t nw = (int64_t)gridDim.x * 4;
   int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
 
+  extern __shared__ float xs_dyn[];
+  const float *xs = nullptr;
+  if (xlds) {  // uniform: the whole workgroup stages x once
+    stage_x(x, xtype, (int)k, xs_dyn);
+    xs = xs_dyn;
+  }
   float xv[PPL][F::RUNS][16];
   float sx[PPL][F::RUNS];
 #pragma unroll
@@ -155,7 +204,7 @@ __global__ __launch_bounds__(256) void k_gemv_long(const uint8_t *__restrict__ w
     for (int r = 0; r < F::RUNS; ++r) {
       sx[i][r] = 0.0f;
       if (p < P) {
-        load_run<16>(x, xtype, F::run_off(p, r), xv[i][r]);
+        load_piece_x<F>(x, xtype, xs, p, r, xv[i][r]);
 #pragma unroll
         for (int t = 0; t < 16; ++t) sx[i][r] += xv[i][r][t];
       } else {
@@ -293,8 +342,9 @@ int run_long(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, 
   // HBM latency, few enough that every wave sees several rows.
   const int64_t waves = wt->n < 256 * 16 ? wt->n : 256 * 16;
   const unsigned blocks = (unsigned)((waves + 3) / 4);
-  hipLaunchKernelGGL((k_gemv_long<F, PPL>), dim3(blocks), dim3(256), 0, s, wt->data, wt->data + wt->aux_off, x,
-                     xtype, y, ytype, wt->n, wt->k);
+  const size_t xb = xlds_bytes(wt->k);
+  hipLaunchKernelGGL((k_gemv_long<F, PPL>), dim3(blocks), dim3(256), xb, s, wt->data, wt->data + wt->aux_off, x,
+                     xtype, y, ytype, wt->n, wt->k, xb != 0);
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }
 
@@ -325,8 +375,9 @@ int run_m1(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hi
   }
   const int64_t groups = (wt->n + rows_per_wg - 1) / rows_per_wg;
   const unsigned blocks = (unsigned)(groups < 16384 ? groups : 16384);
-  hipLaunchKernelGGL((k_gemv_m1<F>), dim3(blocks), dim3(threads), 0, s, wt->data, wt->data + wt->aux_off,
-                     x, xtype, y, ytype, wt->n, wt->k, seg_log2, team, rows_per_wg);
+  const size_t xb = xlds_bytes(wt->k);
+  hipLaunchKernelGGL((k_gemv_m1<F>), dim3(blocks), dim3(threads), xb, s, wt->data, wt->data + wt->aux_off,
+                     x, xtype, y, ytype, wt->n, wt->k, seg_log2, team, rows_per_wg, xb != 0);
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }
 
