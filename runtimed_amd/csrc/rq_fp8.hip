@@ -20,8 +20,6 @@
 // one MFMA operand column touch distinct 16-byte bank groups.
 //
 // Roofline: MFMA-bound (fp8 dense peak 5.0 PFLOP/s); flops = 2*m*n*k.
-#include <stdlib.h>
-
 #include "rq_e4m3.h"
 #include "rq_epilogue.h"
 #include "rq_internal.h"
@@ -386,13 +384,8 @@ int launch_fp8_gemm(const uint8_t *xq, const float *xs, int64_t m, const uint8_t
   if (k % 128 == 0 && aligned) {
     // 256 x 256 tiles (128 x 128 per wave) when there are enough of them to
     // cover the CUs, else 128 x 128.
-    // RQ_FP8_TILE=128|256 overrides the choice (tuning and profiling).
-    static const int forced = [] {
-      const char *e = getenv("RQ_FP8_TILE");
-      return e ? atoi(e) : 0;
-    }();
     const int64_t big = ((m + 255) / 256) * ((n + 255) / 256);
-    if (forced == 256 || (forced != 128 && big >= 200)) {
+    if (big >= 200) {
       const dim3 grid((unsigned)((n + 255) / 256), (unsigned)((m + 255) / 256));
       hipLaunchKernelGGL(k_fp8_gemm_pipe, grid, dim3(256), 0, s, xq, xs, m, w, ws, n, k, y, ytype);
     } else {

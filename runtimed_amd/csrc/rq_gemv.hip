@@ -124,7 +124,7 @@ __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
   int64_t row = g * rows_per_wg + row_in_wg;
   typename F::Piece cur = F::load(w, aux, row < n ? row : n - 1, k, pl);
 
-  extern __shared__ float xs_dyn[];
+  extern __shared__ __attribute__((aligned(16))) float xs_dyn[];
   const float *xs = nullptr;
   if (xlds) {  // uniform: the whole workgroup stages x once
     stage_x(x, xtype, (int)k, xs_dyn);
@@ -189,7 +189,7 @@ __global__ __launch_bounds__(256) void k_gemv_long(const uint8_t *__restrict__ w
   const int64_t nw = (int64_t)gridDim.x * 4;
   int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
 
-  extern __shared__ float xs_dyn[];
+  extern __shared__ __attribute__((aligned(16))) float xs_dyn[];
   const float *xs = nullptr;
   if (xlds) {  // uniform: the whole workgroup stages x once
     stage_x(x, xtype, (int)k, xs_dyn);

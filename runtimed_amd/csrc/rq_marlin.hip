@@ -74,13 +74,15 @@ __global__ __launch_bounds__(256) void k_marlin_dequant(const uint4 *__restrict_
 }
 
 // Sum over the 32 inputs of one record of x[base .. base+32) * (q - 8).
-__device__ __forceinline__ float record_dot(const uint32_t (&wd)[4], const void *x, int xtype, int64_t base,
-                                            int valid, bool vec) {
+// xs: the activation rows of this workgroup staged in LDS as f32 (base is
+// then an offset into xs), or null to read x from global memory.
+__device__ __forceinline__ float record_dot(const uint32_t (&wd)[4], const void *x, int xtype, const float *xs,
+                                            int64_t base, int valid, bool vec) {
   float a = 0.0f;
   if (vec && valid == 32) {
 #pragma unroll
     for (int j4 = 0; j4 < 8; ++j4) {
-      const float4 xv = load_x4(x, xtype, base + 4 * j4);
+      const float4 xv = xs ? *reinterpret_cast<const float4 *>(xs + base + 4 * j4) : load_x4(x, xtype, base + 4 * j4);
       const uint32_t v = wd[j4 >> 1] >> (16 * (j4 & 1));
       a = fmaf(xv.x, (float)(v & 15u) - 8.0f, a);
       a = fmaf(xv.y, (float)((v >> 4) & 15u) - 8.0f, a);
@@ -89,7 +91,8 @@ __device__ __forceinline__ float record_dot(const uint32_t (&wd)[4], const void 
     }
   } else {
     for (int e = 0; e < valid; ++e)
-      a = fmaf(load_x1(x, xtype, base + e), (float)((wd[e >> 3] >> (4 * (e & 7))) & 15u) - 8.0f, a);
+      a = fmaf(xs ? xs[base + e] : load_x1(x, xtype, base + e), (float)((wd[e >> 3] >> (4 * (e & 7))) & 15u) - 8.0f,
+               a);
   }
   return a;
 }
@@ -99,15 +102,26 @@ template <int R, int MT>
 __global__ __launch_bounds__(512) void k_marlin_gemv(const uint4 *__restrict__ packed, const float *__restrict__ s,
                                                      const void *__restrict__ x, int xtype, int64_t m, int64_t n,
                                                      int64_t k, int64_t kc, void *__restrict__ y, int ytype,
-                                                     bool vec) {
+                                                     bool vec, bool xlds) {
   constexpr int GROUPS = 64 / R;      // lane groups per wave
   constexpr int SLOTS = 8 * GROUPS;   // chunk slots per workgroup
   __shared__ float red[8][MT][R];
+  extern __shared__ __attribute__((aligned(16))) float xs_dyn[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rl = lane % R;
   const int64_t row = (int64_t)blockIdx.x * R + rl;
   const int slot = wave * GROUPS + lane / R;
   const int64_t m0 = (int64_t)blockIdx.y * MT;
+  // The MT activation rows are read by every lane group of the workgroup:
+  // staged once in LDS (lane groups on one chunk then read the same address,
+  // an LDS broadcast) instead of once per lane from global memory.
+  const float *xs = nullptr;
+  if (xlds) {
+    const int64_t rows = m - m0 < MT ? m - m0 : MT;
+    for (int64_t e = threadIdx.x; e < rows * k; e += 512) xs_dyn[e] = load_x1(x, xtype, m0 * k + e);
+    __syncthreads();
+    xs = xs_dyn;
+  }
   float acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
@@ -129,7 +143,8 @@ __global__ __launch_bounds__(512) void k_marlin_gemv(const uint4 *__restrict__ p
           const int valid = (int)(k - kb < 32 ? k - kb : 32);
 #pragma unroll
           for (int t = 0; t < MT; ++t)
-            if (m0 + t < m) acc[t] += record_dot(wd, x, xtype, (m0 + t) * k + kb, valid, vec);
+            if (m0 + t < m)
+          acc[t] += record_dot(wd, x, xtype, xs, (xs ? t * k : (m0 + t) * k) + kb, valid, vec);
         }
       }
     }
@@ -159,8 +174,10 @@ template <int R, int MT>
 void launch_gemv(const uint4 *packed, const float *s, const void *x, int xtype, int64_t m, int64_t n, int64_t k,
                  int64_t kc, void *y, int ytype, bool vec, hipStream_t st) {
   const dim3 grid((unsigned)((n + R - 1) / R), (unsigned)((m + MT - 1) / MT));
-  hipLaunchKernelGGL((k_marlin_gemv<R, MT>), grid, dim3(512), 0, st, packed, s, x, xtype, m, n, k, kc, y, ytype,
-                     vec);
+  // MT rows of f32 activations in LDS when they fit in 64 KB.
+  const size_t xb = (size_t)MT * k * sizeof(float) <= 65536 ? (size_t)MT * k * sizeof(float) : 0;
+  hipLaunchKernelGGL((k_marlin_gemv<R, MT>), grid, dim3(512), xb, st, packed, s, x, xtype, m, n, k, kc, y, ytype,
+                     vec, xb != 0);
 }
 
 template <int R>
