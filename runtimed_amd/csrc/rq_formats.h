@@ -85,9 +85,11 @@ struct FmtQ4K {
     // wave usually hold different chunks c, and a branch would run both).
     const int sh = 16 * (pc.c & 1);
     const uint32_t Y = pc.hd.y >> sh, Z = pc.hd.z >> sh, W = pc.hd.w >> sh;
-    const bool low = pc.c < 2;
-    const uint32_t sc = opaque(low ? (Y & 0x3F3Fu) : ((W & 0x0F0Fu) | ((Y >> 2) & 0x3030u)));
-    const uint32_t mn = opaque(low ? (Z & 0x3F3Fu) : (((W >> 4) & 0x0F0Fu) | ((Z >> 2) & 0x3030u)));
+    // The case is picked by a mask the optimizer cannot see through, so it
+    // cannot turn the selection back into a branch.
+    const uint32_t low = opaque(pc.c < 2 ? 0xFFFFFFFFu : 0u);
+    const uint32_t sc = opaque((Y & 0x3F3Fu & low) | (((W & 0x0F0Fu) | ((Y >> 2) & 0x3030u)) & ~low));
+    const uint32_t mn = opaque((Z & 0x3F3Fu & low) | ((((W >> 4) & 0x0F0Fu) | ((Z >> 2) & 0x3030u)) & ~low));
     const float d = h2f(pc.hd.x), dmin = h2f(pc.hd.x >> 16);
     a0 = d * ub(sc, 0);
     b0 = dmin * ub(mn, 0);

@@ -1,12 +1,12 @@
 // rq_smallm.hip -- quantized linear y = x W^T for 2 <= M <= 64 bf16
-// activation rows (speculative verify; config-4 shapes) on the matrix cores.
+// activation rows (speculative verify) on the matrix cores.
 //
 // The weight rows are the MFMA A operand (v_mfma_f32_16x16x32_bf16: lane l
 // holds row l % 16 and 8 k-values chosen by l / 16) and the activation rows
 // the B operand, so a weight is decoded once, straight into A registers (no
 // LDS), and used by all M rows.  The cost per weight is then the decode
 // (about 3 VALU instructions) whatever M is, against decode + M FMAs on the
-// VALU, and the kernel stays near the weight-streaming bound up to M = 64.
+// VALU.
 //
 // K order inside an MFMA is free as long as A and B agree.  Per 64-wide
 // chunk of a weight row, lane group g = l / 16 takes chunk elements
@@ -15,8 +15,9 @@
 // takes the quarter [8g + 4h, + 4) of each.  The activations are loaded for
 // the same positions.
 //
-// Workgroup: 4 waves on 16 weight rows; wave w takes chunks w, w + 4, ...;
-// the four partial 16 x (16 MT) tiles are summed through LDS.
+// Workgroup: 4 waves on 16 weight rows; wave w takes chunks w, w + 4, ...,
+// loading a batch of them at once; the four partial 16 x (16 MT) tiles are
+// summed through LDS.
 #include <hip/hip_runtime.h>
 
 #include "rq_epilogue.h"
@@ -240,13 +241,62 @@ __device__ __forceinline__ bf16x8 pick(uint32_t a0, uint32_t a1, uint32_t b0, ui
   return __builtin_bit_cast(bf16x8, (uint4){a0, a1, b0, b1});
 }
 
-// MT column tiles of 16 activation rows (M <= 16 MT).
+// x fragments of chunk t for every column tile: elements [8g, 8g + 8) and
+// [32 + 8g, 32 + 8g + 8) of the chunk, 16 bytes each.
+// (LLVM vector types: loads into HIP's uint4 struct become memcpys that
+// keep the fragment in scratch memory.)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+template <int MT>
+struct XFrag {
+  u32x4 a[MT], b[MT];
+};
+
+template <int MT>
+__device__ __forceinline__ void load_x(XFrag<MT> &f, const uint16_t *const (&xr)[MT], int64_t t) {
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) {
+    f.a[ct] = *reinterpret_cast<const u32x4 *>(xr[ct] + 64 * t);
+    f.b[ct] = *reinterpret_cast<const u32x4 *>(xr[ct] + 64 * t + 32);
+  }
+}
+
+// Decode chunk c into A fragments and multiply with the activation
+// fragments; vm (all ones or zero) masks the decoded weights, so a masked
+// chunk adds exact zeros.
 template <class C, int MT>
-__global__ __launch_bounds__(256) void k_smallm(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
-                                                const uint16_t *__restrict__ x, int64_t m,
-                                                void *__restrict__ y, int ytype, int64_t n, int64_t k) {
-  __shared__ f32x4 part[4][MT][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4;
+__device__ __forceinline__ void mma_chunk(const typename C::Chunk &c, const XFrag<MT> &xf, f32x4 (&acc)[MT], int g,
+                                          uint32_t vm) {
+  uint32_t o[8];
+  decode_chunk<C>(c, o, g);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] &= vm;
+  // MFMA h takes the quarter [8g + 4h, + 4) of both runs: words 2h, 2h + 1
+  // of each 16-byte fragment.
+  const bf16x8 f0 = pick(o[0], o[1], o[4], o[5]), f1 = pick(o[2], o[3], o[6], o[7]);
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct)
+    acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f0, pick(xf.a[ct].x, xf.a[ct].y, xf.b[ct].x, xf.b[ct].y),
+                                                      acc[ct], 0, 0, 0);
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct)
+    acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f1, pick(xf.a[ct].z, xf.a[ct].w, xf.b[ct].z, xf.b[ct].w),
+                                                      acc[ct], 0, 0, 0);
+}
+
+// MT column tiles of 16 activation rows (M <= 16 MT); NW waves split K,
+// wave w taking chunks w, w + NW, ...  A wave issues the loads of B chunks
+// (weights and activations) at once, then decodes and multiplies them.
+// The loop body has no conditional work: a load whose result is used under
+// a branch is sunk into the branch and waited for there, and a prefetch
+// carried from one iteration to the next is merged back into a load at the
+// loop top.  Chunks past the end load a valid chunk again and are masked.
+template <class C, int MT, int NW, int B>
+__global__ __launch_bounds__(64 * NW) void k_smallm(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
+                                                    const uint16_t *__restrict__ x, int64_t m,
+                                                    void *__restrict__ y, int ytype, int64_t n, int64_t k) {
+  __shared__ f32x4 part[NW][MT][64];
+  const int lane = threadIdx.x & 63, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t n0 = (int64_t)blockIdx.x * 16;
   const int64_t row = n0 + (lane & 15) < n ? n0 + (lane & 15) : n - 1;
   const int64_t nk = k / 64;
@@ -264,27 +314,22 @@ __global__ __launch_bounds__(256) void k_smallm(const uint8_t *__restrict__ w, c
 #pragma unroll
   for (int ct = 0; ct < MT; ++ct) acc[ct] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
-  typename C::Chunk cur = C::load(w, aux, row, k, wave < nk ? wave : 0, g);
-  for (int64_t t = wave; t < nk; t += 4) {
-    const typename C::Chunk c = cur;
-    if (t + 4 < nk) cur = C::load(w, aux, row, k, t + 4, g);
-    uint4 xa[MT], xb[MT];
+  for (int64_t t = wave; t < nk; t += B * NW) {
+    typename C::Chunk c[B];
+    XFrag<MT> xf[B];
 #pragma unroll
-    for (int ct = 0; ct < MT; ++ct) {
-      xa[ct] = *reinterpret_cast<const uint4 *>(xr[ct] + 64 * t);
-      xb[ct] = *reinterpret_cast<const uint4 *>(xr[ct] + 64 * t + 32);
+    for (int i = 0; i < B; ++i) {
+      const int64_t ti = t + i * NW < nk ? t + i * NW : t;
+      c[i] = C::load(w, aux, row, k, ti, g);
+      load_x<MT>(xf[i], xr, ti);
     }
-    uint32_t o[8];
-    decode_chunk<C>(c, o, g);
+    // Keep every load of the batch ahead of the first use (the scheduler
+    // would otherwise trade loads in flight for registers).
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const bf16x8 fa = pick(o[2 * h], o[2 * h + 1], o[4 + 2 * h], o[4 + 2 * h + 1]);
-#pragma unroll
-      for (int ct = 0; ct < MT; ++ct) {
-        const uint32_t *pa = &xa[ct].x, *pb = &xb[ct].x;
-        const bf16x8 fb = pick(pa[2 * h], pa[2 * h + 1], pb[2 * h], pb[2 * h + 1]);
-        acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, fb, acc[ct], 0, 0, 0);
-      }
+    for (int i = 0; i < B; ++i) {
+      const uint32_t vm = i == 0 ? 0xFFFFFFFFu : opaque(t + i * NW < nk ? 0xFFFFFFFFu : 0u);
+      mma_chunk<C, MT>(c[i], xf[i], acc, g, vm);
     }
   }
 
@@ -293,11 +338,11 @@ __global__ __launch_bounds__(256) void k_smallm(const uint8_t *__restrict__ w, c
   __syncthreads();
   // 16 x 16 C layout: lane l holds column (activation row) l % 16 and weight
   // rows 4 (l / 16) + i.  Thread t sums one lane slot of one column tile.
-  for (int slot = threadIdx.x; slot < MT * 64; slot += 256) {
+  for (int slot = threadIdx.x; slot < MT * 64; slot += 64 * NW) {
     const int ct = slot >> 6, l = slot & 63;
     f32x4 v = part[0][ct][l];
 #pragma unroll
-    for (int q = 1; q < 4; ++q) v += part[q][ct][l];
+    for (int q = 1; q < NW; ++q) v += part[q][ct][l];
     const int64_t mr = 16 * ct + (l & 15);
     if (mr < m) {
 #pragma unroll
@@ -309,18 +354,26 @@ __global__ __launch_bounds__(256) void k_smallm(const uint8_t *__restrict__ w, c
   }
 }
 
+// Four waves per workgroup.  Batch sizes as measured on the 0.5B-model
+// layer shapes: 4 chunks for one and two column tiles; one for four (their
+// registers leave no room for a batch, and the kernel is decode-bound).
+// More waves per workgroup or deeper batches were slower: the masked
+// chunks of a partly filled batch cost as much decode as real ones.
+template <class C, int MT>
+int run_mt(const rq_weight *wt, const uint16_t *x, int64_t m, void *y, int ytype, hipStream_t s) {
+  constexpr int B = MT == 4 ? 1 : 4;
+  const dim3 grid((unsigned)((wt->n + 15) / 16));
+  const uint8_t *aux = wt->data + wt->aux_off;
+  hipLaunchKernelGGL((k_smallm<C, MT, 4, B>), grid, dim3(256), 0, s, wt->data, aux, x, m, y, ytype, wt->n, wt->k);
+  return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "small-M launch failed");
+}
+
 template <class C>
 int run(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {
-  const dim3 grid((unsigned)((wt->n + 15) / 16));
   const uint16_t *xb = static_cast<const uint16_t *>(x);
-  const uint8_t *aux = wt->data + wt->aux_off;
-  if (m <= 16)
-    hipLaunchKernelGGL((k_smallm<C, 1>), grid, dim3(256), 0, s, wt->data, aux, xb, m, y, ytype, wt->n, wt->k);
-  else if (m <= 32)
-    hipLaunchKernelGGL((k_smallm<C, 2>), grid, dim3(256), 0, s, wt->data, aux, xb, m, y, ytype, wt->n, wt->k);
-  else
-    hipLaunchKernelGGL((k_smallm<C, 4>), grid, dim3(256), 0, s, wt->data, aux, xb, m, y, ytype, wt->n, wt->k);
-  return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "small-M launch failed");
+  if (m <= 16) return run_mt<C, 1>(wt, xb, m, y, ytype, s);
+  if (m <= 32) return run_mt<C, 2>(wt, xb, m, y, ytype, s);
+  return run_mt<C, 4>(wt, xb, m, y, ytype, s);
 }
 
 }  // namespace
