@@ -34,6 +34,21 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint8_t *s, uint32_t &
   }
 }
 
+// The same on the scale bytes held as three words (bytes 0-3, 4-7, 8-11),
+// so they stay in registers.
+__device__ __forceinline__ void scale_min_k4_w(int j, uint32_t Y, uint32_t Z, uint32_t W, uint32_t &sc,
+                                               uint32_t &m) {
+  const int sh = 8 * (j & 3);
+  const uint32_t y = (Y >> sh) & 0xFFu, z = (Z >> sh) & 0xFFu, w = (W >> sh) & 0xFFu;
+  if (j < 4) {
+    sc = y & 63u;
+    m = z & 63u;
+  } else {
+    sc = (w & 0xFu) | ((y >> 6) << 4);
+    m = (w >> 4) | ((z >> 6) << 4);
+  }
+}
+
 // One element of one GGUF block from raw bytes (any alignment).
 __device__ float decode_raw(int qtype, const uint8_t *b, int i) {
   switch (qtype) {
@@ -112,12 +127,8 @@ __device__ float4 quad_q4k(const uint8_t *__restrict__ src, uint64_t t) {
   const uint4 hd = *reinterpret_cast<const uint4 *>(b);
   const int chunk = i0 >> 6, r = i0 & 63, j = 2 * chunk + (r >> 5);
   const uint32_t qw = *reinterpret_cast<const uint32_t *>(b + 16 + 32 * chunk + (r & 31));
-  uint8_t s[12];
-  *reinterpret_cast<uint32_t *>(s) = hd.y;
-  *reinterpret_cast<uint32_t *>(s + 4) = hd.z;
-  *reinterpret_cast<uint32_t *>(s + 8) = hd.w;
   uint32_t sc, m;
-  scale_min_k4(j, s, sc, m);
+  scale_min_k4_w(j, hd.y, hd.z, hd.w, sc, m);
   const float d1 = f16_bits_to_f32(hd.x & 0xFFFFu) * (float)sc;
   const float m1 = f16_bits_to_f32(hd.x >> 16) * (float)m;
   const uint32_t q4 = (r < 32) ? (qw & 0x0F0F0F0Fu) : ((qw >> 4) & 0x0F0F0F0Fu);
@@ -138,12 +149,8 @@ __device__ float4 quad_q5k(const uint8_t *__restrict__ src, uint64_t t) {
   const int chunk = i0 >> 6, r = i0 & 63, l = r & 31, j = 2 * chunk + (r >> 5);
   const uint32_t qw = *reinterpret_cast<const uint32_t *>(b + 48 + 32 * chunk + l);
   const uint32_t hw = *reinterpret_cast<const uint32_t *>(b + 16 + l);
-  uint8_t s[12];
-  *reinterpret_cast<uint32_t *>(s) = hd.y;
-  *reinterpret_cast<uint32_t *>(s + 4) = hd.z;
-  *reinterpret_cast<uint32_t *>(s + 8) = hd.w;
   uint32_t sc, m;
-  scale_min_k4(j, s, sc, m);
+  scale_min_k4_w(j, hd.y, hd.z, hd.w, sc, m);
   const float d1 = f16_bits_to_f32(hd.x & 0xFFFFu) * (float)sc;
   const float m1 = f16_bits_to_f32(hd.x >> 16) * (float)m;
   const int bit = 2 * chunk + (r >> 5);

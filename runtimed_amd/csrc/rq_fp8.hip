@@ -23,9 +23,12 @@
 #include "rq_e4m3.h"
 #include "rq_epilogue.h"
 #include "rq_internal.h"
+#include "rq_pipe.h"
 
 namespace rq {
 namespace {
+
+using namespace pipe;
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -186,17 +189,6 @@ __global__ __launch_bounds__(256) void k_fp8_gemm_mfma(const uint8_t *__restrict
 // without staging registers.  Rows carry no padding; instead the four 16-byte
 // chunks of row r are stored XOR-swizzled by (r >> 2) & 3, so the 32 lanes
 // that read one operand column of 32 rows hit 16 distinct 16-byte bank slots.
-constexpr int P_STAGE = 32768, P_B = 16384;
-
-typedef __attribute__((address_space(3))) void lds_void;
-
-__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
-
-template <int VM>
-__device__ __forceinline__ void wait_vm() {
-  // s_waitcnt vmcnt(VM) with expcnt / lgkmcnt left at their maxima (gfx9 encoding)
-  __builtin_amdgcn_s_waitcnt((VM & 0xF) | ((VM >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
 
 // Issue the direct loads of one stage.  The LDS pointer is __restrict__ so
 // that, once inlined, the accesses carry scoped alias metadata and the
@@ -212,47 +204,9 @@ __device__ __forceinline__ void pipe_issue(uint8_t *__restrict__ S, const uint8_
     __builtin_amdgcn_global_load_lds(gb[j] + k0, (lds_void *)(S + P_B + (64 * wave + 16 * j) * 64), 16, 0, 0);
 }
 
-// LDS operand reads are issued as explicit ds_read_b128 and completed by one
-// s_waitcnt lgkmcnt(0) that takes every loaded register as an operand, so no
-// use can be scheduled before the wait.  (As compiler-visible LDS loads they
-// would each be preceded by a wait for all in-flight direct loads, because
-// the compiler cannot prove that those target another stage buffer.)
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ u32x4 ds_read16(const uint8_t *p) {
-  u32x4 v;
-  const uint32_t off = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(off));
-  return v;
-}
-
-// Fragment registers of one K-step: 8 x 16 bytes of A rows, 8 of B rows.
-struct Frags {
-  u32x4 x[16];
-};
-
-// Address (LDS byte offset) of fragment f (0..7 A, 8..15 B) of a stage.
-__device__ __forceinline__ const uint8_t *frag_addr(const uint8_t *S, int f, int wm, int wn, int lane) {
-  const int g = lane >> 5, half = f & 1, t = (f >> 1) & 3;
-  const int r = (f < 8 ? 128 * wm : 128 * wn) + 32 * t + (lane & 31);
-  return S + (f < 8 ? 0 : P_B) + r * 64 + 16 * ((2 * g + half) ^ swz(r));
-}
-
 __device__ __forceinline__ i32x8 frag_a(const Frags &F, int i) {
   const u32x4 x0 = F.x[2 * i], x1 = F.x[2 * i + 1];
   return (i32x8){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
-}
-
-__device__ __forceinline__ void wait_lds(Frags &F) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(F.x[0]), "+v"(F.x[1]), "+v"(F.x[2]), "+v"(F.x[3]));
-  asm volatile("" : "+v"(F.x[4]), "+v"(F.x[5]), "+v"(F.x[6]), "+v"(F.x[7]));
-  asm volatile("" : "+v"(F.x[8]), "+v"(F.x[9]), "+v"(F.x[10]), "+v"(F.x[11]));
-  asm volatile("" : "+v"(F.x[12]), "+v"(F.x[13]), "+v"(F.x[14]), "+v"(F.x[15]));
-}
-
-__device__ __forceinline__ void read_all(const uint8_t *__restrict__ S, Frags &F, int wm, int wn, int lane) {
-#pragma unroll
-  for (int f = 0; f < 16; ++f) F.x[f] = ds_read16(frag_addr(S, f, wm, wn, lane));
 }
 
 // The 16 MFMAs of one K-step on `cur`, each followed by one LDS read of the

@@ -22,6 +22,7 @@
 // flops = 2*m*n*k); HBM-bound below (weight bytes dominate).
 #include "rq_epilogue.h"
 #include "rq_formats.h"
+#include "rq_pipe.h"
 
 namespace rq {
 namespace {
@@ -142,6 +143,212 @@ __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restric
   });
 }
 
+// ---- pipelined 256 x 256 kernel ------------------------------------------
+//
+// Four waves of 128 x 128 (4 x 4 MFMA tiles of 32 x 32, 256 accumulators in
+// AGPRs), K-steps of 32 inputs (64 bytes of bf16 per row) through four LDS
+// stages of 32 KB: 256 activation rows then 256 weight rows, swizzled as in
+// rq_pipe.h.  Every global load goes to registers (the compiler then counts
+// its waits exactly; mixed with direct-to-LDS loads it would wait for all of
+// them) and every LDS access is explicit (ordered against the bare barriers).
+//
+// Step s: each thread writes its four 16-byte activation chunks of step
+// s + 2 (loaded at step s - 2; 4 lanes per row, 16 rows per load
+// instruction) into their stage and loads those of step s + 4.  On even
+// steps it decodes piece h = t % 2 of weight rows t / 2 and t / 2 + 128 for
+// chunk (s + 2) / 2 (loaded at step s - 4; the two lanes of a row read
+// adjacent bytes): run 0 of piece 2c + h holds inputs 16h .. 16h + 15 of
+// K-step 2c and run 1 those of K-step 2c + 1, so the chunk fills the weight
+// rows of steps s + 2 and s + 3; then it loads chunk (s + 6) / 2.  The
+// MFMAs run in two passes (pass H takes 16-byte chunk 2g + H of every row,
+// g = lane / 32, for A and B alike); the fragments of pass 1 are read from
+// LDS during pass 0 and those of the next step's pass 0 during pass 1, so a
+// stage is read during steps s - 1 and s and written during s - 2 or s - 3.
+// Indices past the end are clamped (their loads and writes land in stages
+// that are never read), so the loop body has no branches; k must be a
+// multiple of 128 (four steps per iteration).
+using namespace pipe;
+
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void ds_write16(uint8_t *p, u32x4v v) {
+  const uint32_t off = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)p;
+  asm volatile("ds_write_b128 %0, %1" : : "v"(off), "v"(v));
+}
+
+// Fragments of one MFMA pass: A of tiles 0..3, then B of tiles 0..3.
+struct Pass {
+  u32x4v x[8];
+};
+
+__device__ __forceinline__ void wait_pass(Pass &P) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(P.x[0]), "+v"(P.x[1]), "+v"(P.x[2]), "+v"(P.x[3]));
+  asm volatile("" : "+v"(P.x[4]), "+v"(P.x[5]), "+v"(P.x[6]), "+v"(P.x[7]));
+}
+
+// LDS address of fragment f (0..3 A tiles, 4..7 B tiles) of pass H.
+__device__ __forceinline__ const uint8_t *pass_addr(const uint8_t *S, int f, int H, int wm, int wn, int lane) {
+  const int t = f & 3, r = (f < 4 ? 128 * wm : 128 * wn) + 32 * t + (lane & 31);
+  return S + (f < 4 ? 0 : P_B) + r * 64 + 16 * ((2 * (lane >> 5) + H) ^ swz(r));
+}
+
+__device__ __forceinline__ bf16x8 as_bf16(u32x4v v) { return __builtin_bit_cast(bf16x8, v); }
+
+// The 16 MFMAs of one pass on `cur`, each followed by one LDS read of the
+// pass `nxt` (stage S, pass H), pinned in that order so the reads run under
+// the matrix work.
+__device__ __forceinline__ void mfma_pass(const Pass &cur, Pass &nxt, const uint8_t *S, int H,
+                                          f32x16 (&acc)[4][4], int wm, int wn, int lane) {
+  static_for<4>([&](auto I) {
+    static_for<4>([&](auto J) {
+      acc[I][J] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16(cur.x[I]), as_bf16(cur.x[4 + J]), acc[I][J], 0, 0,
+                                                          0);
+      if constexpr (J == 0 || J == 2) {
+        constexpr int f = 2 * I + J / 2;
+        __builtin_amdgcn_sched_barrier(0x6);  // VALU / SALU may cross
+        nxt.x[f] = ds_read16(pass_addr(S, f, H, wm, wn, lane));
+        __builtin_amdgcn_sched_barrier(0x6);
+      }
+    });
+  });
+}
+
+__device__ __forceinline__ void write_runs(uint8_t *S0, uint8_t *S1, int row, int h, const uint32_t (&o)[16]) {
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      ds_write16((r ? S1 : S0) + P_B + row * 64 + 16 * ((2 * h + q) ^ swz(row)),
+                 (u32x4v){o[8 * r + 4 * q], o[8 * r + 4 * q + 1], o[8 * r + 4 * q + 2], o[8 * r + 4 * q + 3]});
+}
+
+// Activation chunk `lane % 4` of rows 64 wave + 16 j + lane / 4 (j < 4).
+__device__ __forceinline__ void write_a(uint8_t *S, int wave, int lane, const u32x4v (&a)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 64 * wave + 16 * j + (lane >> 2);
+    ds_write16(S + r * 64 + 16 * ((lane & 3) ^ swz(r)), a[j]);
+  }
+}
+
+__device__ __forceinline__ void load_a(const uint8_t *const (&src)[4], int64_t s, u32x4v (&a)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) a[j] = *reinterpret_cast<const u32x4v *>(src[j] + 64 * s);
+}
+
+__device__ __forceinline__ void wait_lds_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+template <class F>
+__global__ __launch_bounds__(256) void k_qgemm_pipe(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
+                                                    const uint16_t *__restrict__ x, int64_t m, int64_t n,
+                                                    int64_t k, void *__restrict__ y, int ytype) {
+  __shared__ __attribute__((aligned(1024))) uint8_t S0[P_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t S1[P_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t S2[P_STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t S3[P_STAGE];
+  uint8_t *const SB[4] = {S0, S1, S2, S3};
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.y * 256, n0 = (int64_t)blockIdx.x * 256;
+  const int64_t nk = k / 32;
+  const int last = (int)nk - 1;
+
+  // Activation rows past m re-read row m - 1 and weight rows past n re-read
+  // row n - 1; their results are never stored.
+  const uint8_t *asrc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t gm = m0 + 64 * wave + 16 * j + (lane >> 2);
+    asrc[j] = reinterpret_cast<const uint8_t *>(x + (gm < m ? gm : m - 1) * k) + 16 * (lane & 3);
+  }
+  const int h = tid & 1, br = tid >> 1;
+  const uint64_t rk0 = (uint64_t)(n0 + br < n ? n0 + br : n - 1) * (uint64_t)k;
+  const uint64_t rk1 = (uint64_t)(n0 + br + 128 < n ? n0 + br + 128 : n - 1) * (uint64_t)k;
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = (f32x16){0};
+
+  // Prologue: stages 0 and 1 written, activations of steps 2 and 3 and the
+  // pieces of chunk 1 in flight, pass 0 of step 0 read.
+  u32x4v ra[2][4];
+  typename F::Piece pb[2][2];  // [chunk % 2][row]: chunks c + 1 and c + 2 in flight
+  {
+    u32x4v a0[4], a1[4];
+    load_a(asrc, 0, a0);
+    load_a(asrc, 1, a1);
+    const typename F::Piece p0 = F::load_e(w, aux, rk0, h), p1 = F::load_e(w, aux, rk1, h);
+    load_a(asrc, 2 < nk ? 2 : last, ra[0]);
+    load_a(asrc, 3 < nk ? 3 : last, ra[1]);
+    // piece h of chunks 1 and 2 (clamped to the last chunk)
+    const int c1 = (2 < nk ? 2 : last - 1) + h, c2 = (4 < nk ? 4 : last - 1) + h;
+    pb[1][0] = F::load_e(w, aux, rk0, c1);
+    pb[1][1] = F::load_e(w, aux, rk1, c1);
+    pb[0][0] = F::load_e(w, aux, rk0, c2);
+    pb[0][1] = F::load_e(w, aux, rk1, c2);
+    write_a(S0, wave, lane, a0);
+    write_a(S1, wave, lane, a1);
+    uint32_t o[16];
+    F::decode_bf16(p0, o);
+    write_runs(S0, S1, br, h, o);
+    F::decode_bf16(p1, o);
+    write_runs(S0, S1, br + 128, h, o);
+  }
+  wait_lds_all();
+  __builtin_amdgcn_s_barrier();
+  Pass P0, P1;
+#pragma unroll
+  for (int f = 0; f < 8; ++f) P0.x[f] = ds_read16(pass_addr(S0, f, 0, wm, wn, lane));
+  wait_pass(P0);
+
+  // Step s, stage buffer B = s % 4 (P0 holds pass 0 of step s on entry and
+  // pass 0 of step s + 1 on exit).
+  auto step = [&](int64_t s, auto Bc) {
+    constexpr int B = decltype(Bc)::value;
+    __builtin_amdgcn_s_barrier();
+    // The decode has no memory operations, so it can be scheduled among
+    // the MFMAs; the LDS writes and the next loads follow the matrix work.
+    // chunk (s + 2) / 2 sits in slot ((s + 2) / 2) % 2 = (B / 2 + 1) % 2
+    constexpr int SL = ((B >> 1) + 1) & 1;
+    uint32_t o0[16], o1[16];
+    if constexpr ((B & 1) == 0) {
+      F::decode_bf16(pb[SL][0], o0);
+      F::decode_bf16(pb[SL][1], o1);
+    }
+    mfma_pass(P0, P1, SB[B], 1, acc, wm, wn, lane);
+    wait_pass(P1);
+    mfma_pass(P1, P0, SB[(B + 1) & 3], 0, acc, wm, wn, lane);
+    write_a(SB[(B + 2) & 3], wave, lane, ra[B & 1]);
+    load_a(asrc, s + 4 < nk ? s + 4 : last, ra[B & 1]);
+    if constexpr ((B & 1) == 0) {
+      write_runs(SB[(B + 2) & 3], SB[(B + 3) & 3], br, h, o0);
+      write_runs(SB[(B + 2) & 3], SB[(B + 3) & 3], br + 128, h, o1);
+      const int pn = (int)(s + 6 < nk ? s + 6 : last - 1) + h;  // piece h of chunk (s + 6) / 2
+      pb[SL][0] = F::load_e(w, aux, rk0, pn);
+      pb[SL][1] = F::load_e(w, aux, rk1, pn);
+    }
+    wait_pass(P0);
+    wait_lds_all();
+  };
+  for (int64_t t = 0; t < nk; t += 4) {
+    step(t, std::integral_constant<int, 0>{});
+    step(t + 1, std::integral_constant<int, 1>{});
+    step(t + 2, std::integral_constant<int, 2>{});
+    step(t + 3, std::integral_constant<int, 3>{});
+  }
+
+  const bool vec = vec_stores_ok(y, n);
+  const float one[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  static_for<4>([&](auto I) {
+    static_for<4>([&](auto J) {
+      store_tile32<false>(acc[I][J], y, ytype, m, n, m0 + 128 * wm + I * 32, n0 + 128 * wn + J * 32, one, one,
+                          nullptr, nullptr, lane, vec);
+    });
+  });
+}
+
 // y = sum over s < splits of part[s] (f32 partials of m * n outputs).
 __global__ __launch_bounds__(256) void k_splitk_sum(const float *__restrict__ part, int splits, int64_t mn,
                                                     void *__restrict__ y, int ytype) {
@@ -189,10 +396,20 @@ int launch(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hi
 }
 
 template <class F>
+int launch_pipe(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {
+  const dim3 grid((unsigned)((wt->n + 255) / 256), (unsigned)((m + 255) / 256));
+  hipLaunchKernelGGL((k_qgemm_pipe<F>), grid, dim3(256), 0, s, wt->data, wt->data + wt->aux_off,
+                     static_cast<const uint16_t *>(x), m, wt->n, wt->k, y, ytype);
+  return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemm launch failed");
+}
+
+template <class F>
 int by_m(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {
   if (m <= 64) return launch<F, 64, 128, 2, 2>(wt, x, m, y, ytype, s);
-  // 256 x 256 tiles when they still give every CU a workgroup, else 128 x 128.
+  // 256 x 256 tiles when they still give every CU a workgroup (pipelined
+  // when K is a multiple of 128), else 128 x 128.
   const int64_t big_tiles = ((m + 255) / 256) * ((wt->n + 255) / 256);
+  if (big_tiles >= 256 && wt->k % 128 == 0) return launch_pipe<F>(wt, x, m, y, ytype, s);
   if (big_tiles >= 256) return launch<F, 256, 256, 2, 4>(wt, x, m, y, ytype, s);
   return launch<F, 128, 128, 2, 2>(wt, x, m, y, ytype, s);
 }

@@ -178,16 +178,28 @@ __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
 // M = 1, long rows (P > 64 pieces): one wave per row, PPL pieces per lane
 // (piece lane + 64 i), activations in registers; the wave walks rows with a
 // grid stride and loads the next row's pieces before it computes the
-// current one, so about PPL x 2 pieces per lane are in flight.  No barriers:
-// the row total is a DPP sum over the wave.
-template <class F, int PPL>
-__global__ __launch_bounds__(256) void k_gemv_long(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
-                                                   const void *__restrict__ x, int xtype, void *__restrict__ y,
-                                                   int ytype, int64_t n, int64_t k, bool xlds) {
+// current one, so about PPL x 2 pieces per lane are in flight.  No barriers
+// in the loop: the row total is a DPP sum over the wave.  WPG waves per
+// workgroup share one LDS copy of x; the first row's weight loads are
+// issued before it is staged.
+template <class F, int PPL, int WPG>
+__global__ __launch_bounds__(64 * WPG) void k_gemv_long(const uint8_t *__restrict__ w,
+                                                        const uint8_t *__restrict__ aux, const void *__restrict__ x,
+                                                        int xtype, void *__restrict__ y, int ytype, int64_t n,
+                                                        int64_t k, bool xlds) {
   const int lane = threadIdx.x & 63;
   const int P = (int)(k / F::PE);
-  const int64_t nw = (int64_t)gridDim.x * 4;
-  int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t nw = (int64_t)gridDim.x * WPG;
+  int64_t row = (int64_t)blockIdx.x * WPG + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  // Unconditional loads of clamped pieces and rows (see k_gemv_m1): the
+  // next row's loads stay in flight while the current row is computed.
+  int pc[PPL];
+#pragma unroll
+  for (int i = 0; i < PPL; ++i) pc[i] = lane + 64 * i < P ? lane + 64 * i : P - 1;
+  typename F::Piece cur[PPL];
+#pragma unroll
+  for (int i = 0; i < PPL; ++i) cur[i] = F::load(w, aux, row < n ? row : n - 1, k, pc[i]);
 
   extern __shared__ __attribute__((aligned(16))) float xs_dyn[];
   const float *xs = nullptr;
@@ -214,15 +226,6 @@ __global__ __launch_bounds__(256) void k_gemv_long(const uint8_t *__restrict__ w
     }
   }
 
-  // Unconditional loads of clamped pieces and rows (see k_gemv_m1): the
-  // next row's loads stay in flight while the current row is computed.
-  if (row >= n) return;
-  int pc[PPL];
-#pragma unroll
-  for (int i = 0; i < PPL; ++i) pc[i] = lane + 64 * i < P ? lane + 64 * i : P - 1;
-  typename F::Piece cur[PPL];
-#pragma unroll
-  for (int i = 0; i < PPL; ++i) cur[i] = F::load(w, aux, row, k, pc[i]);
   for (; row < n; row += nw) {
     const int64_t rn = row + nw;
     const int64_t rl = rn < n ? rn : row;
@@ -341,10 +344,19 @@ int run_long(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, 
   // 16 waves per CU walking rows: enough weight bytes in flight to cover
   // HBM latency, few enough that every wave sees several rows.
   const int64_t waves = wt->n < 256 * 16 ? wt->n : 256 * 16;
-  const unsigned blocks = (unsigned)((waves + 3) / 4);
   const size_t xb = xlds_bytes(wt->k);
-  hipLaunchKernelGGL((k_gemv_long<F, PPL>), dim3(blocks), dim3(256), xb, s, wt->data, wt->data + wt->aux_off, x,
-                     xtype, y, ytype, wt->n, wt->k, xb != 0);
+  // Eight waves per workgroup (measured best of 4 / 8 / 16 on 14336 x 4096)
+  // for PPL <= 2; longer rows keep four (the Q6_K decode at PPL = 3 would
+  // not fit eight waves' registers).
+  if constexpr (PPL <= 2) {
+    const unsigned blocks = (unsigned)((waves + 7) / 8);
+    hipLaunchKernelGGL((k_gemv_long<F, PPL, 8>), dim3(blocks), dim3(512), xb, s, wt->data, wt->data + wt->aux_off, x,
+                       xtype, y, ytype, wt->n, wt->k, xb != 0);
+  } else {
+    const unsigned blocks = (unsigned)((waves + 3) / 4);
+    hipLaunchKernelGGL((k_gemv_long<F, PPL, 4>), dim3(blocks), dim3(256), xb, s, wt->data, wt->data + wt->aux_off, x,
+                       xtype, y, ytype, wt->n, wt->k, xb != 0);
+  }
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }
 
