@@ -256,15 +256,17 @@ def extra_prefill(torch, rq, synth, dev, steps, warmup):
         y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
         w.forward(x, out=y)
         torch.cuda.synchronize()
-        reps = 3 if n * k > 1e8 else max(3, steps // 2)
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        t0.record()
-        for _ in range(reps):
-            w.forward(x, out=y)
-        t1.record()
-        torch.cuda.synchronize()
-        ms = t0.elapsed_time(t1) / reps
+        # launches captured in one graph (the split-K shapes allocate their
+        # partials stream-ordered inside it), timed over replays
+        reps = 3 if n * k > 1e8 else 10
+
+        def launches():
+            for _ in range(reps):
+                w.forward(x, out=y)
+
+        g = capture(torch, launches)
+        ms = Timer(torch).replay(g, 2 if n * k > 1e8 else max(2, steps // 4), 1) / reps
+        del g
         tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
         res.append({"shape": f"{name} {n}x{k}", "ms": round(ms, 4), "TFLOP/s": round(tf, 2),
                     "frac_mfma_bf16": round(tf / BF16_PEAK_TFLOPS, 4)})
