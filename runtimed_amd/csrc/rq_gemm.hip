@@ -169,16 +169,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restric
 // multiple of 128 (four steps per iteration).
 using namespace pipe;
 
-typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ void ds_write16(uint8_t *p, u32x4v v) {
-  const uint32_t off = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)p;
-  asm volatile("ds_write_b128 %0, %1" : : "v"(off), "v"(v));
-}
-
 // Fragments of one MFMA pass: A of tiles 0..3, then B of tiles 0..3.
 struct Pass {
-  u32x4v x[8];
+  u32x4 x[8];
 };
 
 __device__ __forceinline__ void wait_pass(Pass &P) {
@@ -192,7 +185,7 @@ __device__ __forceinline__ const uint8_t *pass_addr(const uint8_t *S, int f, int
   return S + (f < 4 ? 0 : P_B) + r * 64 + 16 * ((2 * (lane >> 5) + H) ^ swz(r));
 }
 
-__device__ __forceinline__ bf16x8 as_bf16(u32x4v v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ bf16x8 as_bf16(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // The 16 MFMAs of one pass on `cur`, each followed by one LDS read of the
 // pass `nxt` (stage S, pass H), pinned in that order so the reads run under
@@ -219,11 +212,11 @@ __device__ __forceinline__ void write_runs(uint8_t *S0, uint8_t *S1, int row, in
 #pragma unroll
     for (int q = 0; q < 2; ++q)
       ds_write16((r ? S1 : S0) + P_B + row * 64 + 16 * ((2 * h + q) ^ swz(row)),
-                 (u32x4v){o[8 * r + 4 * q], o[8 * r + 4 * q + 1], o[8 * r + 4 * q + 2], o[8 * r + 4 * q + 3]});
+                 (u32x4){o[8 * r + 4 * q], o[8 * r + 4 * q + 1], o[8 * r + 4 * q + 2], o[8 * r + 4 * q + 3]});
 }
 
 // Activation chunk `lane % 4` of rows 64 wave + 16 j + lane / 4 (j < 4).
-__device__ __forceinline__ void write_a(uint8_t *S, int wave, int lane, const u32x4v (&a)[4]) {
+__device__ __forceinline__ void write_a(uint8_t *S, int wave, int lane, const u32x4 (&a)[4]) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = 64 * wave + 16 * j + (lane >> 2);
@@ -231,9 +224,9 @@ __device__ __forceinline__ void write_a(uint8_t *S, int wave, int lane, const u3
   }
 }
 
-__device__ __forceinline__ void load_a(const uint8_t *const (&src)[4], int64_t s, u32x4v (&a)[4]) {
+__device__ __forceinline__ void load_a(const uint8_t *const (&src)[4], int64_t s, u32x4 (&a)[4]) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) a[j] = *reinterpret_cast<const u32x4v *>(src[j] + 64 * s);
+  for (int j = 0; j < 4; ++j) a[j] = *reinterpret_cast<const u32x4 *>(src[j] + 64 * s);
 }
 
 __device__ __forceinline__ void wait_lds_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
@@ -273,10 +266,10 @@ __global__ __launch_bounds__(256) void k_qgemm_pipe(const uint8_t *__restrict__ 
 
   // Prologue: stages 0 and 1 written, activations of steps 2 and 3 and the
   // pieces of chunk 1 in flight, pass 0 of step 0 read.
-  u32x4v ra[2][4];
+  u32x4 ra[2][4];
   typename F::Piece pb[2][2];  // [chunk % 2][row]: chunks c + 1 and c + 2 in flight
   {
-    u32x4v a0[4], a1[4];
+    u32x4 a0[4], a1[4];
     load_a(asrc, 0, a0);
     load_a(asrc, 1, a1);
     const typename F::Piece p0 = F::load_e(w, aux, rk0, h), p1 = F::load_e(w, aux, rk1, h);

@@ -26,7 +26,8 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((VM & 0xF) | ((VM >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// LDS operand reads are issued as explicit ds_read_b128 and completed by one
+// LDS operand reads (and writes) are issued as explicit ds_read_b128 /
+// ds_write_b128; reads are completed by one
 // s_waitcnt lgkmcnt(0) that takes every loaded register as an operand, so no
 // use can be scheduled before the wait.  (As compiler-visible LDS loads they
 // would each be preceded by a wait for all in-flight direct loads, because
@@ -38,6 +39,11 @@ __device__ __forceinline__ u32x4 ds_read16(const uint8_t *p) {
   const uint32_t off = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
   asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(off));
   return v;
+}
+
+__device__ __forceinline__ void ds_write16(uint8_t *p, u32x4 v) {
+  const uint32_t off = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)p;
+  asm volatile("ds_write_b128 %0, %1" : : "v"(off), "v"(v));
 }
 
 // Fragment registers of one K-step: 8 x 16 bytes of A rows, 8 of B rows.

@@ -1,10 +1,11 @@
-"""The pipelined FP8 GEMM issues its LDS fragment reads as explicit
-ds_read_b128 instructions and completes them with one explicit
+"""The pipelined FP8 and quantized bf16 GEMMs issue their LDS fragment reads
+as explicit ds_read_b128 instructions and complete them with one explicit
 s_waitcnt lgkmcnt(0) (the compiler cannot see these reads, so it cannot
-order their uses).  This test compiles rq_fp8.hip to gfx950 assembly and
-checks, instruction by instruction, that no register written by such a read
-is read or overwritten before the wait that completes it: a register copied
-or reused early would hold stale data, or be clobbered when the read lands."""
+order their uses).  This test compiles rq_fp8.hip and rq_gemm.hip to gfx950
+assembly and checks, instruction by instruction, that no register written by
+such a read is read or overwritten before the wait that completes it: a
+register copied or reused early would hold stale data, or be clobbered when
+the read lands."""
 import re
 import shutil
 import subprocess
@@ -60,17 +61,30 @@ def test_checker_flags_an_early_use():
     assert reads == 1 and [b[0] for b in bad] == [2]
 
 
-@pytest.mark.skipif(shutil.which(HIPCC) is None and not Path(HIPCC).exists(), reason="hipcc not present")
-def test_fp8_pipe_lds_reads_complete_before_use(tmp_path):
-    out = tmp_path / "fp8.s"
+def _check(tmp_path, src: str, pattern: str, min_reads: int):
+    out = tmp_path / (Path(src).stem + ".s")
     cmd = [HIPCC, "-O3", "-std=c++17", "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang",
            "-packed-fp32-ops", "--cuda-device-only", "-S", "-x", "hip",
-           str(ROOT / "runtimed_amd" / "csrc" / "rq_fp8.hip"), "-o", str(out)]
+           str(ROOT / "runtimed_amd" / "csrc" / src), "-o", str(out)]
     subprocess.run(cmd, check=True, capture_output=True)
     lines = out.read_text().splitlines()
-    kernels = [m.group(1) for l in lines if (m := re.match(r"^(_Z\S*k_fp8_gemm_pipe\S*):", l))]
-    assert kernels, "pipelined kernel not found in the assembly"
+    kernels = [m.group(1) for l in lines if (m := re.match(r"^(_Z\S*" + pattern + r"\S*):", l))]
+    assert kernels, f"{pattern} not found in the assembly"
     for kern in kernels:
         bad, reads = early_uses(lines, kern)
-        assert reads >= 16
-        assert not bad, bad[:5]
+        assert reads >= min_reads, (kern, reads)
+        assert not bad, (kern, bad[:5])
+
+
+HAVE_HIPCC = shutil.which(HIPCC) is not None or Path(HIPCC).exists()
+
+
+@pytest.mark.skipif(not HAVE_HIPCC, reason="hipcc not present")
+def test_fp8_pipe_lds_reads_complete_before_use(tmp_path):
+    _check(tmp_path, "rq_fp8.hip", "k_fp8_gemm_pipe", 16)
+
+
+@pytest.mark.skipif(not HAVE_HIPCC, reason="hipcc not present")
+def test_qgemm_pipe_lds_reads_complete_before_use(tmp_path):
+    # one kernel per GGUF format; 8 reads of the first pass plus 16 per step
+    _check(tmp_path, "rq_gemm.hip", "k_qgemm_pipe", 24)
