@@ -12,8 +12,11 @@ captured once as a HIP graph and replayed.  value = algorithmic bytes per step
 The same JSON line carries the roofline of the dominant kernel (the gate/up
 projection GEMV, timed in its own graph of R launches), a CPU baseline (the
 oracle's runtimed-gguf dequant + f32 GEMV on this host's cores) and, under
-"extra", the other workloads: the Q8_0 GEMV, the small-M verify sweep, the
-M=512 prefill GEMMs and the FP8 e4m3 GEMM.
+"extra", the other workloads: the decode set with fused weights, the Q8_0
+GEMV, the streaming-shape Q4_K GEMV, the small-M verify sweep (bf16 and f32
+activations), the M=512 prefill GEMMs, the FP8 e4m3 GEMM, the Marlin INT4
+GEMV, the paged-KV quantizer, the GGUF upload and a vendor-BLAS reference
+point.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -222,11 +225,13 @@ def extra_large_gemv(torch, rq, synth, dev, steps, warmup):
             "GB/s": round(b / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
-def extra_verify(torch, rq, W, dev, steps, warmup):
+def extra_verify(torch, rq, W, dev, steps, warmup, dtype=None, ms_list=(1, 2, 4, 8, 16, 64)):
+    dt = dtype if dtype is not None else torch.bfloat16
+    eb = 4 if dt == torch.float32 else 2
     out = []
-    for m in (1, 2, 4, 8, 16, 64):
-        xs = {k: torch.randn((m, k), device=dev).to(torch.bfloat16) for k in (896, 4864)}
-        ys = {name: torch.empty((m, n), dtype=torch.bfloat16, device=dev) for name, n, k in LAYER}
+    for m in ms_list:
+        xs = {k: torch.randn((m, k), device=dev).to(dt) for k in (896, 4864)}
+        ys = {name: torch.empty((m, n), dtype=dt, device=dev) for name, n, k in LAYER}
 
         def tok():
             for lw in W:
@@ -235,13 +240,14 @@ def extra_verify(torch, rq, W, dev, steps, warmup):
 
         g = capture(torch, tok)
         ms = Timer(torch).replay(g, max(2, steps // 4), 1)
-        b = layer_bytes(2, 2, m) * len(W)
+        b = layer_bytes(eb, eb, m) * len(W)
         fl = 2.0 * m * sum(n * k for _, n, k in LAYER) * len(W)
         out.append({"m": m, "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
                     "TFLOP/s": round(fl / (ms * 1e-3) / 1e12, 3),
                     "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
         del g
-    return {"workload": "verify sweep, Qwen2-0.5B Q4_K layer, bf16 activations", "sweep": out}
+    name = "bf16" if dt == torch.bfloat16 else "f32 (the reference's compute type)"
+    return {"workload": f"verify sweep, Qwen2-0.5B Q4_K layer, {name} activations", "sweep": out}
 
 
 def extra_prefill(torch, rq, synth, dev, steps, warmup):
@@ -589,6 +595,8 @@ def main():
                          ("q8_0_gemv", lambda: extra_q8_gemv(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("q4_k_gemv_large", lambda: extra_large_gemv(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("verify", lambda: extra_verify(torch, rq, W[:32], dev, args.steps, args.warmup)),
+                         ("verify_f32", lambda: extra_verify(torch, rq, W[:32], dev, args.steps, args.warmup,
+                                                             torch.float32, (2, 4, 16, 64))),
                          ("prefill", lambda: extra_prefill(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("fp8_gemm", lambda: extra_fp8(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("marlin_int4_gemv", lambda: extra_marlin(torch, rq, dev, args.steps, args.warmup)),

@@ -85,6 +85,10 @@ int launch_linear_mfma(const rq_weight *w, const void *x, int64_t m, void *y, in
 // verify), RQ_E_UNSUPPORTED outside that or for formats it has no decoder for.
 int launch_linear_smallm(const rq_weight *w, const void *x, int64_t m, void *y, int ytype,
                          hipStream_t s);
+// The same for f32 / f16 activations on the f32 matrix cores with exact f32
+// weights (f32 accumulation).
+int launch_linear_smallm_f32(const rq_weight *wt, const void *x, int xtype, int64_t m, void *y, int ytype,
+                             hipStream_t s);
 // y = x * W^T with W dense f32 [n, k] in device memory.
 int launch_linear_dense_f32(const float *w, int64_t n, int64_t k, const void *x, int xtype,
                             int64_t m, void *y, int ytype, hipStream_t s);

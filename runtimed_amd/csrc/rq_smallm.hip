@@ -1,5 +1,7 @@
-// rq_smallm.hip -- quantized linear y = x W^T for 2 <= M <= 64 bf16
-// activation rows (speculative verify) on the matrix cores.
+// rq_smallm.hip -- quantized linear y = x W^T for 2 <= M <= 64 activation
+// rows (speculative verify) on the matrix cores: bf16 activations on
+// v_mfma_f32_16x16x32_bf16, f32 / f16 activations on v_mfma_f32_16x16x4_f32
+// with exact f32 weights (second half of the file).
 //
 // The weight rows are the MFMA A operand (v_mfma_f32_16x16x32_bf16: lane l
 // holds row l % 16 and 8 k-values chosen by l / 16) and the activation rows
@@ -50,7 +52,8 @@ struct SmQ4K {
     ch.q = *reinterpret_cast<const uint2 *>(bp + 16 + 32 * ch.c + 8 * g);
     return ch;
   }
-  __device__ static void decode(const Chunk &ch, uint32_t (&o)[8]) {
+  template <class E>
+  __device__ static void decode_with(const Chunk &ch, int, E &&emit) {
     FmtQ4K::Piece pc;
     pc.hd = ch.hd;
     pc.c = ch.c;
@@ -60,10 +63,10 @@ struct SmQ4K {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const uint32_t lo = q[j] & 0x0F0F0F0Fu, hi = (q[j] >> 4) & 0x0F0F0F0Fu;
-      o[2 * j] = pk_bf16(fmaf(ub(lo, 0), a0, -b0), fmaf(ub(lo, 1), a0, -b0));
-      o[2 * j + 1] = pk_bf16(fmaf(ub(lo, 2), a0, -b0), fmaf(ub(lo, 3), a0, -b0));
-      o[4 + 2 * j] = pk_bf16(fmaf(ub(hi, 0), a1, -b1), fmaf(ub(hi, 1), a1, -b1));
-      o[4 + 2 * j + 1] = pk_bf16(fmaf(ub(hi, 2), a1, -b1), fmaf(ub(hi, 3), a1, -b1));
+      emit(2 * j, fmaf(ub(lo, 0), a0, -b0), fmaf(ub(lo, 1), a0, -b0));
+      emit(2 * j + 1, fmaf(ub(lo, 2), a0, -b0), fmaf(ub(lo, 3), a0, -b0));
+      emit(4 + 2 * j, fmaf(ub(hi, 0), a1, -b1), fmaf(ub(hi, 1), a1, -b1));
+      emit(4 + 2 * j + 1, fmaf(ub(hi, 2), a1, -b1), fmaf(ub(hi, 3), a1, -b1));
     }
   }
 };
@@ -94,7 +97,8 @@ struct SmQ6K {
     c.d = reinterpret_cast<const uint16_t *>(aux)[blk];
     return c;
   }
-  __device__ static void decode(const Chunk &c, uint32_t (&o)[8], int g) {
+  template <class E>
+  __device__ static void decode_with(const Chunk &c, int g, E &&emit) {
     const float d = h2f(c.d);
     // l / 16 = g / 2 for both runs of this lane group
     const int sb = g >> 1;
@@ -108,10 +112,10 @@ struct SmQ6K {
       const uint32_t h = hh[j] >> sh;
       const uint32_t q0 = ((a[j] >> sh) & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
       const uint32_t q1 = ((b[j] >> sh) & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
-      o[2 * j] = pk_bf16(fmaf(ub(q0, 0), s0, z0), fmaf(ub(q0, 1), s0, z0));
-      o[2 * j + 1] = pk_bf16(fmaf(ub(q0, 2), s0, z0), fmaf(ub(q0, 3), s0, z0));
-      o[4 + 2 * j] = pk_bf16(fmaf(ub(q1, 0), s1, z1), fmaf(ub(q1, 1), s1, z1));
-      o[4 + 2 * j + 1] = pk_bf16(fmaf(ub(q1, 2), s1, z1), fmaf(ub(q1, 3), s1, z1));
+      emit(2 * j, fmaf(ub(q0, 0), s0, z0), fmaf(ub(q0, 1), s0, z0));
+      emit(2 * j + 1, fmaf(ub(q0, 2), s0, z0), fmaf(ub(q0, 3), s0, z0));
+      emit(4 + 2 * j, fmaf(ub(q1, 0), s1, z1), fmaf(ub(q1, 1), s1, z1));
+      emit(4 + 2 * j + 1, fmaf(ub(q1, 2), s1, z1), fmaf(ub(q1, 3), s1, z1));
     }
   }
 };
@@ -131,15 +135,16 @@ struct SmQ8 {
     c.d = *reinterpret_cast<const uint32_t *>(aux + 2 * (e >> 5));
     return c;
   }
-  __device__ static void decode(const Chunk &c, uint32_t (&o)[8]) {
+  template <class E>
+  __device__ static void decode_with(const Chunk &c, int, E &&emit) {
     const float d0 = h2f(c.d), d1 = h2f(c.d >> 16);
     const uint32_t a[2] = {c.a.x, c.a.y}, b[2] = {c.b.x, c.b.y};
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      o[2 * j] = pk_bf16(d0 * (float)(int8_t)(a[j] & 0xFFu), d0 * (float)(int8_t)((a[j] >> 8) & 0xFFu));
-      o[2 * j + 1] = pk_bf16(d0 * (float)(int8_t)((a[j] >> 16) & 0xFFu), d0 * (float)(int8_t)(a[j] >> 24));
-      o[4 + 2 * j] = pk_bf16(d1 * (float)(int8_t)(b[j] & 0xFFu), d1 * (float)(int8_t)((b[j] >> 8) & 0xFFu));
-      o[4 + 2 * j + 1] = pk_bf16(d1 * (float)(int8_t)((b[j] >> 16) & 0xFFu), d1 * (float)(int8_t)(b[j] >> 24));
+      emit(2 * j, d0 * (float)(int8_t)(a[j] & 0xFFu), d0 * (float)(int8_t)((a[j] >> 8) & 0xFFu));
+      emit(2 * j + 1, d0 * (float)(int8_t)((a[j] >> 16) & 0xFFu), d0 * (float)(int8_t)(a[j] >> 24));
+      emit(4 + 2 * j, d1 * (float)(int8_t)(b[j] & 0xFFu), d1 * (float)(int8_t)((b[j] >> 8) & 0xFFu));
+      emit(4 + 2 * j + 1, d1 * (float)(int8_t)((b[j] >> 16) & 0xFFu), d1 * (float)(int8_t)(b[j] >> 24));
     }
   }
 };
@@ -161,7 +166,8 @@ struct SmQ5K {
     ch.h = *reinterpret_cast<const uint2 *>(bp + 16 + 8 * g);
     return ch;
   }
-  __device__ static void decode(const Chunk &ch, uint32_t (&o)[8]) {
+  template <class E>
+  __device__ static void decode_with(const Chunk &ch, int, E &&emit) {
     FmtQ4K::Piece pc;
     pc.hd = ch.hd;
     pc.c = ch.c;
@@ -173,10 +179,10 @@ struct SmQ5K {
       const uint32_t h = hh[j] >> (2 * ch.c);
       const uint32_t lo = (q[j] & 0x0F0F0F0Fu) | ((h << 4) & 0x10101010u);
       const uint32_t hi = ((q[j] >> 4) & 0x0F0F0F0Fu) | ((h << 3) & 0x10101010u);
-      o[2 * j] = pk_bf16(fmaf(ub(lo, 0), a0, -b0), fmaf(ub(lo, 1), a0, -b0));
-      o[2 * j + 1] = pk_bf16(fmaf(ub(lo, 2), a0, -b0), fmaf(ub(lo, 3), a0, -b0));
-      o[4 + 2 * j] = pk_bf16(fmaf(ub(hi, 0), a1, -b1), fmaf(ub(hi, 1), a1, -b1));
-      o[4 + 2 * j + 1] = pk_bf16(fmaf(ub(hi, 2), a1, -b1), fmaf(ub(hi, 3), a1, -b1));
+      emit(2 * j, fmaf(ub(lo, 0), a0, -b0), fmaf(ub(lo, 1), a0, -b0));
+      emit(2 * j + 1, fmaf(ub(lo, 2), a0, -b0), fmaf(ub(lo, 3), a0, -b0));
+      emit(4 + 2 * j, fmaf(ub(hi, 0), a1, -b1), fmaf(ub(hi, 1), a1, -b1));
+      emit(4 + 2 * j + 1, fmaf(ub(hi, 2), a1, -b1), fmaf(ub(hi, 3), a1, -b1));
     }
   }
 };
@@ -209,7 +215,8 @@ struct SmQx0 {
     }
     return c;
   }
-  __device__ static void decode(const Chunk &c, uint32_t (&o)[8], int g) {
+  template <class E>
+  __device__ static void decode_with(const Chunk &c, int g, E &&emit) {
     const float z = Q5 ? 16.0f : 8.0f;
     const int sh = 4 * (g >> 1);
     const uint32_t qa[2] = {c.a.x, c.a.y}, qb[2] = {c.b.x, c.b.y};
@@ -221,20 +228,27 @@ struct SmQx0 {
       for (int j = 0; j < 2; ++j) {
         uint32_t v = ((r ? qb[j] : qa[j]) >> sh) & 0x0F0F0F0Fu;
         if (Q5) v |= spread4(hbits >> (4 * j)) << 4;
-        o[4 * r + 2 * j] = pk_bf16(fmaf(ub(v, 0), d, nz), fmaf(ub(v, 1), d, nz));
-        o[4 * r + 2 * j + 1] = pk_bf16(fmaf(ub(v, 2), d, nz), fmaf(ub(v, 3), d, nz));
+        emit(4 * r + 2 * j, fmaf(ub(v, 0), d, nz), fmaf(ub(v, 1), d, nz));
+        emit(4 * r + 2 * j + 1, fmaf(ub(v, 2), d, nz), fmaf(ub(v, 3), d, nz));
       }
     }
   }
 };
 
+// The 16 weights of lane group g as bf16 pairs (o[i]: weights 2i, 2i + 1) or
+// as exact f32 values (f[2i], f[2i + 1]); one fused multiply-add each, which
+// is the reference's single rounding (the scale times the code is exact).
 template <class C>
 __device__ __forceinline__ void decode_chunk(const typename C::Chunk &c, uint32_t (&o)[8], int g) {
-  if constexpr (__is_same(C, SmQ6K) || __is_same(C, SmQx0<false>) || __is_same(C, SmQx0<true>)) {
-    C::decode(c, o, g);
-  } else {
-    C::decode(c, o);
-  }
+  C::decode_with(c, g, [&](int i, float a, float b) { o[i] = pk_bf16(a, b); });
+}
+
+template <class C>
+__device__ __forceinline__ void decode_chunk_f32(const typename C::Chunk &c, float (&f)[16], int g) {
+  C::decode_with(c, g, [&](int i, float a, float b) {
+    f[2 * i] = a;
+    f[2 * i + 1] = b;
+  });
 }
 
 __device__ __forceinline__ bf16x8 pick(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1) {
@@ -281,6 +295,31 @@ __device__ __forceinline__ void mma_chunk(const typename C::Chunk &c, const XFra
   for (int ct = 0; ct < MT; ++ct)
     acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f1, pick(xf.a[ct].z, xf.a[ct].w, xf.b[ct].z, xf.b[ct].w),
                                                       acc[ct], 0, 0, 0);
+}
+
+// The NW waves' partial 16 x (16 MT) tiles summed through LDS and stored.
+// 16 x 16 C layout: lane l holds column (activation row) l % 16 and weight
+// rows 4 (l / 16) + i.  Thread t sums one lane slot of one column tile.
+template <int MT, int NW>
+__device__ __forceinline__ void reduce_store(f32x4 (&part)[NW][MT][64], const f32x4 (&acc)[MT], int wave, int lane,
+                                             int64_t m, int64_t n, int64_t n0, void *y, int ytype) {
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) part[wave][ct][lane] = acc[ct];
+  __syncthreads();
+  for (int slot = threadIdx.x; slot < MT * 64; slot += 64 * NW) {
+    const int ct = slot >> 6, l = slot & 63;
+    f32x4 v = part[0][ct][l];
+#pragma unroll
+    for (int q = 1; q < NW; ++q) v += part[q][ct][l];
+    const int64_t mr = 16 * ct + (l & 15);
+    if (mr < m) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t nr = n0 + 4 * (l >> 4) + i;
+        if (nr < n) store_one(y, ytype, mr * n + nr, v[i]);
+      }
+    }
+  }
 }
 
 // MT column tiles of 16 activation rows (M <= 16 MT); NW waves split K,
@@ -333,24 +372,131 @@ __global__ __launch_bounds__(64 * NW) void k_smallm(const uint8_t *__restrict__ 
     }
   }
 
+  reduce_store<MT, NW>(part, acc, wave, lane, m, n, n0, y, ytype);
+}
+
+// ---- f32 / f16 activations ------------------------------------------------
+//
+// The reference computes in f32; for f32 (or f16) activation rows the same
+// kernel runs on v_mfma_f32_16x16x4_f32 with the weights decoded to exact f32
+// (the reference's dequantized values) as the A operand and the activations
+// as the B operand, f32 products and accumulation.  A chunk's 16 weights of
+// lane group g take 16 MFMAs of K = 4, the four lane groups supplying the
+// four K slots: MFMA j pairs weight j of every lane group with the
+// activation at the same position (elements 8g + j, or 32 + 8g + j - 8).
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+template <int MT>
+struct XFragF {
+  f32x4v a[MT][4];  // elements 8g .. 8g + 7, then 32 + 8g .. 32 + 8g + 7
+};
+
+template <int MT, int XT>
+__device__ __forceinline__ void load_xf(XFragF<MT> &f, const uint8_t *const (&xr)[MT], int64_t t) {
 #pragma unroll
-  for (int ct = 0; ct < MT; ++ct) part[wave][ct][lane] = acc[ct];
-  __syncthreads();
-  // 16 x 16 C layout: lane l holds column (activation row) l % 16 and weight
-  // rows 4 (l / 16) + i.  Thread t sums one lane slot of one column tile.
-  for (int slot = threadIdx.x; slot < MT * 64; slot += 64 * NW) {
-    const int ct = slot >> 6, l = slot & 63;
-    f32x4 v = part[0][ct][l];
-#pragma unroll
-    for (int q = 1; q < NW; ++q) v += part[q][ct][l];
-    const int64_t mr = 16 * ct + (l & 15);
-    if (mr < m) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t nr = n0 + 4 * (l >> 4) + i;
-        if (nr < n) store_one(y, ytype, mr * n + nr, v[i]);
-      }
+  for (int ct = 0; ct < MT; ++ct) {
+    if constexpr (XT == RQ_F32) {
+      const float *p = reinterpret_cast<const float *>(xr[ct]) + 64 * t;
+      f.a[ct][0] = *reinterpret_cast<const f32x4v *>(p);
+      f.a[ct][1] = *reinterpret_cast<const f32x4v *>(p + 4);
+      f.a[ct][2] = *reinterpret_cast<const f32x4v *>(p + 32);
+      f.a[ct][3] = *reinterpret_cast<const f32x4v *>(p + 36);
+    } else {
+      typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+      const _Float16 *p = reinterpret_cast<const _Float16 *>(xr[ct]) + 64 * t;
+      const f16x8 lo = *reinterpret_cast<const f16x8 *>(p), hi = *reinterpret_cast<const f16x8 *>(p + 32);
+      f.a[ct][0] = (f32x4v){(float)lo[0], (float)lo[1], (float)lo[2], (float)lo[3]};
+      f.a[ct][1] = (f32x4v){(float)lo[4], (float)lo[5], (float)lo[6], (float)lo[7]};
+      f.a[ct][2] = (f32x4v){(float)hi[0], (float)hi[1], (float)hi[2], (float)hi[3]};
+      f.a[ct][3] = (f32x4v){(float)hi[4], (float)hi[5], (float)hi[6], (float)hi[7]};
     }
+  }
+}
+
+template <class C, int MT>
+__device__ __forceinline__ void mma_chunk_f32(const typename C::Chunk &c, const XFragF<MT> &xf, f32x4 (&acc)[MT],
+                                              int g, uint32_t vm) {
+  float f[16];
+  decode_chunk_f32<C>(c, f, g);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float wj = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, f[j]) & vm);
+#pragma unroll
+    for (int ct = 0; ct < MT; ++ct)
+      acc[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(wj, xf.a[ct][j >> 2][j & 3], acc[ct], 0, 0, 0);
+  }
+}
+
+template <class C, int MT, int NW, int B, int XT>
+__global__ __launch_bounds__(64 * NW) void k_smallm_f32(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
+                                                        const uint8_t *__restrict__ x, int64_t m,
+                                                        void *__restrict__ y, int ytype, int64_t n, int64_t k) {
+  __shared__ f32x4 part[NW][MT][64];
+  const int lane = threadIdx.x & 63, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const int64_t row = n0 + (lane & 15) < n ? n0 + (lane & 15) : n - 1;
+  const int64_t nk = k / 64;
+  constexpr int XB = XT == RQ_F32 ? 4 : 2;  // bytes per activation
+
+  const uint8_t *xr[MT];
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) {
+    const int64_t mr = 16 * ct + (lane & 15);
+    xr[ct] = x + ((mr < m ? mr : m - 1) * k + 8 * g) * XB;
+  }
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) acc[ct] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+  for (int64_t t = wave; t < nk; t += B * NW) {
+    typename C::Chunk c[B];
+    XFragF<MT> xf[B];
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      const int64_t ti = t + i * NW < nk ? t + i * NW : t;
+      c[i] = C::load(w, aux, row, k, ti, g);
+      load_xf<MT, XT>(xf[i], xr, ti);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      const uint32_t vm = i == 0 ? 0xFFFFFFFFu : opaque(t + i * NW < nk ? 0xFFFFFFFFu : 0u);
+      mma_chunk_f32<C, MT>(c[i], xf[i], acc, g, vm);
+    }
+  }
+
+  reduce_store<MT, NW>(part, acc, wave, lane, m, n, n0, y, ytype);
+}
+
+template <class C, int MT, int XT>
+int run_mt_f32(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {
+  constexpr int B = MT == 1 ? 4 : (MT == 2 ? 2 : 1);
+  const dim3 grid((unsigned)((wt->n + 15) / 16));
+  const uint8_t *aux = wt->data + wt->aux_off;
+  hipLaunchKernelGGL((k_smallm_f32<C, MT, 4, B, XT>), grid, dim3(256), 0, s, wt->data, aux,
+                     static_cast<const uint8_t *>(x), m, y, ytype, wt->n, wt->k);
+  return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "small-M launch failed");
+}
+
+template <class C, int XT>
+int run_f32(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {
+  if (m <= 16) return run_mt_f32<C, 1, XT>(wt, x, m, y, ytype, s);
+  if (m <= 32) return run_mt_f32<C, 2, XT>(wt, x, m, y, ytype, s);
+  return run_mt_f32<C, 4, XT>(wt, x, m, y, ytype, s);
+}
+
+template <int XT>
+int dispatch_f32(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {
+  switch (wt->qtype) {
+    case RQ_Q4_K: return run_f32<SmQ4K, XT>(wt, x, m, y, ytype, s);
+    case RQ_Q6_K: return run_f32<SmQ6K, XT>(wt, x, m, y, ytype, s);
+    case RQ_Q8_0: return run_f32<SmQ8, XT>(wt, x, m, y, ytype, s);
+    case RQ_Q5_K: return run_f32<SmQ5K, XT>(wt, x, m, y, ytype, s);
+    case RQ_Q4_0: return run_f32<SmQx0<false>, XT>(wt, x, m, y, ytype, s);
+    case RQ_Q5_0: return run_f32<SmQx0<true>, XT>(wt, x, m, y, ytype, s);
+    default: return RQ_E_UNSUPPORTED;
   }
 }
 
@@ -377,6 +523,16 @@ int run(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipSt
 }
 
 }  // namespace
+
+// f32 / f16 activations, 2 <= m <= 64, k % 64 == 0, 16-byte aligned x
+// (dispatched from m = 4).
+int launch_linear_smallm_f32(const rq_weight *wt, const void *x, int xtype, int64_t m, void *y, int ytype,
+                             hipStream_t s) {
+  if (m < 2 || m > 64 || wt->k % 64 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
+  if (xtype == RQ_F32) return dispatch_f32<RQ_F32>(wt, x, m, y, ytype, s);
+  if (xtype == RQ_F16) return dispatch_f32<RQ_F16>(wt, x, m, y, ytype, s);
+  return RQ_E_UNSUPPORTED;
+}
 
 // bf16 activations, 2 <= m <= 64, k % 64 == 0, 16-byte aligned x.
 int launch_linear_smallm(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {

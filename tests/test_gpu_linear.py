@@ -83,6 +83,33 @@ def test_prefill_bf16_out(dev, qtype):
     assert norm_err(y, ref(xb.float().numpy(), wf)) <= TOL_BF16
 
 
+# f32 and f16 activations with 4 <= M <= 64 run on the f32 matrix cores
+# (v_mfma_f32_16x16x4_f32) with the exact dequantized weights: the f32
+# tolerance holds; M < 4, M > 64 and K % 64 != 0 stay on the VALU kernel.
+ALL_FORMATS = [rq.Q4_K, rq.Q6_K, rq.Q8_0, rq.Q5_K, rq.Q4_0, rq.Q5_0]
+
+
+@pytest.mark.parametrize("qtype", ALL_FORMATS)
+@pytest.mark.parametrize("m,n,k", [(2, 4864, 896), (4, 4864, 896), (5, 130, 256), (16, 896, 4864), (17, 300, 512),
+                                   (40, 64, 2048), (64, 258, 128), (65, 96, 256)])
+def test_small_m_f32_activations(dev, qtype, m, n, k):
+    w, wf = make(qtype, n, k, 17 + m + n)
+    x = torch.from_numpy(synth.activations(5 + m, m, k))
+    y = w.forward(x.to(dev)).cpu().numpy()
+    assert y.dtype == np.float32
+    assert norm_err(y, ref(x.numpy(), wf)) <= TOL_F32
+
+
+@pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0])
+@pytest.mark.parametrize("m", [3, 33])
+def test_small_m_f16_activations(dev, qtype, m):
+    w, wf = make(qtype, 200, 896, 3 + m)
+    x = torch.from_numpy(synth.activations(8 + m, m, 896)).to(torch.float16)
+    y = w.forward(x.to(dev), out_dtype=torch.float32).cpu().numpy()
+    # f16 activations are exact in f32; f32 accumulation
+    assert norm_err(y, ref(x.float().numpy(), wf)) <= TOL_F32
+
+
 @pytest.mark.parametrize("xdt,ydt", [(torch.float32, torch.float16), (torch.float16, torch.float32),
                                      (torch.bfloat16, torch.bfloat16)])
 def test_activation_and_output_types(dev, xdt, ydt):
