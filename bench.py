@@ -37,6 +37,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP8_PEAK_TFLOPS = 5000.0
+F32_PEAK_TFLOPS = 157.3
 
 # (name, n, k) of the Qwen2-0.5B layer, y = x W^T with W [n, k]
 LAYER = [("q", 896, 896), ("k", 128, 896), ("v", 128, 896), ("o", 896, 896),
@@ -250,16 +251,19 @@ def extra_verify(torch, rq, W, dev, steps, warmup, dtype=None, ms_list=(1, 2, 4,
     return {"workload": f"verify sweep, Qwen2-0.5B Q4_K layer, {name} activations", "sweep": out}
 
 
-def extra_prefill(torch, rq, synth, dev, steps, warmup):
+def extra_prefill(torch, rq, synth, dev, steps, warmup, f32=False):
     m = 512
     shapes = [("q/k/o Q4_K", rq.Q4_K, 2048, 2048), ("v Q6_K", rq.Q6_K, 2048, 2048),
               ("gate/up Q4_K", rq.Q4_K, 8192, 2048), ("down Q6_K", rq.Q6_K, 2048, 8192),
               ("lm_head Q6_K", rq.Q6_K, 262144, 2048)]
+    dt = torch.float32 if f32 else torch.bfloat16
+    if f32:
+        shapes = shapes[:4]
     res = []
     for name, qt, n, k in shapes:
         w = rq.QWeight(qt, synth.weight_blocks(qt, 7, n, k), n, k)
-        x = torch.randn((m, k), device=dev).to(torch.bfloat16)
-        y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        x = torch.randn((m, k), device=dev).to(dt)
+        y = torch.empty((m, n), dtype=dt, device=dev)
         w.forward(x, out=y)
         torch.cuda.synchronize()
         # launches captured in one graph (the split-K shapes allocate their
@@ -274,10 +278,14 @@ def extra_prefill(torch, rq, synth, dev, steps, warmup):
         ms = Timer(torch).replay(g, 2 if n * k > 1e8 else max(2, steps // 4), 1) / reps
         del g
         tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        frac = ("frac_mfma_f32", F32_PEAK_TFLOPS) if f32 else ("frac_mfma_bf16", BF16_PEAK_TFLOPS)
         res.append({"shape": f"{name} {n}x{k}", "ms": round(ms, 4), "TFLOP/s": round(tf, 2),
-                    "frac_mfma_bf16": round(tf / BF16_PEAK_TFLOPS, 4)})
+                    frac[0]: round(tf / frac[1], 4)})
         del w
         torch.cuda.empty_cache()
+    if f32:
+        return {"workload": "prefill M=512, f32 activations and outputs (the reference's compute type), "
+                            "f32 matrix cores on 64-row slices", "shapes": res}
     return {"workload": "prefill M=512, bf16 activations and outputs, f32 accumulation", "shapes": res}
 
 
@@ -597,6 +605,8 @@ def main():
                          ("verify", lambda: extra_verify(torch, rq, W[:32], dev, args.steps, args.warmup)),
                          ("verify_f32", lambda: extra_verify(torch, rq, W[:32], dev, args.steps, args.warmup,
                                                              torch.float32, (2, 4, 16, 64))),
+                         ("prefill_f32", lambda: extra_prefill(torch, rq, synth, dev, args.steps, args.warmup,
+                                                               f32=True)),
                          ("prefill", lambda: extra_prefill(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("fp8_gemm", lambda: extra_fp8(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("marlin_int4_gemv", lambda: extra_marlin(torch, rq, dev, args.steps, args.warmup)),

@@ -433,6 +433,23 @@ int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m
     const int rc = launch_linear_smallm_f32(wt, x, xtype, m, y, ytype, s);
     if (rc != RQ_E_UNSUPPORTED) return rc;
   }
+  // More rows (prefill with f32 activations, the reference's compute type):
+  // the same kernel on slices of 64 activation rows (the weights are read
+  // once per slice, mostly from cache), a last slice of 2 or 3 rows on the
+  // VALU kernel and a single row on the GEMV.
+  if (m > 64 && (xtype == RQ_F32 || xtype == RQ_F16) && wt->k % 64 == 0 &&
+      reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+    const size_t xb = xtype == RQ_F32 ? 4 : 2, yb = ytype == RQ_F32 ? 4 : 2;
+    for (int64_t r0 = 0; r0 < m; r0 += 64) {
+      const int64_t mm = m - r0 < 64 ? m - r0 : 64;
+      const void *xs = static_cast<const uint8_t *>(x) + (size_t)r0 * (size_t)wt->k * xb;
+      void *ys = static_cast<uint8_t *>(y) + (size_t)r0 * (size_t)wt->n * yb;
+      const int rc = mm >= 4 ? launch_linear_smallm_f32(wt, xs, xtype, mm, ys, ytype, s)
+                             : launch_linear_fused(wt, xs, xtype, mm, ys, ytype, s);
+      if (rc) return rc;
+    }
+    return RQ_OK;
+  }
   switch (wt->qtype) {
     case RQ_Q4_K:
       // Pieces must not straddle rows: rows start on 64-element chunk bounds.

@@ -100,6 +100,19 @@ def test_small_m_f32_activations(dev, qtype, m, n, k):
     assert norm_err(y, ref(x.numpy(), wf)) <= TOL_F32
 
 
+# More than 64 f32 rows run as slices of 64 on the same kernel, with a last
+# slice of 1..3 rows on the VALU kernel or the GEMV.
+@pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0, rq.Q5_0])
+@pytest.mark.parametrize("m,n,k", [(200, 300, 512), (129, 130, 256), (66, 64, 2048), (131, 96, 896)])
+def test_f32_activations_sliced(dev, qtype, m, n, k):
+    w, wf = make(qtype, n, k, 23 + m)
+    x = torch.from_numpy(synth.activations(7 + m, m, k))
+    for ydt in (torch.float32, torch.bfloat16):
+        y = w.forward(x.to(dev), out_dtype=ydt).float().cpu().numpy()
+        tol = TOL_F32 if ydt == torch.float32 else TOL_BF16
+        assert norm_err(y, ref(x.numpy(), wf)) <= tol
+
+
 @pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0])
 @pytest.mark.parametrize("m", [3, 33])
 def test_small_m_f16_activations(dev, qtype, m):
