@@ -142,6 +142,61 @@ __device__ __forceinline__ void store_tile32(const rq_f32x16 &acc, void *y, int 
   }
 }
 
+// ---- LDS-staged epilogue for 256 x 256 tiles of 2-byte outputs ------------
+//
+// Stored straight from the accumulators, a 2-byte output tile is written in
+// 64-byte row pieces (8 bytes per lane, 8 rows per instruction), half cache
+// lines scattered over rows n * 2 bytes apart.  Staged row-major
+// in LDS (256 rows of 512 bytes; the 16-byte chunk c of row r at
+// c ^ 4 (r % 4), so the four rows that one write instruction covers fall in
+// disjoint 64-byte groups and a row's reads stay a permutation), the tile
+// leaves as whole rows: 32 lanes x 16 bytes per row, two rows per wave
+// instruction.
+
+// A wave's 128 x 128 block (4 x 4 MFMA tiles of 32 x 32, rows rb.., columns
+// cb.. of the staged tile) into T; values scaled by sx * sw when SCALED.
+template <bool SCALED>
+__device__ __forceinline__ void stage_block_2b(const rq_f32x16 (&acc)[4][4], uint8_t *T, int rb, int cb, int ytype,
+                                               const float (&sx)[4][4], const float (&sw)[4][4], int lane) {
+  const int h = lane >> 5, t = lane & 3;
+  static_for<4>([&](auto I) {
+    static_for<4>([&](auto J) {
+      static_for<4>([&](auto G) {
+        constexpr int g = decltype(G)::value;
+        const rq_f32x16 &a = acc[I][J];
+        float v0 = a[4 * g], v1 = a[4 * g + 1], v2 = a[4 * g + 2], v3 = a[4 * g + 3];
+        quad_transpose(v0, v1, v2, v3, lane);
+        if (SCALED) {
+          v0 *= sx[I][g] * sw[J][0];
+          v1 *= sx[I][g] * sw[J][1];
+          v2 *= sx[I][g] * sw[J][2];
+          v3 *= sx[I][g] * sw[J][3];
+        }
+        const int r = rb + 32 * I + 8 * g + 4 * h + t;
+        const int c = cb + 32 * J + (lane & 28);  // first of 4 columns
+        const uint32_t lo = ytype == RQ_BF16 ? pack_bf16x2(v0, v1) : pack_f16x2(v0, v1);
+        const uint32_t hi = ytype == RQ_BF16 ? pack_bf16x2(v2, v3) : pack_f16x2(v2, v3);
+        *reinterpret_cast<uint2 *>(T + r * 512 + (((c >> 3) ^ (4 * (r & 3))) << 4) + ((c >> 2) & 1) * 8) =
+            make_uint2(lo, hi);
+      });
+    });
+  });
+}
+
+// The staged tile to y[m0 .. m0 + 256, n0 .. n0 + 256) (2-byte elements, row
+// stride n), 256 threads.
+__device__ __forceinline__ void store_staged_2b(const uint8_t *T, void *y, int64_t n, int64_t m0, int64_t n0,
+                                                int tid) {
+  const int c = tid & 31;
+  uint8_t *base = static_cast<uint8_t *>(y) + (m0 * n + n0) * 2 + 16 * c;
+#pragma unroll 4
+  for (int i = 0; i < 32; ++i) {
+    const int r = 8 * i + (tid >> 5);
+    const uint4 v = *reinterpret_cast<const uint4 *>(T + r * 512 + ((c ^ (4 * (r & 3))) << 4));
+    *reinterpret_cast<uint4 *>(base + (int64_t)r * n * 2) = v;
+  }
+}
+
 // vec flag of store_tile32 for an output buffer.
 __device__ __forceinline__ bool vec_stores_ok(const void *y, int64_t n) {
   return ((reinterpret_cast<uintptr_t>(y) & 15) == 0) && ((n & 3) == 0);

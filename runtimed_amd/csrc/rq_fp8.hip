@@ -231,10 +231,9 @@ __global__ __launch_bounds__(256) void k_fp8_gemm_pipe(const uint8_t *__restrict
                                                       const uint8_t *__restrict__ b,
                                                       const float *__restrict__ ws, int64_t n,
                                                       int64_t k, void *__restrict__ y, int ytype) {
-  __shared__ __attribute__((aligned(1024))) uint8_t S0[P_STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t S1[P_STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t S2[P_STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t S3[P_STAGE];
+  // four stages, one array: after the loop it holds the staged output tile
+  __shared__ __attribute__((aligned(1024))) uint8_t SM[4 * P_STAGE];
+  uint8_t *const S0 = SM, *const S1 = SM + P_STAGE, *const S2 = SM + 2 * P_STAGE, *const S3 = SM + 3 * P_STAGE;
   uint8_t *const SB[4] = {S0, S1, S2, S3};
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -305,6 +304,13 @@ __global__ __launch_bounds__(256) void k_fp8_gemm_pipe(const uint8_t *__restrict
   for (int i = 0; i < 4; ++i) tile_row_scales(xs, m, m0 + 128 * wm + i * 32, lane, sx[i]);
 #pragma unroll
   for (int j = 0; j < 4; ++j) tile_col_scales(ws, n, n0 + 128 * wn + j * 32, lane, sw[j]);
+  if (ytype != RQ_F32 && vec && n % 8 == 0 && m0 + 256 <= m && n0 + 256 <= n) {
+    __syncthreads();  // every wave's stage reads are done
+    stage_block_2b<true>(acc, SM, 128 * wm, 128 * wn, ytype, sx, sw, lane);
+    __syncthreads();
+    store_staged_2b(SM, y, n, m0, n0, threadIdx.x);
+    return;
+  }
   static_for<4>([&](auto I) {
     static_for<4>([&](auto J) {
       store_tile32<true>(acc[I][J], y, ytype, m, n, m0 + 128 * wm + I * 32, n0 + 128 * wn + J * 32,

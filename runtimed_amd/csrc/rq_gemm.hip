@@ -235,10 +235,9 @@ template <class F>
 __global__ __launch_bounds__(256) void k_qgemm_pipe(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
                                                     const uint16_t *__restrict__ x, int64_t m, int64_t n,
                                                     int64_t k, void *__restrict__ y, int ytype) {
-  __shared__ __attribute__((aligned(1024))) uint8_t S0[P_STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t S1[P_STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t S2[P_STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t S3[P_STAGE];
+  // four stages, one array: after the loop it holds the staged output tile
+  __shared__ __attribute__((aligned(1024))) uint8_t SM[4 * P_STAGE];
+  uint8_t *const S0 = SM, *const S1 = SM + P_STAGE, *const S2 = SM + 2 * P_STAGE, *const S3 = SM + 3 * P_STAGE;
   uint8_t *const SB[4] = {S0, S1, S2, S3};
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -333,6 +332,14 @@ __global__ __launch_bounds__(256) void k_qgemm_pipe(const uint8_t *__restrict__ 
   }
 
   const bool vec = vec_stores_ok(y, n);
+  if (ytype != RQ_F32 && vec && n % 8 == 0 && m0 + 256 <= m && n0 + 256 <= n) {
+    __syncthreads();  // every wave's stage reads are done
+    const float ones[4][4] = {};
+    stage_block_2b<false>(acc, SM, 128 * wm, 128 * wn, ytype, ones, ones, lane);
+    __syncthreads();
+    store_staged_2b(SM, y, n, m0, n0, tid);
+    return;
+  }
   const float one[4] = {1.0f, 1.0f, 1.0f, 1.0f};
   static_for<4>([&](auto I) {
     static_for<4>([&](auto J) {
