@@ -27,6 +27,8 @@
 namespace rq {
 namespace {
 
+using namespace pipe;
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float float2v __attribute__((ext_vector_type(2)));
@@ -41,7 +43,7 @@ constexpr int BK = 64, LDS_K = BK + 8;
 // Split K: workgroup z covers K-steps [z * steps, (z + 1) * steps) and, when
 // part is not null, writes its f32 partial tile to part + z * m * n instead
 // of y (k_splitk_sum adds the partials).
-template <class F, int BM, int BN, int WM, int WN>
+template <class F, int BM, int BN, int WM, int WN, int D>
 __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restrict__ w,
                                                        const uint8_t *__restrict__ aux,
                                                        const uint16_t *__restrict__ x, int64_t m,
@@ -59,41 +61,44 @@ __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restric
   const int wm = wave / WN, wn = wave % WN;
   const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
 
-  // weight piece of this thread: row n0 + (tid >> 1), half h = tid & 1
+  // Weight piece of this thread: row n0 + (tid >> 1), half h = tid & 1;
+  // activation slots: row (tid >> 3) + A_ROWS * i, 8 bf16 at column
+  // 8 * (tid & 7).  Rows past n or m re-read the last row (unconditional
+  // loads); their products land in outputs that are never stored.
   const int brow = tid >> 1, bh = tid & 1;
-  const int64_t gn = n0 + brow;
-  const bool bvalid = gn < n;
-  // activation slots: row (tid >> 3) + A_ROWS * i, 8 bf16 at column 8 * (tid & 7)
+  const int64_t gn = n0 + brow < n ? n0 + brow : n - 1;
   const int arow = tid >> 3, acol = 8 * (tid & 7);
-
-  uint4 ra[A_LOADS];
-  typename F::Piece pb;
-  auto gload = [&](int64_t kt) {
+  const uint16_t *xa[A_LOADS];
 #pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) {
-      const int64_t gm = m0 + arow + A_ROWS * i;
-      ra[i] = gm < m ? *reinterpret_cast<const uint4 *>(x + gm * k + kt * BK + acol)
-                     : make_uint4(0, 0, 0, 0);
-    }
-    if (bvalid) pb = F::load(w, aux, gn, k, (int)(2 * kt + bh));
+  for (int i = 0; i < A_LOADS; ++i) {
+    const int64_t gm = m0 + arow + A_ROWS * i;
+    xa[i] = x + (gm < m ? gm : m - 1) * k + acol;
+  }
+
+  // Loads run D K-steps ahead in D register slots (LLVM vector types: a
+  // HIP uint4 array would be copied through private memory).
+  const int64_t kt0 = (int64_t)blockIdx.z * steps;
+  const int64_t nk = (k / BK - kt0 < steps ? k / BK - kt0 : steps);
+  u32x4 ra[D][A_LOADS];
+  typename F::Piece pb[D];
+  auto gload = [&](int slot, int64_t s) {  // local step s, clamped to the split
+    const int64_t kt = kt0 + (s < nk ? s : nk - 1);
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i) ra[slot][i] = *reinterpret_cast<const u32x4 *>(xa[i] + kt * BK);
+    pb[slot] = F::load(w, aux, gn, k, (int)(2 * kt + bh));
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int slot, int buf) {
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i)
-      *reinterpret_cast<uint4 *>(&As[buf][(arow + A_ROWS * i) * LDS_K + acol]) = ra[i];
+      *reinterpret_cast<u32x4 *>(&As[buf][(arow + A_ROWS * i) * LDS_K + acol]) = ra[slot][i];
     uint32_t ob[16];
-    if (bvalid) {
-      F::decode_bf16(pb, ob);
-    } else {
-#pragma unroll
-      for (int t = 0; t < 16; ++t) ob[t] = 0u;
-    }
+    F::decode_bf16(pb[slot], ob);
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      uint4 *dst = reinterpret_cast<uint4 *>(&Bs[buf][brow * LDS_K + 16 * bh + 32 * r]);
+      u32x4 *dst = reinterpret_cast<u32x4 *>(&Bs[buf][brow * LDS_K + 16 * bh + 32 * r]);
 #pragma unroll
       for (int q = 0; q < 2; ++q)
-        dst[q] = make_uint4(ob[8 * r + 4 * q], ob[8 * r + 4 * q + 1], ob[8 * r + 4 * q + 2], ob[8 * r + 4 * q + 3]);
+        dst[q] = (u32x4){ob[8 * r + 4 * q], ob[8 * r + 4 * q + 1], ob[8 * r + 4 * q + 2], ob[8 * r + 4 * q + 3]};
     }
   };
 
@@ -103,14 +108,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restric
 #pragma unroll
     for (int j = 0; j < NI; ++j) acc[i][j] = (f32x16){0};
 
-  const int64_t kt0 = (int64_t)blockIdx.z * steps;
-  const int64_t nk = (k / BK - kt0 < steps ? k / BK - kt0 : steps);
-  gload(kt0);
-  sstore(0);
-  __syncthreads();
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    const int buf = (int)(kt & 1);
-    if (kt + 1 < nk) gload(kt0 + kt + 1);
+  auto mfma_step = [&](int buf) {
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       const int kc = ks * 16 + 8 * (lane >> 5);
@@ -127,8 +125,29 @@ __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restric
         for (int j = 0; j < NI; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < nk) sstore(buf ^ 1);
-    __syncthreads();
+  };
+
+  // Slot (s % D) holds step s once loaded.  Step s: the matrix work on LDS
+  // buffer s % 2; step s + 1 (loaded D - 1 steps ago) is written to the other
+  // buffer and its slot refilled with step s + 1 + D; one barrier.  The
+  // stores of steps past the end are made anyway (clamped data into a buffer
+  // that is never read) and only their matrix work is skipped, so no load is
+  // made under a branch.
+#pragma unroll
+  for (int j = 0; j < D; ++j) gload(j, j);
+  sstore(0, 0);
+  gload(0, D);
+  __syncthreads();
+  for (int64_t kt = 0; kt < nk; kt += D) {
+    static_for<D>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      const int64_t s = kt + j;
+      const int buf = (int)(s & 1);
+      if (s < nk) mfma_step(buf);
+      sstore((j + 1) % D, buf ^ 1);
+      gload((j + 1) % D, s + 1 + D);
+      __syncthreads();
+    });
   }
 
   void *out = part ? static_cast<void *>(part + (int64_t)blockIdx.z * m * n) : y;
@@ -167,7 +186,6 @@ __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restric
 // Indices past the end are clamped (their loads and writes land in stages
 // that are never read), so the loop body has no branches; k must be a
 // multiple of 128 (four steps per iteration).
-using namespace pipe;
 
 // Fragments of one MFMA pass: A of tiles 0..3, then B of tiles 0..3.
 struct Pass {
@@ -368,7 +386,7 @@ int splits_for(int64_t tiles, int64_t nk) {
   return sp;
 }
 
-template <class F, int BM, int BN, int WM, int WN>
+template <class F, int BM, int BN, int WM, int WN, int D = 3>
 int launch(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s, int sp_force = 0) {
   const int64_t nk = wt->k / BK;
   const int64_t gx = (wt->n + BN - 1) / BN, gy = (m + BM - 1) / BM;
@@ -383,7 +401,7 @@ int launch(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hi
                        (long long)wt->n);
   }
   const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)used);
-  hipLaunchKernelGGL((k_qgemm<F, BM, BN, WM, WN>), grid, dim3(64 * WM * WN), 0, s, wt->data,
+  hipLaunchKernelGGL((k_qgemm<F, BM, BN, WM, WN, D>), grid, dim3(64 * WM * WN), 0, s, wt->data,
                      wt->data + wt->aux_off, static_cast<const uint16_t *>(x), m, wt->n, wt->k, y,
                      ytype, steps, part);
   if (part) {
@@ -410,7 +428,7 @@ int by_m(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipS
   // when K is a multiple of 128), else 128 x 128.
   const int64_t big_tiles = ((m + 255) / 256) * ((wt->n + 255) / 256);
   if (big_tiles >= 256 && wt->k % 128 == 0) return launch_pipe<F>(wt, x, m, y, ytype, s);
-  if (big_tiles >= 256) return launch<F, 256, 256, 2, 4>(wt, x, m, y, ytype, s);
+  if (big_tiles >= 256) return launch<F, 256, 256, 2, 4, 1>(wt, x, m, y, ytype, s);
   // Fewer than 128 tiles of 128 x 128 (2048-wide layers at M = 512): short K
   // takes 64 x 128 tiles; long K keeps 128 x 128 and splits K eight ways
   // (at most, 16 K-steps per split).  Measured on the 2048 / 8192 prefill
