@@ -349,38 +349,32 @@ def extra_marlin(torch, rq, dev, steps, warmup):
 def extra_kv(torch, rq, dev, steps, warmup):
     """Paged-KV quantizer: one layer's K for a 4096-token prompt with 8 KV
     heads of 128 ([1, 8, 4096, 128] bf16, 8 MB), 64 distinct inputs; bytes
-    counted once each way (input read, codes and scales written)."""
+    counted once each way (input read, codes and scales written).  The 64
+    calls are captured in one graph (the quantizer's partial maxima are
+    allocated stream-ordered inside it) and timed over replays."""
     shape = (1, 8, 4096, 128)
     copies = 64
     ins = [torch.randn(shape, device=dev).to(torch.bfloat16) for _ in range(copies)]
     q = torch.empty(shape, dtype=torch.uint8, device=dev)
     s = torch.empty(8, device=dev)
     out = torch.empty(shape, dtype=torch.bfloat16, device=dev)
-    st = rq._stream(dev)
     b, h, sd = 1, 8, 4096 * 128
     res = {}
     for mode, name in ((rq.KV_FP8, "fp8"), (rq.KV_INT8, "int8")):
         def quant():
+            st = rq._stream(dev)
             for t in ins:
                 rq.check(rq.lib().rq_kv_quantize(rq._ptr(t), rq.BF16, b, h, sd, mode, rq._ptr(q), rq._ptr(s), st))
 
         def deq():
+            st = rq._stream(dev)
             for _ in range(copies):
                 rq.check(rq.lib().rq_kv_dequantize(rq._ptr(q), mode, rq._ptr(s), b, h, sd, rq._ptr(out), rq.BF16, st))
 
         for label, fn, nbytes in (("quantize", quant, b * h * sd * 3 + h * 4), ("dequantize", deq, b * h * sd * 3)):
-            for _ in range(warmup):
-                fn()
-            torch.cuda.synchronize()
-            t0 = torch.cuda.Event(enable_timing=True)
-            t1 = torch.cuda.Event(enable_timing=True)
-            reps = max(2, steps // 4)
-            t0.record()
-            for _ in range(reps):
-                fn()
-            t1.record()
-            torch.cuda.synchronize()
-            ms = t0.elapsed_time(t1) / (reps * copies)
+            g = capture(torch, fn)
+            ms = Timer(torch).replay(g, max(2, steps // 4), warmup) / copies
+            del g
             res[f"{name}_{label}"] = {"us": round(ms * 1e3, 3), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
                                       "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     return {"workload": "KV block quantizer [1, 8, 4096, 128] bf16 <-> fp8 / int8 codes, per-head scales", **res}
