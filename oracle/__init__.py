@@ -1,8 +1,8 @@
 """ctypes view of the CPU oracle (oracle/librq_oracle.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by the smoke check of
-__graft_entry__.py and by the CPU-baseline leg of bench.py, always as the
-checker or the timed CPU baseline, never by the product path (runtimed_amd/).
+__graft_entry__.py and by the CPU-baseline leg of bench.py, always to check
+results or as the timed CPU baseline, never by the product path (runtimed_amd/).
 """
 from __future__ import annotations
 

@@ -6,7 +6,7 @@
  * helpers in crates/runtimed-model/src/weights/load_safetensors.rs and
  * crates/runtimed-model/src/ops/fp8_gemm.rs).  Only tests/, the smoke check
  * in __graft_entry__.py and the CPU-baseline leg of bench.py may load it, and
- * only as the checker or the timed CPU baseline.  The product library
+ * only to check results or as the timed CPU baseline.  The product library
  * (librq.so) never links or calls it.
  *
  * Every function cites the reference file:line it restates.  How each one is

@@ -4,8 +4,8 @@
  *
  * TEST INFRASTRUCTURE ONLY (see rq_oracle.h): a plain-C restatement of
  * crates/runtimed-model/src/ops/marlin_gemv.rs and
- * crates/runtimed-model/src/cache/paged/quantize.rs, used as the checker of
- * the device kernels and never by the product library.
+ * crates/runtimed-model/src/cache/paged/quantize.rs, used to check the
+ * device kernels and never by the product library.
  *
  * Rust semantics restated here: f32::round rounds half away from zero (C
  * roundf); `x.clamp(lo, hi) as u32 / as i8` maps NaN to 0 and saturates

@@ -4,7 +4,7 @@
 // (Q4_K, Q6_K, Q8_0), f32 accumulation, f32/bf16/f16 output.  Semantics of the
 // reference's dense path (linear_layer.rs:88-104 after dequant_tensor,
 // dequant.rs:83-146) with the weights rounded once to bf16 on their way into
-// the matrix cores (north-star tolerance for bf16 operands: 2e-2 normalized).
+// the matrix cores (the tolerance for bf16 operands: 2e-2 normalized).
 //
 // Tiling.  A workgroup computes a BM x BN tile of y (256 x 256 with 8 waves
 // for large problems, 128 x 128 or 64 x 128 with 4 waves otherwise).  Each

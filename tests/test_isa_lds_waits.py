@@ -54,7 +54,7 @@ def early_uses(lines, kernel: str):
     return bad, reads
 
 
-def test_checker_flags_an_early_use():
+def test_scan_flags_an_early_use():
     lines = ["k:", "\tds_read_b128 v[4:7], v1", "\tv_mov_b32 v9, v5", "\ts_waitcnt lgkmcnt(0)",
              "\tv_mov_b32 v9, v5", "\ts_endpgm"]
     bad, reads = early_uses(lines, "k")

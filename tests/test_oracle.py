@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/) before it is trusted as the GPU checker.
+"""Pins the CPU oracle (oracle/) before it is trusted to check the GPU results.
 
 Each oracle function is checked by at least one of:
   * the reference's own known-answer tests, transcribed verbatim
