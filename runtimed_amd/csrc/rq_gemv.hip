@@ -66,6 +66,62 @@ __device__ __forceinline__ void stage_x(const void *x, int xtype, int k, float *
   __syncthreads();
 }
 
+// The same staging split in two, for kernels that issue x's loads before
+// their weight loads: the load counter retires loads in issue order, so a
+// wait for x loads issued after the weights would hold the staging until the
+// (HBM) weights had landed too.  Thread t loads the 16-byte chunks t,
+// t + blockDim, ... of x (4 f32 or 8 f16/bf16 elements each) with one
+// unconditional load form for every type (clamped to the last chunk); the
+// conversion and the LDS stores follow the weight loads.  XR = chunks per
+// thread, >= ceil(k / (elements per chunk) / blockDim).
+typedef uint32_t chunk16 __attribute__((ext_vector_type(4)));
+
+__host__ __device__ inline int x_chunks(int64_t k, int xtype) { return (int)(k >> (xtype == RQ_F32 ? 2 : 3)); }
+
+template <int XR>
+__device__ __forceinline__ void load_x_chunks(const void *x, int xtype, int k, chunk16 (&v)[XR]) {
+  const int nc = x_chunks(k, xtype);
+#pragma unroll
+  for (int i = 0; i < XR; ++i) {
+    const int c = (int)threadIdx.x + i * (int)blockDim.x;
+    v[i] = reinterpret_cast<const chunk16 *>(x)[c < nc ? c : nc - 1];
+  }
+}
+
+// Every thread stores all XR chunks, threads past the end the (clamped) last
+// chunk again: identical bytes to the same place.  A store under "c < nc"
+// would let the compiler sink the load into that branch, behind the weights.
+template <int XR>
+__device__ __forceinline__ void store_x_chunks(int xtype, int k, const chunk16 (&v)[XR], float *xs) {
+  const int nc = x_chunks(k, xtype);
+#pragma unroll
+  for (int i = 0; i < XR; ++i) {
+    const int c0 = (int)threadIdx.x + i * (int)blockDim.x;
+    const int c = c0 < nc ? c0 : nc - 1;
+    const chunk16 u = v[i];
+    if (xtype == RQ_F32) {
+      *reinterpret_cast<float4 *>(xs + xpad(4 * c)) =
+          make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+    } else {
+      float f[8];
+      const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (xtype == RQ_BF16) {
+          f[2 * j] = __uint_as_float(wd[j] << 16);
+          f[2 * j + 1] = __uint_as_float(wd[j] & 0xFFFF0000u);
+        } else {
+          f[2 * j] = h2f(wd[j]);
+          f[2 * j + 1] = h2f(wd[j] >> 16);
+        }
+      }
+      *reinterpret_cast<float4 *>(xs + xpad(8 * c)) = make_float4(f[0], f[1], f[2], f[3]);
+      *reinterpret_cast<float4 *>(xs + xpad(8 * c + 4)) = make_float4(f[4], f[5], f[6], f[7]);
+    }
+  }
+  __syncthreads();
+}
+
 template <int LEN>
 __device__ __forceinline__ void load_run_lds(const float *xs, int e0, float *dst) {
   const float4 *src = reinterpret_cast<const float4 *>(xs + xpad(e0));
@@ -90,18 +146,22 @@ __device__ __forceinline__ void load_piece_x(const void *x, int xtype, const flo
 // into registers and reused for every row it visits.  Rows with P <= 64
 // pieces sit on an aligned segment of seg = max(16, next_pow2(P)) lanes
 // (64/seg rows per wave); longer rows are split over a team of T = ceil(P/64)
-// waves whose partial sums meet in LDS.  The weight loads of the first row are
-// issued before the activation loads, and each iteration issues the next
-// row's loads before it computes, so HBM latency overlaps everything else.
-template <class F>
+// waves whose partial sums meet in LDS.  With XR > 0 the loads of x (XR
+// 16-byte chunks per thread, L2-resident) are issued first and the first
+// row's weight loads right behind them, so x is staged in LDS while the
+// weights are still in flight; with XR = 0 (x longer than XR chunks per
+// thread cover) the weights go first and x is staged after them.  Each
+// iteration issues the next row's loads before it computes, so HBM latency
+// overlaps everything else.
+template <class F, int XR>
 __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
                                                 const uint8_t *__restrict__ aux,
                                                 const void *__restrict__ x, int xtype,
                                                 void *__restrict__ y, int ytype, int64_t n,
                                                 int64_t k, int seg_log2, int team,
-                                                int rows_per_wg, bool xlds) {
+                                                int rows_per_wg, int64_t groups, bool xlds) {
   __shared__ float red[8][8];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int P = (int)(k / F::PE);
   int row_in_wg, p, tm;
   if (team == 1) {
@@ -109,8 +169,13 @@ __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
     p = lane & ((1 << seg_log2) - 1);
     tm = 0;
   } else {
-    row_in_wg = wv / team;
-    tm = wv - row_in_wg * team;
+    // wv / team and wv % team on scalar registers (wv < 8)
+    row_in_wg = 0;
+    tm = wv;
+    while (tm >= team) {
+      tm -= team;
+      ++row_in_wg;
+    }
     p = 64 * tm + lane;
   }
   const bool live = p < P;
@@ -119,16 +184,25 @@ __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
   // (the prefetched row too) before the next use.  Dead lanes and rows past
   // n contribute nothing (the dot product is selected away).
   const int pl = live ? p : P - 1;
-  const int64_t groups = (n + rows_per_wg - 1) / rows_per_wg;
   int64_t g = blockIdx.x;
   int64_t row = g * rows_per_wg + row_in_wg;
-  typename F::Piece cur = F::load(w, aux, row < n ? row : n - 1, k, pl);
-
   extern __shared__ __attribute__((aligned(16))) float xs_dyn[];
   const float *xs = nullptr;
-  if (xlds) {  // uniform: the whole workgroup stages x once
-    stage_x(x, xtype, (int)k, xs_dyn);
+  typename F::Piece cur;
+  if constexpr (XR > 0) {  // launched only with the LDS copy of x
+    chunk16 xc[XR];
+    load_x_chunks<XR>(x, xtype, (int)k, xc);
+    __builtin_amdgcn_sched_barrier(0);
+    cur = F::load(w, aux, row < n ? row : n - 1, k, pl);
+    __builtin_amdgcn_sched_barrier(0);
+    store_x_chunks<XR>(xtype, (int)k, xc, xs_dyn);
     xs = xs_dyn;
+  } else {
+    cur = F::load(w, aux, row < n ? row : n - 1, k, pl);
+    if (xlds) {  // uniform: the whole workgroup stages x once
+      stage_x(x, xtype, (int)k, xs_dyn);
+      xs = xs_dyn;
+    }
   }
   float xv[F::RUNS][16];
   float sx[F::RUNS];
@@ -388,8 +462,23 @@ int run_m1(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hi
   const int64_t groups = (wt->n + rows_per_wg - 1) / rows_per_wg;
   const unsigned blocks = (unsigned)(groups < 16384 ? groups : 16384);
   const size_t xb = xlds_bytes(wt->k);
-  hipLaunchKernelGGL((k_gemv_m1<F>), dim3(blocks), dim3(threads), xb, s, wt->data, wt->data + wt->aux_off,
-                     x, xtype, y, ytype, wt->n, wt->k, seg_log2, team, rows_per_wg, xb != 0);
+  // x chunks per thread when x is staged (x is 16-byte aligned here); more
+  // than four keep the weights-first order.
+  int xr = 0;
+  if (xb && wt->k % 8 == 0) {
+    const int per = (x_chunks(wt->k, xtype) + threads - 1) / threads;
+    xr = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 0;
+  }
+#define RQ_M1(XR)                                                                                               \
+  hipLaunchKernelGGL((k_gemv_m1<F, XR>), dim3(blocks), dim3(threads), xb, s, wt->data, wt->data + wt->aux_off, \
+                     x, xtype, y, ytype, wt->n, wt->k, seg_log2, team, rows_per_wg, groups, xb != 0)
+  switch (xr) {
+    case 1: RQ_M1(1); break;
+    case 2: RQ_M1(2); break;
+    case 4: RQ_M1(4); break;
+    default: RQ_M1(0); break;
+  }
+#undef RQ_M1
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }
 

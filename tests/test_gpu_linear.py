@@ -46,6 +46,28 @@ def test_decode_gemv_f32(dev, qtype, n, k):
     assert norm_err(y, ref(x, wf)) <= TOL_F32
 
 
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("qtype,n,k", [
+    (rq.Q4_K, 4864, 896),   # 16-byte chunks of x per thread: 1 (f32) / 1 (16-bit)
+    (rq.Q4_K, 512, 2048),   # 2 / 1
+    (rq.Q6_K, 256, 4096),   # 4 / 2
+    (rq.Q6_K, 128, 896),    # 1 / 1, Q6_K rows starting mid-block
+    (rq.Q4_K, 896, 4864),   # three-wave teams: 4 / 2
+    (rq.Q4_K, 64, 12288),   # six-wave teams: f32 x staged after the weights, 16-bit 4
+    (rq.Q8_0, 96, 16384),   # x too long for the LDS copy
+])
+def test_decode_gemv_activation_types(dev, xdt, qtype, n, k):
+    # M = 1 with each activation type: x is staged in LDS from raw 16-byte
+    # chunks (4 f32 or 8 f16/bf16 values) before the weights arrive
+    print(f"gemv x={xdt} qtype={qtype} n={n} k={k}", flush=True)
+    w, wf = make(qtype, n, k, 20 + n + k)
+    x = torch.from_numpy(synth.activations(4, 1, k)).to(xdt)
+    y = w.forward(x.to(dev), out_dtype=torch.float32).cpu().numpy()
+    assert y.shape == (1, n)
+    # 16-bit activations are exact in f32: the f32 accumulation gate holds
+    assert norm_err(y, ref(x.float().numpy(), wf)) <= TOL_F32
+
+
 @pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0])
 @pytest.mark.parametrize("m", [2, 4, 8, 16, 64])
 def test_verify_small_m_bf16(dev, qtype, m):
