@@ -210,7 +210,10 @@ __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
   for (int r = 0; r < F::RUNS; ++r) {
     sx[r] = 0.0f;
     if (live) {
-      load_piece_x<F>(x, xtype, xs, p, r, xv[r]);
+      // With XR > 0 the LDS copy always exists; saying so at compile time
+      // keeps the global-load path (and its drain-all waits) out of the code.
+      if constexpr (XR > 0) load_run_lds<16>(xs_dyn, (int)F::run_off(p, r), xv[r]);
+      else load_piece_x<F>(x, xtype, xs, p, r, xv[r]);
 #pragma unroll
       for (int t = 0; t < 16; ++t) sx[r] += xv[r][t];
     } else {
@@ -219,12 +222,10 @@ __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
     }
   }
 
-  for (; g < groups; g += gridDim.x) {
-    const int64_t gn = g + gridDim.x;
-    const int64_t row_n = gn * rows_per_wg + row_in_wg;
-    const typename F::Piece nxt = F::load(w, aux, (gn < groups && row_n < n) ? row_n : (row < n ? row : n - 1), k, pl);
-    const float d = F::dot(cur, xv, sx);
-    float acc = (live && row < n) ? d : 0.0f;
+  // Dot product, row total and store of one row group.
+  auto emit = [&](const typename F::Piece &pc, int64_t r) {
+    const float d = F::dot(pc, xv, sx);
+    float acc = (live && r < n) ? d : 0.0f;
     if (team == 1) {
       const int seg = 1 << seg_log2;
       if (seg >= 16) {
@@ -232,18 +233,31 @@ __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
       } else {
         for (int off = seg >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
       }
-      if ((lane & (seg - 1)) == seg - 1 && row < n) store_out(y, ytype, row, acc);
+      if ((lane & (seg - 1)) == seg - 1 && r < n) store_out(y, ytype, r, acc);
     } else {
       acc = seg_sum(acc, 64);
       if (lane == 63) red[row_in_wg][tm] = acc;
       __syncthreads();
-      if (tm == 0 && lane == 63 && row < n) {
+      if (tm == 0 && lane == 63 && r < n) {
         float tot = red[row_in_wg][0];
         for (int t = 1; t < team; ++t) tot += red[row_in_wg][t];
-        store_out(y, ytype, row, tot);
+        store_out(y, ytype, r, tot);
       }
       __syncthreads();
     }
+  };
+  // One row group per workgroup (every decode-sized matrix): no prefetch.
+  // A next-row load in the last pass is never used, and the wave still has
+  // to wait for it before it can end.
+  if (groups <= (int64_t)gridDim.x) {
+    emit(cur, row);
+    return;
+  }
+  for (; g < groups; g += gridDim.x) {
+    const int64_t gn = g + gridDim.x;
+    const int64_t row_n = gn * rows_per_wg + row_in_wg;
+    const typename F::Piece nxt = F::load(w, aux, (gn < groups && row_n < n) ? row_n : (row < n ? row : n - 1), k, pl);
+    emit(cur, row);
     cur = nxt;
     row = row_n;
   }
