@@ -264,36 +264,58 @@ __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
 }
 
 // M = 1, long rows (P > 64 pieces): one wave per row, PPL pieces per lane
-// (piece lane + 64 i), activations in registers; the wave walks rows with a
-// grid stride and loads the next row's pieces before it computes the
-// current one, so about PPL x 2 pieces per lane are in flight.  No barriers
-// in the loop: the row total is a DPP sum over the wave.  WPG waves per
-// workgroup share one LDS copy of x; the first row's weight loads are
-// issued before it is staged.
+// (piece lane + 64 i), activations in registers; the wave walks the rows
+// row0, row0 + nw, row0 + 2 nw, ... (nw = waves in the grid) with the loads
+// of D of them in flight: D slots of pieces, refilled with the row D strides
+// ahead as soon as a slot's row is computed.  Slot indices are static and
+// every load is unconditional (rows past n clamp to the slot's own row, just
+// read), so the compiler's waits are exact counts; the last group of D rows
+// refills nothing.  No barriers in the loop: the row total is a DPP sum over
+// the wave.  WPG waves per workgroup share one LDS copy of x.  With XR > 0
+// (XR = 16-byte chunks of x per thread, enough for any k this instance
+// takes) x's loads go out first and the first D rows' weight loads right
+// behind them, so x is staged while the weights are in flight.
 template <class F, int PPL, int WPG>
+constexpr int long_xr() {
+  constexpr int need = (PPL * F::PE + 4 * WPG - 1) / (4 * WPG);  // f32 chunks per thread at k = 64 PPL PE
+  return need <= 4 ? need : 0;
+}
+
+template <class F, int PPL, int WPG, int D>
 __global__ __launch_bounds__(64 * WPG) void k_gemv_long(const uint8_t *__restrict__ w,
                                                         const uint8_t *__restrict__ aux, const void *__restrict__ x,
                                                         int xtype, void *__restrict__ y, int ytype, int64_t n,
                                                         int64_t k, bool xlds) {
+  constexpr int XR = long_xr<F, PPL, WPG>();
   const int lane = threadIdx.x & 63;
   const int P = (int)(k / F::PE);
   const int64_t nw = (int64_t)gridDim.x * WPG;
-  int64_t row = (int64_t)blockIdx.x * WPG + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row0 = (int64_t)blockIdx.x * WPG + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
-  // Unconditional loads of clamped pieces and rows (see k_gemv_m1): the
-  // next row's loads stay in flight while the current row is computed.
   int pc[PPL];
 #pragma unroll
   for (int i = 0; i < PPL; ++i) pc[i] = lane + 64 * i < P ? lane + 64 * i : P - 1;
-  typename F::Piece cur[PPL];
+  typename F::Piece sl[D][PPL];
+  auto fill = [&](int j, int64_t r, int64_t fallback) {
+    const int64_t rr = r < n ? r : fallback;
 #pragma unroll
-  for (int i = 0; i < PPL; ++i) cur[i] = F::load(w, aux, row < n ? row : n - 1, k, pc[i]);
+    for (int i = 0; i < PPL; ++i) sl[j][i] = F::load(w, aux, rr, k, pc[i]);
+  };
+  const int64_t first = row0 < n ? row0 : n - 1;
 
   extern __shared__ __attribute__((aligned(16))) float xs_dyn[];
-  const float *xs = nullptr;
-  if (xlds) {  // uniform: the whole workgroup stages x once
-    stage_x(x, xtype, (int)k, xs_dyn);
-    xs = xs_dyn;
+  if constexpr (XR > 0) {  // launched only with the LDS copy of x
+    chunk16 xc[XR];
+    load_x_chunks<XR>(x, xtype, (int)k, xc);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < D; ++j) fill(j, row0 + j * nw, first);
+    __builtin_amdgcn_sched_barrier(0);
+    store_x_chunks<XR>(xtype, (int)k, xc, xs_dyn);
+  } else {
+#pragma unroll
+    for (int j = 0; j < D; ++j) fill(j, row0 + j * nw, first);
+    if (xlds) stage_x(x, xtype, (int)k, xs_dyn);  // uniform: the whole workgroup stages x once
   }
   float xv[PPL][F::RUNS][16];
   float sx[PPL][F::RUNS];
@@ -304,7 +326,8 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv_long(const uint8_t *__restric
     for (int r = 0; r < F::RUNS; ++r) {
       sx[i][r] = 0.0f;
       if (p < P) {
-        load_piece_x<F>(x, xtype, xs, p, r, xv[i][r]);
+        if constexpr (XR > 0) load_run_lds<16>(xs_dyn, (int)F::run_off(p, r), xv[i][r]);
+        else load_piece_x<F>(x, xtype, xlds ? xs_dyn : nullptr, p, r, xv[i][r]);
 #pragma unroll
         for (int t = 0; t < 16; ++t) sx[i][r] += xv[i][r][t];
       } else {
@@ -314,23 +337,30 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv_long(const uint8_t *__restric
     }
   }
 
-  for (; row < n; row += nw) {
-    const int64_t rn = row + nw;
-    const int64_t rl = rn < n ? rn : row;
-    typename F::Piece nxt[PPL];
-#pragma unroll
-    for (int i = 0; i < PPL; ++i) nxt[i] = F::load(w, aux, rl, k, pc[i]);
+  auto emit = [&](int j, int64_t r) {
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < PPL; ++i) {
-      const float d = F::dot(cur[i], xv[i], sx[i]);
+      const float d = F::dot(sl[j][i], xv[i], sx[i]);
       acc += lane + 64 * i < P ? d : 0.0f;
     }
     acc = seg_sum(acc, 64);
-    if (lane == 63) store_out(y, ytype, row, acc);
+    if (lane == 63 && r < n) store_out(y, ytype, r, acc);
+  };
+  // Groups of D rows: every group but the last refills its slots.
+  const int64_t rows = row0 < n ? (n - row0 + nw - 1) / nw : 0;  // rows of this wave
+  const int64_t groups = (rows + D - 1) / D;
+  int64_t base = row0;
+  for (int64_t g = 1; g < groups; ++g, base += D * nw) {
 #pragma unroll
-    for (int i = 0; i < PPL; ++i) cur[i] = nxt[i];
+    for (int j = 0; j < D; ++j) {
+      const int64_t r = base + j * nw;
+      emit(j, r);
+      fill(j, r + D * nw, r < n ? r : n - 1);
+    }
   }
+#pragma unroll
+  for (int j = 0; j < D; ++j) emit(j, base + j * nw);
 }
 
 // M > 1 (interim path): each piece is decoded once to exact f32 weights and
@@ -429,8 +459,8 @@ int run_multi(const rq_weight *wt, const void *x, int xtype, int64_t m, void *y,
 
 template <class F, int PPL>
 int run_long(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s) {
-  // 16 waves per CU walking rows: enough weight bytes in flight to cover
-  // HBM latency, few enough that every wave sees several rows.
+  // 16 waves per CU walking rows, each with two rows of weight loads in
+  // flight (measured best of 8 / 16 / 24 / 32 waves per CU).
   const int64_t waves = wt->n < 256 * 16 ? wt->n : 256 * 16;
   const size_t xb = xlds_bytes(wt->k);
   // Eight waves per workgroup (measured best of 4 / 8 / 16 on 14336 x 4096)
@@ -438,12 +468,17 @@ int run_long(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, 
   // not fit eight waves' registers).
   if constexpr (PPL <= 2) {
     const unsigned blocks = (unsigned)((waves + 7) / 8);
-    hipLaunchKernelGGL((k_gemv_long<F, PPL, 8>), dim3(blocks), dim3(512), xb, s, wt->data, wt->data + wt->aux_off, x,
-                       xtype, y, ytype, wt->n, wt->k, xb != 0);
+    if (long_xr<F, PPL, 8>() > 0 && !xb) return RQ_E_UNSUPPORTED;  // k <= 64 PPL PE always fits the LDS copy
+    // Two rows in flight per wave: on Q4_K 14336 x 4096, 10.5 us against
+    // 11.9 (three rows) and 13.4 (four), whose registers leave room for one
+    // eight-wave workgroup per CU instead of two.
+    hipLaunchKernelGGL((k_gemv_long<F, PPL, 8, 2>), dim3(blocks), dim3(512), xb, s, wt->data, wt->data + wt->aux_off,
+                       x, xtype, y, ytype, wt->n, wt->k, xb != 0);
   } else {
     const unsigned blocks = (unsigned)((waves + 3) / 4);
-    hipLaunchKernelGGL((k_gemv_long<F, PPL, 4>), dim3(blocks), dim3(256), xb, s, wt->data, wt->data + wt->aux_off, x,
-                       xtype, y, ytype, wt->n, wt->k, xb != 0);
+    if (long_xr<F, PPL, 4>() > 0 && !xb) return RQ_E_UNSUPPORTED;
+    hipLaunchKernelGGL((k_gemv_long<F, PPL, 4, 2>), dim3(blocks), dim3(256), xb, s, wt->data, wt->data + wt->aux_off,
+                       x, xtype, y, ytype, wt->n, wt->k, xb != 0);
   }
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }
