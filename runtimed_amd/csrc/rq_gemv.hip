@@ -142,42 +142,23 @@ __device__ __forceinline__ void load_piece_x(const void *x, int xtype, const flo
   else load_run<16>(x, xtype, F::run_off(p, r), dst);
 }
 
-// M = 1: every lane owns one piece position; its activations are loaded once
-// into registers and reused for every row it visits.  Rows with P <= 64
-// pieces sit on an aligned segment of seg = max(16, next_pow2(P)) lanes
-// (64/seg rows per wave); longer rows are split over a team of T = ceil(P/64)
-// waves whose partial sums meet in LDS.  With XR > 0 the loads of x (XR
-// 16-byte chunks per thread, L2-resident) are issued first and the first
-// row's weight loads right behind them, so x is staged in LDS while the
-// weights are still in flight; with XR = 0 (x longer than XR chunks per
-// thread cover) the weights go first and x is staged after them.  Each
-// iteration issues the next row's loads before it computes, so HBM latency
-// overlaps everything else.
+// M = 1, rows of at most 64 pieces: every lane owns one piece position; its
+// activations are loaded once into registers.  A row sits on an aligned
+// segment of seg = max(16, next_pow2(P)) lanes (64/seg rows per wave).  The
+// loads of x (XR 16-byte chunks per thread, L2-resident) are issued first
+// and the first row's weight loads right behind them, so x is staged in LDS
+// while the weights are still in flight.  A workgroup walking several row
+// groups issues the next group's loads before it computes the current one.
 template <class F, int XR>
-__global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
+__global__ __launch_bounds__(256) void k_gemv_m1(const uint8_t *__restrict__ w,
                                                 const uint8_t *__restrict__ aux,
                                                 const void *__restrict__ x, int xtype,
                                                 void *__restrict__ y, int ytype, int64_t n,
-                                                int64_t k, int seg_log2, int team,
-                                                int rows_per_wg, int64_t groups, bool xlds) {
-  __shared__ float red[8][8];
+                                                int64_t k, int seg_log2, int rows_per_wg, int64_t groups) {
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int P = (int)(k / F::PE);
-  int row_in_wg, p, tm;
-  if (team == 1) {
-    row_in_wg = wv * (64 >> seg_log2) + (lane >> seg_log2);
-    p = lane & ((1 << seg_log2) - 1);
-    tm = 0;
-  } else {
-    // wv / team and wv % team on scalar registers (wv < 8)
-    row_in_wg = 0;
-    tm = wv;
-    while (tm >= team) {
-      tm -= team;
-      ++row_in_wg;
-    }
-    p = 64 * tm + lane;
-  }
+  const int row_in_wg = wv * (64 >> seg_log2) + (lane >> seg_log2);
+  const int p = lane & ((1 << seg_log2) - 1);
   const bool live = p < P;
   // Loads use a piece and row clamped into the matrix, unconditionally:
   // a load under a branch makes the compiler drain every outstanding load
@@ -187,33 +168,19 @@ __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
   int64_t g = blockIdx.x;
   int64_t row = g * rows_per_wg + row_in_wg;
   extern __shared__ __attribute__((aligned(16))) float xs_dyn[];
-  const float *xs = nullptr;
-  typename F::Piece cur;
-  if constexpr (XR > 0) {  // launched only with the LDS copy of x
-    chunk16 xc[XR];
-    load_x_chunks<XR>(x, xtype, (int)k, xc);
-    __builtin_amdgcn_sched_barrier(0);
-    cur = F::load(w, aux, row < n ? row : n - 1, k, pl);
-    __builtin_amdgcn_sched_barrier(0);
-    store_x_chunks<XR>(xtype, (int)k, xc, xs_dyn);
-    xs = xs_dyn;
-  } else {
-    cur = F::load(w, aux, row < n ? row : n - 1, k, pl);
-    if (xlds) {  // uniform: the whole workgroup stages x once
-      stage_x(x, xtype, (int)k, xs_dyn);
-      xs = xs_dyn;
-    }
-  }
+  chunk16 xc[XR];
+  load_x_chunks<XR>(x, xtype, (int)k, xc);
+  __builtin_amdgcn_sched_barrier(0);
+  typename F::Piece cur = F::load(w, aux, row < n ? row : n - 1, k, pl);
+  __builtin_amdgcn_sched_barrier(0);
+  store_x_chunks<XR>(xtype, (int)k, xc, xs_dyn);
   float xv[F::RUNS][16];
   float sx[F::RUNS];
 #pragma unroll
   for (int r = 0; r < F::RUNS; ++r) {
     sx[r] = 0.0f;
     if (live) {
-      // With XR > 0 the LDS copy always exists; saying so at compile time
-      // keeps the global-load path (and its drain-all waits) out of the code.
-      if constexpr (XR > 0) load_run_lds<16>(xs_dyn, (int)F::run_off(p, r), xv[r]);
-      else load_piece_x<F>(x, xtype, xs, p, r, xv[r]);
+      load_run_lds<16>(xs_dyn, (int)F::run_off(p, r), xv[r]);
 #pragma unroll
       for (int t = 0; t < 16; ++t) sx[r] += xv[r][t];
     } else {
@@ -222,29 +189,13 @@ __global__ __launch_bounds__(512) void k_gemv_m1(const uint8_t *__restrict__ w,
     }
   }
 
-  // Dot product, row total and store of one row group.
+  // Dot product, segment total and store of one row group.
   auto emit = [&](const typename F::Piece &pc, int64_t r) {
     const float d = F::dot(pc, xv, sx);
     float acc = (live && r < n) ? d : 0.0f;
-    if (team == 1) {
-      const int seg = 1 << seg_log2;
-      if (seg >= 16) {
-        acc = seg_sum(acc, seg);
-      } else {
-        for (int off = seg >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-      }
-      if ((lane & (seg - 1)) == seg - 1 && r < n) store_out(y, ytype, r, acc);
-    } else {
-      acc = seg_sum(acc, 64);
-      if (lane == 63) red[row_in_wg][tm] = acc;
-      __syncthreads();
-      if (tm == 0 && lane == 63 && r < n) {
-        float tot = red[row_in_wg][0];
-        for (int t = 1; t < team; ++t) tot += red[row_in_wg][t];
-        store_out(y, ytype, r, tot);
-      }
-      __syncthreads();
-    }
+    const int seg = 1 << seg_log2;
+    acc = seg_sum(acc, seg);
+    if ((lane & (seg - 1)) == seg - 1 && r < n) store_out(y, ytype, r, acc);
   };
   // One row group per workgroup (every decode-sized matrix): no prefetch.
   // A next-row load in the last pass is never used, and the wave still has
@@ -361,6 +312,115 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv_long(const uint8_t *__restric
   }
 #pragma unroll
   for (int j = 0; j < D; ++j) emit(j, base + j * nw);
+}
+
+// A run of 16 activations at element e0 (a multiple of 16) straight from
+// global memory: four 16-byte chunks, clamped to the last chunk of x, in one
+// unconditional load form for every type (f32 uses all four, f16 / bf16 the
+// first two), converted after the loads.
+__device__ __forceinline__ void load_run_raw(const void *x, int xtype, int k, int e0, chunk16 (&v)[4]) {
+  const int nc = x_chunks(k, xtype);
+  const int c0 = e0 >> (xtype == RQ_F32 ? 2 : 3);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = reinterpret_cast<const chunk16 *>(x)[c0 + j < nc ? c0 + j : nc - 1];
+}
+
+__device__ __forceinline__ void convert_run(int xtype, const chunk16 (&v)[4], float *dst) {
+  if (xtype == RQ_F32) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      dst[4 * j + 0] = __uint_as_float(v[j].x);
+      dst[4 * j + 1] = __uint_as_float(v[j].y);
+      dst[4 * j + 2] = __uint_as_float(v[j].z);
+      dst[4 * j + 3] = __uint_as_float(v[j].w);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t wd[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        dst[8 * j + 2 * q] = xtype == RQ_BF16 ? __uint_as_float(wd[q] << 16) : h2f(wd[q]);
+        dst[8 * j + 2 * q + 1] = xtype == RQ_BF16 ? __uint_as_float(wd[q] & 0xFFFF0000u) : h2f(wd[q] >> 16);
+      }
+    }
+  }
+}
+
+// M = 1, long rows on fewer rows (P > 64 pieces, n < 4096): a workgroup is
+// one team of T = blockDim / 64 waves covering a row's pieces (piece
+// 64 tm + lane), walking the rows blockIdx.x, blockIdx.x + gridDim.x, ...
+// with D rows of weight loads in flight (static slots, unconditional loads,
+// as in k_gemv_long).  The team's lanes hold disjoint pieces, so each lane
+// loads its own activations straight from global memory, once: x is read
+// once per workgroup and needs no LDS copy or barrier.  Those loads go out
+// before the first weight loads (the load counter retires in order).  Each
+// row's wave sums go to LDS; after the last row one barrier, then one thread
+// per row adds the T partial sums.  At most kTeamRows rows per workgroup.
+constexpr int kTeamRows = 64;
+constexpr int kTeamMax = 16;
+
+template <class F, int D>
+__global__ __launch_bounds__(1024) void k_gemv_team(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
+                                                   const void *__restrict__ x, int xtype, void *__restrict__ y,
+                                                   int ytype, int64_t n, int64_t k) {
+  __shared__ float red[kTeamRows][kTeamMax];
+  const int lane = threadIdx.x & 63, tm = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int team = (int)(blockDim.x >> 6);
+  const int P = (int)(k / F::PE);
+  const int p = 64 * tm + lane;
+  const bool live = p < P;
+  const int pl = live ? p : P - 1;
+  const int64_t r0 = blockIdx.x, stride = gridDim.x;
+  const int rows = r0 < n ? (int)((n - r0 + stride - 1) / stride) : 0;  // rows of this workgroup
+
+  chunk16 xc[F::RUNS][4];
+#pragma unroll
+  for (int r = 0; r < F::RUNS; ++r) load_run_raw(x, xtype, (int)k, (int)F::run_off(pl, r), xc[r]);
+  __builtin_amdgcn_sched_barrier(0);
+  typename F::Piece sl[D];
+  const int64_t first = r0 < n ? r0 : n - 1;
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    const int64_t r = r0 + j * stride;
+    sl[j] = F::load(w, aux, r < n ? r : first, k, pl);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float xv[F::RUNS][16];
+  float sx[F::RUNS];
+#pragma unroll
+  for (int r = 0; r < F::RUNS; ++r) {
+    convert_run(xtype, xc[r], xv[r]);
+    sx[r] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) sx[r] += xv[r][t];
+  }
+
+  auto emit = [&](int j, int i) {  // slot j holds row r0 + i * stride
+    const float d = F::dot(sl[j], xv, sx);
+    float acc = (live && i < rows) ? d : 0.0f;
+    acc = seg_sum(acc, 64);
+    if (lane == 63 && i < rows) red[i][tm] = acc;
+  };
+  const int groups = (rows + D - 1) / D;
+  int base = 0;
+  for (int g = 1; g < groups; ++g, base += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const int i = base + j;
+      emit(j, i);
+      const int64_t r = r0 + (int64_t)i * stride, rn = r + D * stride;
+      sl[j] = F::load(w, aux, rn < n ? rn : r, k, pl);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < D; ++j) emit(j, base + j);
+  __syncthreads();
+  for (int i = (int)threadIdx.x; i < rows; i += (int)blockDim.x) {
+    float tot = red[i][0];
+    for (int t = 1; t < team; ++t) tot += red[i][t];
+    store_out(y, ytype, r0 + (int64_t)i * stride, tot);
+  }
 }
 
 // M > 1 (interim path): each piece is decoded once to exact f32 weights and
@@ -486,9 +546,7 @@ int run_long(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, 
 template <class F>
 int run_m1(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s) {
   const int P = (int)(wt->k / F::PE);
-  // Long rows on many rows: one wave per row walking the rows.  Fewer rows
-  // (a decode-sized matrix) keep the team layout, which starts every row at
-  // once.
+  // Long rows on many rows: one wave per row walking the rows.
   if (P > 64 && wt->n >= 4096) {
     switch ((P + 63) / 64) {
       case 2: return run_long<F, 2>(wt, x, xtype, y, ytype, s);
@@ -497,36 +555,34 @@ int run_m1(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hi
       default: break;
     }
   }
-  int seg_log2 = 6, team = 1, rows_per_wg, threads;
-  if (P <= 64) {
-    seg_log2 = ceil_log2(P < 16 ? 16 : P);
-    rows_per_wg = 4 * (64 >> seg_log2);
-    threads = 256;
-  } else {
-    team = (P + 63) / 64;
-    if (team > 8) return RQ_E_UNSUPPORTED;
-    rows_per_wg = 8 / team;
-    threads = 64 * team * rows_per_wg;
+  // Other long rows: a team of waves per row, each workgroup walking up to
+  // kTeamRows rows; about 512 workgroups (measured best of 128-2048 on
+  // 896 x 4864, 2048 x 8192 and 4096 x 14336).
+  if (P > 64) {
+    const int team = (P + 63) / 64;
+    if (team > kTeamMax) return RQ_E_UNSUPPORTED;
+    int64_t per = (wt->n + 511) / 512;
+    if (per > kTeamRows) per = kTeamRows;
+    const int64_t grid = (wt->n + per - 1) / per;
+    if (grid > 0x7FFFFFFF) return RQ_E_UNSUPPORTED;
+    hipLaunchKernelGGL((k_gemv_team<F, 2>), dim3((unsigned)grid), dim3(64 * team), 0, s, wt->data,
+                       wt->data + wt->aux_off, x, xtype, y, ytype, wt->n, wt->k);
+    return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
   }
+  const int seg_log2 = ceil_log2(P < 16 ? 16 : P);
+  const int rows_per_wg = 4 * (64 >> seg_log2);
   const int64_t groups = (wt->n + rows_per_wg - 1) / rows_per_wg;
   const unsigned blocks = (unsigned)(groups < 16384 ? groups : 16384);
+  // k <= 64 pieces always fits the LDS copy of x (x is 16-byte aligned here);
+  // chunks of x per thread: at most 64 PE / 4 / 256 = 4.
   const size_t xb = xlds_bytes(wt->k);
-  // x chunks per thread when x is staged (x is 16-byte aligned here); more
-  // than four keep the weights-first order.
-  int xr = 0;
-  if (xb && wt->k % 8 == 0) {
-    const int per = (x_chunks(wt->k, xtype) + threads - 1) / threads;
-    xr = per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 0;
-  }
-#define RQ_M1(XR)                                                                                               \
-  hipLaunchKernelGGL((k_gemv_m1<F, XR>), dim3(blocks), dim3(threads), xb, s, wt->data, wt->data + wt->aux_off, \
-                     x, xtype, y, ytype, wt->n, wt->k, seg_log2, team, rows_per_wg, groups, xb != 0)
-  switch (xr) {
-    case 1: RQ_M1(1); break;
-    case 2: RQ_M1(2); break;
-    case 4: RQ_M1(4); break;
-    default: RQ_M1(0); break;
-  }
+  const int per = (x_chunks(wt->k, xtype) + 255) / 256;
+#define RQ_M1(XR)                                                                                           \
+  hipLaunchKernelGGL((k_gemv_m1<F, XR>), dim3(blocks), dim3(256), xb, s, wt->data, wt->data + wt->aux_off, \
+                     x, xtype, y, ytype, wt->n, wt->k, seg_log2, rows_per_wg, groups)
+  if (per <= 1) RQ_M1(1);
+  else if (per <= 2) RQ_M1(2);
+  else RQ_M1(4);
 #undef RQ_M1
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }

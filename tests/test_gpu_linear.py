@@ -52,13 +52,16 @@ def test_decode_gemv_f32(dev, qtype, n, k):
     (rq.Q4_K, 512, 2048),   # 2 / 1
     (rq.Q6_K, 256, 4096),   # 4 / 2
     (rq.Q6_K, 128, 896),    # 1 / 1, Q6_K rows starting mid-block
-    (rq.Q4_K, 896, 4864),   # three-wave teams: 4 / 2
-    (rq.Q4_K, 64, 12288),   # six-wave teams: f32 x staged after the weights, 16-bit 4
+    (rq.Q4_K, 896, 4864),   # three-wave teams, two rows per workgroup
+    (rq.Q4_K, 64, 12288),   # six-wave teams
     (rq.Q8_0, 96, 16384),   # x too long for the LDS copy
+    (rq.Q4_K, 1100, 20480),  # a ten-wave team, three rows per workgroup
+    (rq.Q8_0, 4097, 8224),   # 257 pieces a row on n >= 4096: five-wave teams
 ])
 def test_decode_gemv_activation_types(dev, xdt, qtype, n, k):
-    # M = 1 with each activation type: x is staged in LDS from raw 16-byte
-    # chunks (4 f32 or 8 f16/bf16 values) before the weights arrive
+    # M = 1 with each activation type: x is read as raw 16-byte chunks (4 f32
+    # or 8 f16/bf16 values) before the weights arrive, staged in LDS or, for
+    # team layouts, held by the lanes that use it
     print(f"gemv x={xdt} qtype={qtype} n={n} k={k}", flush=True)
     w, wf = make(qtype, n, k, 20 + n + k)
     x = torch.from_numpy(synth.activations(4, 1, k)).to(xdt)
