@@ -14,6 +14,7 @@
 // scale[r] is applied once at the end as in the reference (acc * scale).
 // Bound: HBM, 0.5 byte per weight + 4 bytes of scale per row.
 #include "rq_e4m3.h"
+#include "rq_formats.h"
 #include "rq_internal.h"
 
 namespace rq {
@@ -170,12 +171,160 @@ __global__ __launch_bounds__(512) void k_marlin_gemv(const uint4 *__restrict__ p
   }
 }
 
+// M = 1, 16-byte aligned x, k % 32 == 0, x in 64 KB of LDS: x is loaded first as
+// raw 16-byte chunks (XR a thread; 4 f32 or 8 f16/bf16 values each, one
+// unconditional load form), the first batch of records right behind it, and
+// x is staged in LDS -- with the sum of each 32-input chunk -- while the
+// records are in flight (the load counter retires in issue order: loads of
+// x issued after the records would hold the staging until the records had
+// landed).  Record loads (B a lane per batch) are unconditional on clamped chunks and rows;
+// records past kc are selected away, not branched around (a load whose
+// result is used under a branch is sunk into it).  A record's dot product is
+// sum x q - 8 sum x, with q converted from masked bytes (low nibbles 0x0F0F0F0F
+// of a word are inputs 0, 2, 4, 6; the high ones 1, 3, 5, 7).
+typedef uint32_t mchunk __attribute__((ext_vector_type(4)));
+
+template <int R, int XR, int B>
+__global__ __launch_bounds__(512) void k_marlin_gemv_x(const mchunk *__restrict__ packed, const float *__restrict__ s,
+                                                       const void *__restrict__ x, int xtype, int64_t n, int64_t k,
+                                                       int64_t kc, void *__restrict__ y, int ytype) {
+  constexpr int GROUPS = 64 / R;      // lane groups per wave
+  constexpr int SLOTS = 8 * GROUPS;   // chunk slots per workgroup
+  __shared__ float red[8][R];
+  extern __shared__ __attribute__((aligned(16))) float xs[];  // k activations, then kc chunk sums
+  float *const xsum = xs + k;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rl = lane % R;
+  const int64_t row = (int64_t)blockIdx.x * R + rl;
+  const int64_t rowc = row < n ? row : n - 1;
+  const int slot = wave * GROUPS + lane / R;
+
+  const int epc = xtype == RQ_F32 ? 4 : 8;
+  const int nc = (int)(k / epc);
+  const mchunk *xc0 = static_cast<const mchunk *>(x);
+  mchunk xr[XR];
+#pragma unroll
+  for (int i = 0; i < XR; ++i) {
+    const int c = (int)threadIdx.x + 512 * i;
+    xr[i] = xc0[c < nc ? c : nc - 1];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  mchunk q[B];
+  auto fetch = [&](int64_t c0) {
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const int64_t c = c0 + j * SLOTS;
+      q[j] = packed[(c < kc ? c : kc - 1) * n + rowc];
+    }
+  };
+  fetch(slot);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < XR; ++i) {
+    const int c0 = (int)threadIdx.x + 512 * i;
+    const int c = c0 < nc ? c0 : nc - 1;
+    const mchunk u = xr[i];
+    if (xtype == RQ_F32) {
+      *reinterpret_cast<float4 *>(xs + 4 * c) =
+          make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+    } else {
+      float f[8];
+      const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = wd[j] & 0xFFFFu, hi = wd[j] >> 16;
+        f[2 * j] = xtype == RQ_BF16 ? __uint_as_float(lo << 16) : (float)__builtin_bit_cast(_Float16, (uint16_t)lo);
+        f[2 * j + 1] =
+            xtype == RQ_BF16 ? __uint_as_float(hi << 16) : (float)__builtin_bit_cast(_Float16, (uint16_t)hi);
+      }
+      *reinterpret_cast<float4 *>(xs + 8 * c) = make_float4(f[0], f[1], f[2], f[3]);
+      *reinterpret_cast<float4 *>(xs + 8 * c + 4) = make_float4(f[4], f[5], f[6], f[7]);
+    }
+  }
+  __syncthreads();
+  for (int c = (int)threadIdx.x; c < (int)kc; c += 512) {
+    float t = 0.0f;
+#pragma unroll
+    for (int j4 = 0; j4 < 8; ++j4) {
+      const float4 v = *reinterpret_cast<const float4 *>(xs + 32 * c + 4 * j4);
+      t += (v.x + v.y) + (v.z + v.w);
+    }
+    xsum[c] = t;
+  }
+  __syncthreads();
+
+  float acc = 0.0f;
+  for (int64_t c0 = slot; c0 < kc; c0 += B * SLOTS) {
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const int64_t c = c0 + j * SLOTS;
+      const int64_t cc = c < kc ? c : kc - 1;
+      const float *xp = xs + 32 * cc;
+      const uint32_t wd[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+      float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {  // word w: inputs 8w .. 8w + 7
+        const float4 xa = *reinterpret_cast<const float4 *>(xp + 8 * w);
+        const float4 xb = *reinterpret_cast<const float4 *>(xp + 8 * w + 4);
+        const uint32_t lo = opaque(wd[w] & 0x0F0F0F0Fu), hi = opaque((wd[w] >> 4) & 0x0F0F0F0Fu);
+        a0 = fmaf(xa.x, ub(lo, 0), a0);
+        a1 = fmaf(xa.y, ub(hi, 0), a1);
+        a0 = fmaf(xa.z, ub(lo, 1), a0);
+        a1 = fmaf(xa.w, ub(hi, 1), a1);
+        a0 = fmaf(xb.x, ub(lo, 2), a0);
+        a1 = fmaf(xb.y, ub(hi, 2), a1);
+        a0 = fmaf(xb.z, ub(lo, 3), a0);
+        a1 = fmaf(xb.w, ub(hi, 3), a1);
+      }
+      const float d = (a0 + a1) - 8.0f * xsum[cc];
+      acc += c < kc ? d : 0.0f;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (c0 + B * SLOTS < kc) fetch(c0 + B * SLOTS);
+  }
+#pragma unroll
+  for (int off = R; off < 64; off <<= 1) acc += __shfl_xor(acc, off);
+  if (lane < R) red[wave][rl] = acc;
+  __syncthreads();
+  if (threadIdx.x < R) {
+    const int l = threadIdx.x;
+    const int64_t orow = (int64_t)blockIdx.x * R + l;
+    if (orow < n) {
+      float v = 0.0f;
+#pragma unroll
+      for (int wv = 0; wv < 8; ++wv) v += red[wv][l];
+      store_out(y, ytype, orow, v * s[orow]);
+    }
+  }
+}
+
 template <int R, int MT>
 void launch_gemv(const uint4 *packed, const float *s, const void *x, int xtype, int64_t m, int64_t n, int64_t k,
                  int64_t kc, void *y, int ytype, bool vec, hipStream_t st) {
   const dim3 grid((unsigned)((n + R - 1) / R), (unsigned)((m + MT - 1) / MT));
   // MT rows of f32 activations in LDS when they fit in 64 KB.
   const size_t xb = (size_t)MT * k * sizeof(float) <= 65536 ? (size_t)MT * k * sizeof(float) : 0;
+  // x and its chunk sums in at most 64 KB of LDS; x chunks a thread: k / (4 or 8) / 512 <= 8.
+  if (MT == 1 && m == 1 && vec && k % 32 == 0 && (k + kc) * (int64_t)sizeof(float) <= 65536) {
+    const int64_t per = (k / (xtype == RQ_F32 ? 4 : 8) + 511) / 512;
+    const size_t xsb = (size_t)(k + kc) * sizeof(float);
+    const mchunk *pk = reinterpret_cast<const mchunk *>(packed);
+    // Records a lane loads per batch: one when a lane has at most one
+    // (decode-sized rows; the registers of four cost the second workgroup
+    // per CU), else four.
+    const bool one = kc <= 8 * (64 / R);
+#define RQ_MX(XR)                                                                                                    \
+  if (one)                                                                                                           \
+    hipLaunchKernelGGL((k_marlin_gemv_x<R, XR, 1>), grid, dim3(512), xsb, st, pk, s, x, xtype, n, k, kc, y, ytype); \
+  else                                                                                                               \
+    hipLaunchKernelGGL((k_marlin_gemv_x<R, XR, 4>), grid, dim3(512), xsb, st, pk, s, x, xtype, n, k, kc, y, ytype)
+    if (per <= 1) { RQ_MX(1); }
+    else if (per <= 2) { RQ_MX(2); }
+    else if (per <= 4) { RQ_MX(4); }
+    else { RQ_MX(8); }
+#undef RQ_MX
+    return;
+  }
   hipLaunchKernelGGL((k_marlin_gemv<R, MT>), grid, dim3(512), xb, st, packed, s, x, xtype, m, n, k, kc, y, ytype,
                      vec, xb != 0);
 }
