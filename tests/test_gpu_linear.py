@@ -284,3 +284,39 @@ def test_fused_weights_concatenate(dev, qtype):
     sep = [rq.QWeight(qtype, d, n, 896).forward(x) for d, (n, _) in zip(data, parts)]
     fused = rq.QWeight(qtype, np.concatenate(data), 1152, 896).forward(x)
     assert torch.equal(fused, torch.cat(sep, dim=1))
+
+
+def _random_cases(count=48, seed=2024):
+    """Seeded shapes across every format, activation type and row count: rows
+    that straddle blocks, n not a multiple of any tile, k from one block to a
+    few thousand, M from the GEMV through the small-M kernels to the tiled
+    GEMM and the f32 slices."""
+    rng = np.random.default_rng(seed)
+    ks = [32, 64, 96, 160, 256, 384, 896, 1024, 1088, 2048, 2304, 4864, 5120]
+    ms = [1, 1, 1, 2, 3, 4, 7, 16, 17, 33, 64, 65, 130]
+    xts = [torch.float32, torch.float16, torch.bfloat16]
+    out = []
+    while len(out) < count:
+        qt = ALL_FORMATS[rng.integers(len(ALL_FORMATS))]
+        k = int(ks[rng.integers(len(ks))])
+        elems = rq.GEOMETRY[qt][0]
+        n = int(rng.integers(1, 3000))
+        while (n * k) % elems:
+            n += 1
+        if n * k > 6_000_000:
+            continue
+        out.append((qt, n, k, int(ms[rng.integers(len(ms))]), xts[rng.integers(len(xts))]))
+    return out
+
+
+@pytest.mark.parametrize("qtype,n,k,m,xdt", _random_cases())
+def test_random_shapes(dev, qtype, n, k, m, xdt):
+    print(f"random qtype={qtype} n={n} k={k} m={m} x={xdt}", flush=True)
+    w, wf = make(qtype, n, k, 7 * n + k + m)
+    x = torch.from_numpy(synth.activations(n + m, m, k)).to(xdt)
+    y = w.forward(x.to(dev), out_dtype=torch.float32).cpu().numpy()
+    assert y.shape == (m, n)
+    # bf16 activations with m > 1 run on bf16 matrix cores (weights rounded to
+    # bf16); every other case keeps exact weights and f32 accumulation
+    tol = TOL_BF16 if (xdt == torch.bfloat16 and m > 1) else TOL_F32
+    assert norm_err(y, ref(x.float().numpy(), wf)) <= tol
