@@ -117,6 +117,43 @@ struct FmtQ4K {
     const float shh = ((dh[0] + dh[1]) + (dh[2] + dh[3])) * 0.0625f;  // high nibbles were x16
     return (a0 * sl - b0 * sx[0]) + (a1 * shh - b1 * sx[1]);
   }
+  // dot() for MR activation rows at once: the codes are converted once and
+  // every row's sums run in dot()'s order (row i's result equals dot() on
+  // row i).
+  template <int MR>
+  __device__ __forceinline__ static void dot_rows(const Piece &pc, const float (&xv)[MR][RUNS][16],
+                                                  const float (&sx)[MR][RUNS], float (&out)[MR]) {
+    float a0, b0, a1, b1;
+    scales(pc, a0, b0, a1, b1);
+    const uint32_t q[4] = {pc.qv.x, pc.qv.y, pc.qv.z, pc.qv.w};
+    float wl[16], wh[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = opaque(q[j] & 0x0F0F0F0Fu), hi = opaque(q[j] & 0xF0F0F0F0u);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        wl[4 * j + b] = ub(lo, b);
+        wh[4 * j + b] = ub(hi, b);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+      float dl[4], dh[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        dl[j] = xv[i][0][4 * j] * wl[4 * j];
+        dh[j] = xv[i][1][4 * j] * wh[4 * j];
+#pragma unroll
+        for (int b = 1; b < 4; ++b) {
+          dl[j] = fmaf(xv[i][0][4 * j + b], wl[4 * j + b], dl[j]);
+          dh[j] = fmaf(xv[i][1][4 * j + b], wh[4 * j + b], dh[j]);
+        }
+      }
+      const float sl = (dl[0] + dl[1]) + (dl[2] + dl[3]);
+      const float shh = ((dh[0] + dh[1]) + (dh[2] + dh[3])) * 0.0625f;
+      out[i] = (a0 * sl - b0 * sx[i][0]) + (a1 * shh - b1 * sx[i][1]);
+    }
+  }
   // Weights of the piece as bf16 pairs in run order (o[8r + j]: elements
   // 2j, 2j + 1 of run r) for the MFMA GEMM: one fused multiply-add per
   // weight (a single rounding, then the bf16 rounding), not the exact

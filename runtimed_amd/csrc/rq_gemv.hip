@@ -24,12 +24,20 @@
 //
 // Roofline: HBM-bound.  Algorithmic bytes per call = GGUF block bytes of W +
 // activation bytes + output bytes.
+#include <type_traits>
+
 #include "rq_formats.h"
 
 namespace rq {
 namespace {
 
 constexpr int kThreads = 256;
+
+// Formats with a multi-row dot product (F::dot_rows<MR>).
+template <class F, class = void>
+struct has_dot_rows : std::false_type {};
+template <class F>
+struct has_dot_rows<F, std::void_t<decltype(&F::template dot_rows<2>)>> : std::true_type {};
 
 // --------------------------------------------------------------- kernels --
 
@@ -58,7 +66,7 @@ __device__ __forceinline__ float seg_sum(float v, int seg) {
 // banks.  A run of 16 activations never crosses a padding gap.
 constexpr int64_t kXldsMaxK = 12288;
 __device__ __forceinline__ int xpad(int e) { return e + 4 * (e >> 6); }
-inline size_t xlds_bytes(int64_t k) { return k <= kXldsMaxK ? (size_t)(k + 4 * (k >> 6) + 4) * sizeof(float) : 0; }
+__host__ __device__ inline size_t xlds_bytes(int64_t k) { return k <= kXldsMaxK ? (size_t)(k + 4 * (k >> 6) + 4) * sizeof(float) : 0; }
 
 __device__ __forceinline__ void stage_x(const void *x, int xtype, int k, float *xs) {
   for (int e = 4 * (int)threadIdx.x; e < k; e += 4 * (int)blockDim.x)
@@ -122,6 +130,48 @@ __device__ __forceinline__ void store_x_chunks(int xtype, int k, const chunk16 (
   __syncthreads();
 }
 
+// store_x_chunks for MR activation rows loaded as one run of chunks: chunk
+// c holds elements [c e, (c + 1) e) of the flattened [MR][k] block (e = 4
+// or 8 values; k is a multiple of e), stored in row c e / k at xstride.
+template <int XR>
+__device__ __forceinline__ void store_x_chunks_rows(int xtype, int k, int mr, int xstride, const chunk16 (&v)[XR],
+                                                    float *xs) {
+  const int epc = xtype == RQ_F32 ? 4 : 8;
+  const int nc = mr * k / epc;
+#pragma unroll
+  for (int i = 0; i < XR; ++i) {
+    const int c0 = (int)threadIdx.x + i * (int)blockDim.x;
+    const int c = c0 < nc ? c0 : nc - 1;
+    int e = c * epc, row = 0;
+    while (e >= k) {  // mr <= 2: at most one step
+      e -= k;
+      ++row;
+    }
+    float *dst = xs + row * xstride;
+    const chunk16 u = v[i];
+    if (xtype == RQ_F32) {
+      *reinterpret_cast<float4 *>(dst + xpad(e)) =
+          make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+    } else {
+      float f[8];
+      const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (xtype == RQ_BF16) {
+          f[2 * j] = __uint_as_float(wd[j] << 16);
+          f[2 * j + 1] = __uint_as_float(wd[j] & 0xFFFF0000u);
+        } else {
+          f[2 * j] = h2f(wd[j]);
+          f[2 * j + 1] = h2f(wd[j] >> 16);
+        }
+      }
+      *reinterpret_cast<float4 *>(dst + xpad(e)) = make_float4(f[0], f[1], f[2], f[3]);
+      *reinterpret_cast<float4 *>(dst + xpad(e + 4)) = make_float4(f[4], f[5], f[6], f[7]);
+    }
+  }
+  __syncthreads();
+}
+
 template <int LEN>
 __device__ __forceinline__ void load_run_lds(const float *xs, int e0, float *dst) {
   const float4 *src = reinterpret_cast<const float4 *>(xs + xpad(e0));
@@ -142,14 +192,15 @@ __device__ __forceinline__ void load_piece_x(const void *x, int xtype, const flo
   else load_run<16>(x, xtype, F::run_off(p, r), dst);
 }
 
-// M = 1, rows of at most 64 pieces: every lane owns one piece position; its
-// activations are loaded once into registers.  A row sits on an aligned
+// M = MR (1 or 2), rows of at most 64 pieces: every lane owns one piece
+// position; its activations (MR rows) are loaded once into registers, and a
+// piece's weights are converted once for the MR dot products.  A row sits on an aligned
 // segment of seg = max(16, next_pow2(P)) lanes (64/seg rows per wave).  The
 // loads of x (XR 16-byte chunks per thread, L2-resident) are issued first
 // and the first row's weight loads right behind them, so x is staged in LDS
 // while the weights are still in flight.  A workgroup walking several row
 // groups issues the next group's loads before it computes the current one.
-template <class F, int XR>
+template <class F, int XR, int MR>
 __global__ __launch_bounds__(256) void k_gemv_m1(const uint8_t *__restrict__ w,
                                                 const uint8_t *__restrict__ aux,
                                                 const void *__restrict__ x, int xtype,
@@ -168,34 +219,50 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const uint8_t *__restrict__ w,
   int64_t g = blockIdx.x;
   int64_t row = g * rows_per_wg + row_in_wg;
   extern __shared__ __attribute__((aligned(16))) float xs_dyn[];
+  // MR activation rows (x is [MR][k], contiguous) as one run of chunks; row
+  // i of the LDS copy starts at i * xstride.
+  const int xstride = (int)(xlds_bytes(k) / sizeof(float));
   chunk16 xc[XR];
-  load_x_chunks<XR>(x, xtype, (int)k, xc);
+  load_x_chunks<XR>(x, xtype, MR * (int)k, xc);
   __builtin_amdgcn_sched_barrier(0);
   typename F::Piece cur = F::load(w, aux, row < n ? row : n - 1, k, pl);
   __builtin_amdgcn_sched_barrier(0);
-  store_x_chunks<XR>(xtype, (int)k, xc, xs_dyn);
-  float xv[F::RUNS][16];
-  float sx[F::RUNS];
+  if constexpr (MR == 1) store_x_chunks<XR>(xtype, (int)k, xc, xs_dyn);
+  else store_x_chunks_rows<XR>(xtype, (int)k, MR, xstride, xc, xs_dyn);
+  float xv[MR][F::RUNS][16];
+  float sx[MR][F::RUNS];
 #pragma unroll
-  for (int r = 0; r < F::RUNS; ++r) {
-    sx[r] = 0.0f;
-    if (live) {
-      load_run_lds<16>(xs_dyn, (int)F::run_off(p, r), xv[r]);
+  for (int i = 0; i < MR; ++i)
 #pragma unroll
-      for (int t = 0; t < 16; ++t) sx[r] += xv[r][t];
+    for (int r = 0; r < F::RUNS; ++r) {
+      sx[i][r] = 0.0f;
+      if (live) {
+        load_run_lds<16>(xs_dyn + i * xstride, (int)F::run_off(p, r), xv[i][r]);
+#pragma unroll
+        for (int t = 0; t < 16; ++t) sx[i][r] += xv[i][r][t];
+      } else {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) xv[i][r][t] = 0.0f;
+      }
+    }
+
+  // Dot products, segment totals and stores of one row group.
+  auto emit = [&](const typename F::Piece &pc, int64_t r) {
+    float dr[MR];
+    if constexpr (MR > 1 && has_dot_rows<F>::value) {
+      F::template dot_rows<MR>(pc, xv, sx, dr);
     } else {
 #pragma unroll
-      for (int t = 0; t < 16; ++t) xv[r][t] = 0.0f;
+      for (int i = 0; i < MR; ++i) dr[i] = F::dot(pc, xv[i], sx[i]);
     }
-  }
-
-  // Dot product, segment total and store of one row group.
-  auto emit = [&](const typename F::Piece &pc, int64_t r) {
-    const float d = F::dot(pc, xv, sx);
-    float acc = (live && r < n) ? d : 0.0f;
-    const int seg = 1 << seg_log2;
-    acc = seg_sum(acc, seg);
-    if ((lane & (seg - 1)) == seg - 1 && r < n) store_out(y, ytype, r, acc);
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+      const float d = dr[i];
+      float acc = (live && r < n) ? d : 0.0f;
+      const int seg = 1 << seg_log2;
+      acc = seg_sum(acc, seg);
+      if ((lane & (seg - 1)) == seg - 1 && r < n) store_out(y, ytype, i * n + r, acc);
+    }
   };
   // One row group per workgroup (every decode-sized matrix): no prefetch.
   // A next-row load in the last pass is never used, and the wave still has
@@ -543,6 +610,9 @@ int run_long(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, 
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }
 
+template <class F, int MR>
+int run_seg(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s);
+
 template <class F>
 int run_m1(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s) {
   const int P = (int)(wt->k / F::PE);
@@ -569,21 +639,34 @@ int run_m1(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hi
                        wt->data + wt->aux_off, x, xtype, y, ytype, wt->n, wt->k);
     return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
   }
+  return run_seg<F, 1>(wt, x, xtype, y, ytype, s);
+}
+
+// Rows of at most 64 pieces, MR activation rows: the segment kernel.
+template <class F, int MR>
+int run_seg(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s) {
+  const int P = (int)(wt->k / F::PE);
   const int seg_log2 = ceil_log2(P < 16 ? 16 : P);
   const int rows_per_wg = 4 * (64 >> seg_log2);
   const int64_t groups = (wt->n + rows_per_wg - 1) / rows_per_wg;
   const unsigned blocks = (unsigned)(groups < 16384 ? groups : 16384);
   // k <= 64 pieces always fits the LDS copy of x (x is 16-byte aligned here);
-  // chunks of x per thread: at most 64 PE / 4 / 256 = 4.
-  const size_t xb = xlds_bytes(wt->k);
-  const int per = (x_chunks(wt->k, xtype) + 255) / 256;
-#define RQ_M1(XR)                                                                                           \
-  hipLaunchKernelGGL((k_gemv_m1<F, XR>), dim3(blocks), dim3(256), xb, s, wt->data, wt->data + wt->aux_off, \
+  // chunks of x per thread: at most MR 64 PE / 4 / 256 = 4 MR.
+  const size_t xb = MR * xlds_bytes(wt->k);
+  const int per = (x_chunks(MR * wt->k, xtype) + 255) / 256;
+#define RQ_M1(XR)                                                                                               \
+  hipLaunchKernelGGL((k_gemv_m1<F, XR, MR>), dim3(blocks), dim3(256), xb, s, wt->data, wt->data + wt->aux_off, \
                      x, xtype, y, ytype, wt->n, wt->k, seg_log2, rows_per_wg, groups)
-  if (per <= 1) RQ_M1(1);
-  else if (per <= 2) RQ_M1(2);
-  else RQ_M1(4);
-#undef RQ_M1
+  if (per <= 1) {
+    RQ_M1(1);
+  } else if (per <= 2) {
+    RQ_M1(2);
+  } else if constexpr (MR == 1) {
+    RQ_M1(4);
+  } else {
+    if (per <= 4) RQ_M1(4);
+    else RQ_M1(8);
+  }
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }
 
@@ -593,6 +676,9 @@ int dispatch_fmt(const rq_weight *wt, const void *x, int xtype, int64_t m, void 
   if (wt->k % F::PE != 0) return RQ_E_UNSUPPORTED;
   if (m == 1) return run_m1<F>(wt, x, xtype, y, ytype, s);
   const int P = (int)(wt->k / F::PE);
+  // Two activation rows on the segment kernel: each weight decoded once,
+  // one FMA per weight and row.
+  if (m == 2 && P <= 64 && wt->k % 8 == 0) return run_seg<F, 2>(wt, x, xtype, y, ytype, s);
   if (P <= 32) return run_multi<F, 1>(wt, x, xtype, m, y, ytype, ceil_log2(P), s);
   const int ppl = (P + 63) / 64;
   if (ppl > MAXPPL) return RQ_E_UNSUPPORTED;
@@ -614,7 +700,13 @@ int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m
   // bf16 activations with m > 1 run on the matrix cores: up to 64 rows with
   // the weights as the A operand decoded straight into registers, beyond
   // that the LDS-tiled GEMM.
-  if (m > 1 && xtype == RQ_BF16) {
+  // Two rows of rows with at most 64 pieces stay on the VALU segment kernel
+  // (a weight decoded once, one FMA per weight and row; exact f32 weights).
+  const int seg_pe = wt->qtype == RQ_Q6_K ? 64 : 32;
+  const bool two_rows_seg = m == 2 && wt->k % (2 * seg_pe) == 0 && wt->k / seg_pe <= 64 &&
+                            (wt->qtype == RQ_Q4_K || wt->qtype == RQ_Q6_K || wt->qtype == RQ_Q8_0 ||
+                             wt->qtype == RQ_Q5_K || wt->qtype == RQ_Q4_0 || wt->qtype == RQ_Q5_0);
+  if (m > 1 && xtype == RQ_BF16 && !two_rows_seg) {
     int rc = m <= 64 ? launch_linear_smallm(wt, x, m, y, ytype, s) : RQ_E_UNSUPPORTED;
     if (rc == RQ_E_UNSUPPORTED) rc = launch_linear_mfma(wt, x, m, y, ytype, s);
     if (rc != RQ_E_UNSUPPORTED) return rc;

@@ -71,6 +71,24 @@ def test_decode_gemv_activation_types(dev, xdt, qtype, n, k):
     assert norm_err(y, ref(x.float().numpy(), wf)) <= TOL_F32
 
 
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("qtype,n,k", [(rq.Q4_K, 4864, 896), (rq.Q4_K, 130, 2048), (rq.Q6_K, 896, 896),
+                                       (rq.Q8_0, 128, 896), (rq.Q5_K, 300, 512), (rq.Q4_0, 64, 2048),
+                                       (rq.Q5_0, 77, 256)])
+def test_two_rows_exact_weights(dev, xdt, qtype, n, k):
+    # M = 2 on rows of at most 64 pieces runs the GEMV with both activation
+    # rows: exact f32 weights and f32 accumulation for every activation type,
+    # and each row's result equal, bit for bit, to the M = 1 result of that row
+    print(f"two rows x={xdt} qtype={qtype} n={n} k={k}", flush=True)
+    w, wf = make(qtype, n, k, 40 + n + k)
+    x = torch.from_numpy(synth.activations(9, 2, k)).to(xdt).to(dev)
+    y = w.forward(x, out_dtype=torch.float32)
+    assert norm_err(y.cpu().numpy(), ref(x.float().cpu().numpy(), wf)) <= TOL_F32
+    for i in range(2):
+        y1 = w.forward(x[i:i + 1].contiguous(), out_dtype=torch.float32)
+        assert torch.equal(y[i:i + 1], y1)
+
+
 @pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0])
 @pytest.mark.parametrize("m", [2, 4, 8, 16, 64])
 def test_verify_small_m_bf16(dev, qtype, m):
