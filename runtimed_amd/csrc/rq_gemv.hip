@@ -427,11 +427,11 @@ __device__ __forceinline__ void convert_run(int xtype, const chunk16 (&v)[4], fl
 constexpr int kTeamRows = 64;
 constexpr int kTeamMax = 16;
 
-template <class F, int D>
+template <class F, int D, int MR>
 __global__ __launch_bounds__(1024) void k_gemv_team(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
                                                    const void *__restrict__ x, int xtype, void *__restrict__ y,
                                                    int ytype, int64_t n, int64_t k) {
-  __shared__ float red[kTeamRows][kTeamMax];
+  __shared__ float red[MR][kTeamRows][kTeamMax];
   const int lane = threadIdx.x & 63, tm = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int team = (int)(blockDim.x >> 6);
   const int P = (int)(k / F::PE);
@@ -441,9 +441,13 @@ __global__ __launch_bounds__(1024) void k_gemv_team(const uint8_t *__restrict__ 
   const int64_t r0 = blockIdx.x, stride = gridDim.x;
   const int rows = r0 < n ? (int)((n - r0 + stride - 1) / stride) : 0;  // rows of this workgroup
 
-  chunk16 xc[F::RUNS][4];
+  // MR activation rows (x is [MR][k], contiguous): row i of x starts at
+  // element i k, i.e. chunk i k / (4 or 8) of the whole block.
+  chunk16 xc[MR][F::RUNS][4];
 #pragma unroll
-  for (int r = 0; r < F::RUNS; ++r) load_run_raw(x, xtype, (int)k, (int)F::run_off(pl, r), xc[r]);
+  for (int i = 0; i < MR; ++i)
+#pragma unroll
+    for (int r = 0; r < F::RUNS; ++r) load_run_raw(x, xtype, MR * (int)k, i * (int)k + (int)F::run_off(pl, r), xc[i][r]);
   __builtin_amdgcn_sched_barrier(0);
   typename F::Piece sl[D];
   const int64_t first = r0 < n ? r0 : n - 1;
@@ -453,40 +457,52 @@ __global__ __launch_bounds__(1024) void k_gemv_team(const uint8_t *__restrict__ 
     sl[j] = F::load(w, aux, r < n ? r : first, k, pl);
   }
   __builtin_amdgcn_sched_barrier(0);
-  float xv[F::RUNS][16];
-  float sx[F::RUNS];
+  float xv[MR][F::RUNS][16];
+  float sx[MR][F::RUNS];
 #pragma unroll
-  for (int r = 0; r < F::RUNS; ++r) {
-    convert_run(xtype, xc[r], xv[r]);
-    sx[r] = 0.0f;
+  for (int i = 0; i < MR; ++i)
 #pragma unroll
-    for (int t = 0; t < 16; ++t) sx[r] += xv[r][t];
-  }
+    for (int r = 0; r < F::RUNS; ++r) {
+      convert_run(xtype, xc[i][r], xv[i][r]);
+      sx[i][r] = 0.0f;
+#pragma unroll
+      for (int t = 0; t < 16; ++t) sx[i][r] += xv[i][r][t];
+    }
 
-  auto emit = [&](int j, int i) {  // slot j holds row r0 + i * stride
-    const float d = F::dot(sl[j], xv, sx);
-    float acc = (live && i < rows) ? d : 0.0f;
-    acc = seg_sum(acc, 64);
-    if (lane == 63 && i < rows) red[i][tm] = acc;
+  auto emit = [&](int j, int ir) {  // slot j holds row r0 + ir * stride
+    float dr[MR];
+    if constexpr (MR > 1 && has_dot_rows<F>::value) {
+      F::template dot_rows<MR>(sl[j], xv, sx, dr);
+    } else {
+#pragma unroll
+      for (int i = 0; i < MR; ++i) dr[i] = F::dot(sl[j], xv[i], sx[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+      float acc = (live && ir < rows) ? dr[i] : 0.0f;
+      acc = seg_sum(acc, 64);
+      if (lane == 63 && ir < rows) red[i][ir][tm] = acc;
+    }
   };
   const int groups = (rows + D - 1) / D;
   int base = 0;
   for (int g = 1; g < groups; ++g, base += D) {
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-      const int i = base + j;
-      emit(j, i);
-      const int64_t r = r0 + (int64_t)i * stride, rn = r + D * stride;
+      const int ir = base + j;
+      emit(j, ir);
+      const int64_t r = r0 + (int64_t)ir * stride, rn = r + D * stride;
       sl[j] = F::load(w, aux, rn < n ? rn : r, k, pl);
     }
   }
 #pragma unroll
   for (int j = 0; j < D; ++j) emit(j, base + j);
   __syncthreads();
-  for (int i = (int)threadIdx.x; i < rows; i += (int)blockDim.x) {
-    float tot = red[i][0];
-    for (int t = 1; t < team; ++t) tot += red[i][t];
-    store_out(y, ytype, r0 + (int64_t)i * stride, tot);
+  for (int t = (int)threadIdx.x; t < MR * rows; t += (int)blockDim.x) {
+    const int i = t / rows, ir = t - i * rows;
+    float tot = red[i][ir][0];
+    for (int q = 1; q < team; ++q) tot += red[i][ir][q];
+    store_out(y, ytype, i * n + r0 + (int64_t)ir * stride, tot);
   }
 }
 
@@ -612,6 +628,8 @@ int run_long(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, 
 
 template <class F, int MR>
 int run_seg(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s);
+template <class F, int MR>
+int run_team(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s);
 
 template <class F>
 int run_m1(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s) {
@@ -625,21 +643,26 @@ int run_m1(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hi
       default: break;
     }
   }
-  // Other long rows: a team of waves per row, each workgroup walking up to
-  // kTeamRows rows; about 512 workgroups (measured best of 128-2048 on
-  // 896 x 4864, 2048 x 8192 and 4096 x 14336).
-  if (P > 64) {
-    const int team = (P + 63) / 64;
-    if (team > kTeamMax) return RQ_E_UNSUPPORTED;
-    int64_t per = (wt->n + 511) / 512;
-    if (per > kTeamRows) per = kTeamRows;
-    const int64_t grid = (wt->n + per - 1) / per;
-    if (grid > 0x7FFFFFFF) return RQ_E_UNSUPPORTED;
-    hipLaunchKernelGGL((k_gemv_team<F, 2>), dim3((unsigned)grid), dim3(64 * team), 0, s, wt->data,
-                       wt->data + wt->aux_off, x, xtype, y, ytype, wt->n, wt->k);
-    return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
-  }
+  // Other long rows: a team of waves per row.
+  if (P > 64) return run_team<F, 1>(wt, x, xtype, y, ytype, s);
   return run_seg<F, 1>(wt, x, xtype, y, ytype, s);
+}
+
+// Rows of more than 64 pieces, MR activation rows: a team of waves per row,
+// each workgroup walking up to kTeamRows rows; about 512 workgroups
+// (measured best of 128-2048 on 896 x 4864, 2048 x 8192 and 4096 x 14336).
+template <class F, int MR>
+int run_team(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s) {
+  const int P = (int)(wt->k / F::PE);
+  const int team = (P + 63) / 64;
+  if (team > kTeamMax) return RQ_E_UNSUPPORTED;
+  int64_t per = (wt->n + 511) / 512;
+  if (per > kTeamRows) per = kTeamRows;
+  const int64_t grid = (wt->n + per - 1) / per;
+  if (grid > 0x7FFFFFFF) return RQ_E_UNSUPPORTED;
+  hipLaunchKernelGGL((k_gemv_team<F, 2, MR>), dim3((unsigned)grid), dim3(64 * team), 0, s, wt->data,
+                     wt->data + wt->aux_off, x, xtype, y, ytype, wt->n, wt->k);
+  return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }
 
 // Rows of at most 64 pieces, MR activation rows: the segment kernel.
@@ -679,6 +702,12 @@ int dispatch_fmt(const rq_weight *wt, const void *x, int xtype, int64_t m, void 
   // Two activation rows on the segment kernel: each weight decoded once,
   // one FMA per weight and row.
   if (m == 2 && P <= 64 && wt->k % 8 == 0) return run_seg<F, 2>(wt, x, xtype, y, ytype, s);
+  // (Q6_K's four runs a piece leave no registers for a second row in a
+  // sixteen-wave team.)
+  if constexpr (F::RUNS == 2) {
+    if (m == 2 && P > 64 && wt->n < 4096 && (P + 63) / 64 <= kTeamMax && wt->k % 8 == 0)
+      return run_team<F, 2>(wt, x, xtype, y, ytype, s);
+  }
   if (P <= 32) return run_multi<F, 1>(wt, x, xtype, m, y, ytype, ceil_log2(P), s);
   const int ppl = (P + 63) / 64;
   if (ppl > MAXPPL) return RQ_E_UNSUPPORTED;
@@ -700,10 +729,14 @@ int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m
   // bf16 activations with m > 1 run on the matrix cores: up to 64 rows with
   // the weights as the A operand decoded straight into registers, beyond
   // that the LDS-tiled GEMM.
-  // Two rows of rows with at most 64 pieces stay on the VALU segment kernel
-  // (a weight decoded once, one FMA per weight and row; exact f32 weights).
+  // Two rows stay on the VALU GEMVs (segment and team layouts; n < 4096 for
+  // long rows): a weight decoded once, one FMA per weight and row, exact f32
+  // weights.
   const int seg_pe = wt->qtype == RQ_Q6_K ? 64 : 32;
-  const bool two_rows_seg = m == 2 && wt->k % (2 * seg_pe) == 0 && wt->k / seg_pe <= 64 &&
+  const int64_t seg_p = wt->k / seg_pe;
+  const bool two_rows_seg = m == 2 && wt->k % (2 * seg_pe) == 0 &&
+                            (seg_p <= 64 ||
+                             (wt->n < 4096 && (seg_p + 63) / 64 <= kTeamMax && wt->qtype != RQ_Q6_K)) &&
                             (wt->qtype == RQ_Q4_K || wt->qtype == RQ_Q6_K || wt->qtype == RQ_Q8_0 ||
                              wt->qtype == RQ_Q5_K || wt->qtype == RQ_Q4_0 || wt->qtype == RQ_Q5_0);
   if (m > 1 && xtype == RQ_BF16 && !two_rows_seg) {

@@ -74,11 +74,15 @@ def test_decode_gemv_activation_types(dev, xdt, qtype, n, k):
 @pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("qtype,n,k", [(rq.Q4_K, 4864, 896), (rq.Q4_K, 130, 2048), (rq.Q6_K, 896, 896),
                                        (rq.Q8_0, 128, 896), (rq.Q5_K, 300, 512), (rq.Q4_0, 64, 2048),
-                                       (rq.Q5_0, 77, 256)])
+                                       (rq.Q5_0, 77, 256),
+                                       # long rows on fewer than 4096 rows: teams of 3, 4 and 10 waves
+                                       (rq.Q4_K, 896, 4864), (rq.Q8_0, 300, 8192), (rq.Q4_0, 50, 20480)])
 def test_two_rows_exact_weights(dev, xdt, qtype, n, k):
-    # M = 2 on rows of at most 64 pieces runs the GEMV with both activation
-    # rows: exact f32 weights and f32 accumulation for every activation type,
-    # and each row's result equal, bit for bit, to the M = 1 result of that row
+    # M = 2 runs the GEMVs with both activation rows (segment layout for rows
+    # of at most 64 pieces, team layout for longer rows on n < 4096; Q6_K's
+    # long rows excepted): exact f32 weights and f32 accumulation for every
+    # activation type, and each row's result equal, bit for bit, to the
+    # M = 1 result of that row
     print(f"two rows x={xdt} qtype={qtype} n={n} k={k}", flush=True)
     w, wf = make(qtype, n, k, 40 + n + k)
     x = torch.from_numpy(synth.activations(9, 2, k)).to(xdt).to(dev)
