@@ -143,7 +143,7 @@ __device__ __forceinline__ void store_x_chunks_rows(int xtype, int k, int mr, in
     const int c0 = (int)threadIdx.x + i * (int)blockDim.x;
     const int c = c0 < nc ? c0 : nc - 1;
     int e = c * epc, row = 0;
-    while (e >= k) {  // mr <= 2: at most one step
+    while (e >= k) {  // mr <= 4: at most three steps
       e -= k;
       ++row;
     }
@@ -205,7 +205,8 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const uint8_t *__restrict__ w,
                                                 const uint8_t *__restrict__ aux,
                                                 const void *__restrict__ x, int xtype,
                                                 void *__restrict__ y, int ytype, int64_t n,
-                                                int64_t k, int seg_log2, int rows_per_wg, int64_t groups) {
+                                                int64_t k, int seg_log2, int rows_per_wg, int64_t groups,
+                                                int mrows) {
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int P = (int)(k / F::PE);
   const int row_in_wg = wv * (64 >> seg_log2) + (lane >> seg_log2);
@@ -223,12 +224,14 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const uint8_t *__restrict__ w,
   // i of the LDS copy starts at i * xstride.
   const int xstride = (int)(xlds_bytes(k) / sizeof(float));
   chunk16 xc[XR];
-  load_x_chunks<XR>(x, xtype, MR * (int)k, xc);
+  // mrows <= MR rows of x exist; loads clamp to them, and rows mrows .. MR - 1
+  // of the LDS copy are neither written nor their results stored.
+  load_x_chunks<XR>(x, xtype, mrows * (int)k, xc);
   __builtin_amdgcn_sched_barrier(0);
   typename F::Piece cur = F::load(w, aux, row < n ? row : n - 1, k, pl);
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (MR == 1) store_x_chunks<XR>(xtype, (int)k, xc, xs_dyn);
-  else store_x_chunks_rows<XR>(xtype, (int)k, MR, xstride, xc, xs_dyn);
+  else store_x_chunks_rows<XR>(xtype, (int)k, mrows, xstride, xc, xs_dyn);
   float xv[MR][F::RUNS][16];
   float sx[MR][F::RUNS];
 #pragma unroll
@@ -261,7 +264,7 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const uint8_t *__restrict__ w,
       float acc = (live && r < n) ? d : 0.0f;
       const int seg = 1 << seg_log2;
       acc = seg_sum(acc, seg);
-      if ((lane & (seg - 1)) == seg - 1 && r < n) store_out(y, ytype, i * n + r, acc);
+      if ((lane & (seg - 1)) == seg - 1 && r < n && i < mrows) store_out(y, ytype, i * n + r, acc);
     }
   };
   // One row group per workgroup (every decode-sized matrix): no prefetch.
@@ -627,7 +630,7 @@ int run_long(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, 
 }
 
 template <class F, int MR>
-int run_seg(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s);
+int run_seg(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s, int mrows = MR);
 template <class F, int MR>
 int run_team(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s);
 
@@ -667,7 +670,7 @@ int run_team(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, 
 
 // Rows of at most 64 pieces, MR activation rows: the segment kernel.
 template <class F, int MR>
-int run_seg(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s) {
+int run_seg(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s, int mrows) {
   const int P = (int)(wt->k / F::PE);
   const int seg_log2 = ceil_log2(P < 16 ? 16 : P);
   const int rows_per_wg = 4 * (64 >> seg_log2);
@@ -676,17 +679,20 @@ int run_seg(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, h
   // k <= 64 pieces always fits the LDS copy of x (x is 16-byte aligned here);
   // chunks of x per thread: at most MR 64 PE / 4 / 256 = 4 MR.
   const size_t xb = MR * xlds_bytes(wt->k);
-  const int per = (x_chunks(MR * wt->k, xtype) + 255) / 256;
+  const int per = (x_chunks(mrows * wt->k, xtype) + 255) / 256;
 #define RQ_M1(XR)                                                                                               \
   hipLaunchKernelGGL((k_gemv_m1<F, XR, MR>), dim3(blocks), dim3(256), xb, s, wt->data, wt->data + wt->aux_off, \
-                     x, xtype, y, ytype, wt->n, wt->k, seg_log2, rows_per_wg, groups)
+                     x, xtype, y, ytype, wt->n, wt->k, seg_log2, rows_per_wg, groups, mrows)
   if (per <= 1) {
     RQ_M1(1);
   } else if (per <= 2) {
     RQ_M1(2);
   } else if constexpr (MR == 1) {
     RQ_M1(4);
-  } else {
+  } else if constexpr (MR == 2) {
+    if (per <= 4) RQ_M1(4);
+    else RQ_M1(8);
+  } else {  // four rows of two-run formats: k <= 2048, at most 8 chunks a thread
     if (per <= 4) RQ_M1(4);
     else RQ_M1(8);
   }
@@ -702,6 +708,11 @@ int dispatch_fmt(const rq_weight *wt, const void *x, int xtype, int64_t m, void 
   // Two activation rows on the segment kernel: each weight decoded once,
   // one FMA per weight and row.
   if (m == 2 && P <= 64 && wt->k % 8 == 0) return run_seg<F, 2>(wt, x, xtype, y, ytype, s);
+  // Three f32 / f16 rows: four row slots (two-run formats; Q6_K's four runs
+  // a piece would not fit four rows of activations in registers).
+  if constexpr (F::RUNS == 2) {
+    if ((m == 3 || m == 4) && P <= 64 && wt->k % 8 == 0) return run_seg<F, 4>(wt, x, xtype, y, ytype, s, (int)m);
+  }
   // (Q6_K's four runs a piece leave no registers for a second row in a
   // sixteen-wave team.)
   if constexpr (F::RUNS == 2) {
@@ -728,10 +739,11 @@ int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
   // bf16 activations with m > 1 run on the matrix cores: up to 64 rows with
   // the weights as the A operand decoded straight into registers, beyond
-  // that the LDS-tiled GEMM.
-  // Two rows stay on the VALU GEMVs (segment and team layouts; n < 4096 for
-  // long rows): a weight decoded once, one FMA per weight and row, exact f32
-  // weights.
+  // that the LDS-tiled GEMM -- except two rows (segment and team layouts;
+  // n < 4096 for long rows), which stay on the VALU GEMVs: a weight decoded
+  // once, one FMA per weight and row, exact f32 weights.  (Three and four
+  // bf16 rows on the VALU were slower than the matrix cores: 259 -> 201 GB/s
+  // on the 0.5B verify layer at m = 3.)
   const int seg_pe = wt->qtype == RQ_Q6_K ? 64 : 32;
   const int64_t seg_p = wt->k / seg_pe;
   const bool two_rows_seg = m == 2 && wt->k % (2 * seg_pe) == 0 &&
@@ -746,7 +758,7 @@ int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m
   }
   // f32 / f16 activations with 4 <= m <= 64: exact-f32 weights on the f32
   // matrix cores (16 MFMAs of K = 4 per 64-element chunk; at m = 2..3 the
-  // VALU kernel's few FMAs per weight are cheaper: 37 vs 47 us per 0.5B
+  // VALU kernels' few FMAs per weight are cheaper: 37 vs 47 us per 0.5B
   // layer at m = 2, 150 vs 54 us at m = 16).
   if (m >= 4 && m <= 64 && (xtype == RQ_F32 || xtype == RQ_F16)) {
     const int rc = launch_linear_smallm_f32(wt, x, xtype, m, y, ytype, s);

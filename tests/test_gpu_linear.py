@@ -77,18 +77,23 @@ def test_decode_gemv_activation_types(dev, xdt, qtype, n, k):
                                        (rq.Q5_0, 77, 256),
                                        # long rows on fewer than 4096 rows: teams of 3, 4 and 10 waves
                                        (rq.Q4_K, 896, 4864), (rq.Q8_0, 300, 8192), (rq.Q4_0, 50, 20480)])
-def test_two_rows_exact_weights(dev, xdt, qtype, n, k):
+@pytest.mark.parametrize("m", [2, 3])
+def test_few_rows_exact_weights(dev, xdt, qtype, n, k, m):
     # M = 2 runs the GEMVs with both activation rows (segment layout for rows
     # of at most 64 pieces, team layout for longer rows on n < 4096; Q6_K's
-    # long rows excepted): exact f32 weights and f32 accumulation for every
-    # activation type, and each row's result equal, bit for bit, to the
-    # M = 1 result of that row
-    print(f"two rows x={xdt} qtype={qtype} n={n} k={k}", flush=True)
+    # long rows excepted) for every activation type, M = 3 with f32 / f16
+    # activations the segment layout with four row slots (rows of at most 64
+    # pieces, Q6_K excepted): exact f32 weights and f32 accumulation, and
+    # each row's result equal, bit for bit, to the M = 1 result of that row
+    pieces = k // (64 if qtype == rq.Q6_K else 32)
+    if m == 3 and (xdt == torch.bfloat16 or qtype == rq.Q6_K or pieces > 64):
+        pytest.skip("three rows of this shape and type run on other kernels")
+    print(f"few rows m={m} x={xdt} qtype={qtype} n={n} k={k}", flush=True)
     w, wf = make(qtype, n, k, 40 + n + k)
-    x = torch.from_numpy(synth.activations(9, 2, k)).to(xdt).to(dev)
+    x = torch.from_numpy(synth.activations(9 + m, m, k)).to(xdt).to(dev)
     y = w.forward(x, out_dtype=torch.float32)
     assert norm_err(y.cpu().numpy(), ref(x.float().cpu().numpy(), wf)) <= TOL_F32
-    for i in range(2):
+    for i in range(m):
         y1 = w.forward(x[i:i + 1].contiguous(), out_dtype=torch.float32)
         assert torch.equal(y[i:i + 1], y1)
 
