@@ -259,7 +259,16 @@ __global__ __launch_bounds__(256) void k_qgemm_pipe(const uint8_t *__restrict__ 
   uint8_t *const SB[4] = {S0, S1, S2, S3};
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int64_t m0 = (int64_t)blockIdx.y * 256, n0 = (int64_t)blockIdx.x * 256;
+  // Tile order: workgroup b runs on XCD b % 8 (workgroups are dealt to the
+  // eight XCDs in turn, each with its own L2).  XCD x takes the x-th eighth
+  // of the tiles in M-fastest order, so the M tiles that share a weight tile
+  // run back to back on one XCD and read it from that XCD's L2 after the
+  // first (without the remap they ran half a launch apart on different
+  // XCDs).  Grids whose tile count is not a multiple of 8 keep b.
+  const int64_t gm = gridDim.y, tiles = (int64_t)gridDim.x * gridDim.y;
+  const int64_t b = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+  const int64_t lin = tiles % 8 == 0 ? (b % 8) * (tiles / 8) + b / 8 : b;
+  const int64_t m0 = (lin % gm) * 256, n0 = (lin / gm) * 256;
   const int64_t nk = k / 32;
   const int last = (int)nk - 1;
 

@@ -263,6 +263,7 @@ def test_mfma_gemm_edge_tiles(dev, qtype, m, n, k):
     (rq.Q8_0, 257, 33000, 128),
     (rq.Q4_K, 512, 32768, 64),
     (rq.Q6_K, 512, 32768, 448),
+    (rq.Q6_K, 768, 32768, 256),  # pipelined kernel, three M tiles per weight tile in the XCD-aware order
 ])
 def test_large_gemm(dev, qtype, m, n, k):
     w, wf = make(qtype, n, k, 5 + m + k)
