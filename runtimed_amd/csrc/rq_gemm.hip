@@ -439,11 +439,12 @@ int by_m(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipS
   if (big_tiles >= 256 && wt->k % 128 == 0) return launch_pipe<F>(wt, x, m, y, ytype, s);
   if (big_tiles >= 256) return launch<F, 256, 256, 2, 4, 1>(wt, x, m, y, ytype, s);
   // Fewer than 128 tiles of 128 x 128 (2048-wide layers at M = 512): short K
-  // takes 64 x 128 tiles; long K keeps 128 x 128 and splits K four ways (at
-  // most, 32 K-steps per split).  Measured on the 2048 / 8192 prefill
-  // shapes: q/k/o 36 -> 26 us, down 67 -> 53 us.
+  // takes 64 x 64 tiles of two waves (256 workgroups); long K keeps 128 x 128
+  // and splits K four ways (at most, 32 K-steps per split).  Measured on the
+  // 2048 / 8192 prefill shapes: q/k/o 36 -> 26 us (64 x 128) -> 25.3 us
+  // (64 x 64), v Q6_K 28.2 -> 27.2 us, down 67 -> 53 us.
   const int64_t tiles128 = ((m + 127) / 128) * ((wt->n + 127) / 128), nk = wt->k / BK;
-  if (tiles128 < 128 && nk <= 32) return launch<F, 64, 128, 2, 2>(wt, x, m, y, ytype, s);
+  if (tiles128 < 128 && nk <= 32) return launch<F, 64, 64, 2, 1>(wt, x, m, y, ytype, s);
   if (tiles128 < 128 && nk >= 64) {
     const int sp = (int)(nk / 32 < 4 ? nk / 32 : 4);
     return launch<F, 128, 128, 2, 2>(wt, x, m, y, ytype, s, sp);
