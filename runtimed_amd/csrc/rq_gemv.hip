@@ -12,12 +12,17 @@
 //   Q6_K  ql[l..l+16), ql[l+32..l+48), qh[l..l+16) of one 128-element half =
 //         64 elements in four runs of 16, each with its own int8 scale.
 //   Q8_0  the 32 quants of one block, one f16 scale.
-// A row of k inputs is P = k / piece_elems pieces.  The pieces of one row sit
-// on an aligned segment of SEG = next_pow2(P) lanes (P <= 32: 64/SEG rows per
-// wave step), or, when P > 32, on all 64 lanes with PPL = ceil(P/64) pieces
-// per lane.  A lane's pieces keep the same k positions from row to row, so in
-// the M=1 kernels its activations are loaded once into registers and every
-// later step only streams weight bytes.  Rows are cut from the flat block
+// A row of k inputs is P = k / piece_elems pieces.  Three layouts:
+//   segment  P <= 64: a row on an aligned segment of max(16, next_pow2(P))
+//            lanes, 64 / segment rows per wave (k_gemv_m1);
+//   team     P > 64 on n < 4096 (or more than 256 pieces): a row on a team of
+//            ceil(P / 64) waves, one piece per lane (k_gemv_team);
+//   long     P in 65..256 on n >= 4096: a row on one wave, PPL = ceil(P / 64)
+//            pieces per lane (k_gemv_long).
+// A lane's pieces keep the same k positions from row to row, so its
+// activations (one row, or two / four row slots for M = 2 / 3) are loaded
+// once into registers and every later row only streams weight bytes.  Rows
+// are cut from the flat block
 // stream, so a Q4_K block that straddles two rows (k = 896: 3.5 blocks per
 // row) is read by lanes of both rows, each using the header of the block its
 // own piece lies in.
