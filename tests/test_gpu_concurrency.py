@@ -30,6 +30,11 @@ def test_concurrent_streams_match_serial(dev):
         (_weight(rq.Q6_K, 2048, 8192, 3), torch.randn((300, 8192), generator=g).to(torch.bfloat16)),
         # pipelined 256 x 256 GEMM
         (_weight(rq.Q4_K, 32768, 256, 4), torch.randn((512, 256), generator=g).to(torch.bfloat16)),
+        # two activation rows on the segment GEMV and on the team GEMV (bf16)
+        (_weight(rq.Q4_K, 4864, 896, 5), torch.randn((2, 896), generator=g).to(torch.bfloat16)),
+        (_weight(rq.Q4_K, 896, 4864, 6), torch.randn((2, 4864), generator=g).to(torch.bfloat16)),
+        # three f32 rows on the segment GEMV's four row slots
+        (_weight(rq.Q8_0, 896, 896, 7), torch.randn((3, 896), generator=g)),
     ]
     cases = [(w, x.to(dev)) for w, x in cases]
     serial = [w.forward(x) for w, x in cases]
