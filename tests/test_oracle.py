@@ -102,6 +102,106 @@ def test_q6_k_signed_values_and_scales():  # dequant_k.rs:155-177
     assert oracle.dequant_block("q6_k", lane)[16] == -62.0
 
 
+# ------------------------------------------- hand-derived KATs ----------
+#
+# The reference's own Q4_K KAT (dequant_k.rs:118-129) has dmin = 0 and
+# qs = 0x11, so it fixes neither the min term nor which nibble feeds which
+# sub-block.  The vectors below were worked out by hand from the block
+# layouts (dequant_k.rs:8-80, dequant.rs:50-77) and are written as literal
+# numbers, one per 32-element sub-block, so that a dropped or sign-flipped
+# min, swapped nibbles, a wrong scale_min_k4 branch or a shifted qh mask
+# fails.
+#
+# Scale bytes: for j < 4 sc_j = s[j] & 63, m_j = s[j + 4] & 63; for j >= 4
+# sc_j = (s[j + 4] & 0xF) | (s[j - 4] >> 6) << 4, m_j = (s[j + 4] >> 4) |
+# (s[j] >> 6) << 4.  With
+#   s = 41 82 C3 04 | 41 82 C3 04 | 51 62 73 88
+# sc = [1, 2, 3, 4, 17, 34, 51, 8] and m = [1, 2, 3, 4, 21, 38, 55, 8]:
+# sc_4 = 0x1 | (0x41 >> 6) << 4 = 17, m_4 = 0x5 | (0x41 >> 6) << 4 = 21, ...
+SCALES_BOTH = bytes([0x41, 0x82, 0xC3, 0x04, 0x41, 0x82, 0xC3, 0x04, 0x51, 0x62, 0x73, 0x88])
+SCALES_MINS_ONLY = bytes([0, 0, 0, 0, 0x41, 0x82, 0xC3, 0x04, 0x50, 0x60, 0x70, 0x80])   # sc = 0
+SCALES_SC_ONLY = bytes([0x41, 0x82, 0xC3, 0x04, 0, 0, 0, 0, 0x01, 0x02, 0x03, 0x08])      # m = 0
+F16_ZERO, F16_QUARTER, F16_HALF, F16_ONE = b"\x00\x00", b"\x00\x34", b"\x00\x38", b"\x00\x3c"
+
+
+def _per_sub_block(values, width=32):
+    return np.repeat(np.array(values, dtype=np.float32), width)
+
+
+def test_q4_k_min_term_hand_derived():
+    # d = 0, dmin = 1: every element is -m_j of its sub-block, whatever qs is
+    block = F16_ZERO + F16_ONE + SCALES_MINS_ONLY + bytes((7 * i + 3) & 0xFF for i in range(128))
+    out = oracle.dequant_block("q4_k", block)
+    assert np.array_equal(out, _per_sub_block([-1, -2, -3, -4, -21, -38, -55, -8]))
+
+
+def test_q4_k_nibble_order_hand_derived():
+    # d = 1, dmin = 0, every qs byte 0x21: sub-block 2c takes the low nibbles
+    # (q = 1) of chunk c, sub-block 2c + 1 the high nibbles (q = 2)
+    block = F16_ONE + F16_ZERO + SCALES_SC_ONLY + bytes([0x21] * 128)
+    out = oracle.dequant_block("q4_k", block)
+    assert np.array_equal(out, _per_sub_block([1, 4, 3, 8, 17, 68, 51, 16]))
+
+
+def test_q4_k_scale_and_min_together_hand_derived():
+    # d = 0.5, dmin = 0.25, qs = 0x21: y = 0.5 sc_j q - 0.25 m_j
+    block = F16_HALF + F16_QUARTER + SCALES_BOTH + bytes([0x21] * 128)
+    out = oracle.dequant_block("q4_k", block)
+    assert np.array_equal(out, _per_sub_block([0.25, 1.5, 0.75, 3.0, 3.25, 24.5, 11.75, 6.0]))
+    # one chunk whose low and high nibbles differ per byte: chunk 1 (sub-blocks
+    # 2 and 3) holds bytes 0xF0 then 0x0F alternately
+    qs = bytearray([0x21] * 128)
+    qs[32:64] = bytes([0xF0, 0x0F] * 16)
+    out = oracle.dequant_block("q4_k", F16_HALF + F16_QUARTER + SCALES_BOTH + bytes(qs))
+    # sub-block 2 (low nibbles, sc 3, m 3): q = 0 -> -0.75, q = 15 -> 21.75
+    assert np.array_equal(out[64:96], np.array([-0.75, 21.75] * 16, np.float32))
+    # sub-block 3 (high nibbles, sc 4, m 4): q = 15 -> 29.0, q = 0 -> -1.0
+    assert np.array_equal(out[96:128], np.array([29.0, -1.0] * 16, np.float32))
+
+
+def test_q5_k_min_term_and_high_bits_hand_derived():
+    # d = dmin = 1, qs = 0x21, qh[l] = 1 << (l % 8): sub-block j = 2c + h uses
+    # qh bit 2c + h, so exactly the elements l = j, j + 8, j + 16, j + 24 of
+    # sub-block j get +16.  Per sub-block: (value without, value with the bit)
+    qh = bytes(1 << (l % 8) for l in range(32))
+    block = F16_ONE + F16_ONE + SCALES_BOTH + qh + bytes([0x21] * 128)
+    out = oracle.dequant_block("q5_k", block)
+    pairs = [(0, 16), (2, 34), (0, 48), (4, 68), (-4, 268), (30, 574), (-4, 812), (8, 136)]
+    want = np.empty(256, np.float32)
+    for j, (plain, high) in enumerate(pairs):
+        want[32 * j:32 * j + 32] = plain
+        want[32 * j + j:32 * j + 32:8] = high
+    assert np.array_equal(out, want)
+    # with dmin = 0 the min term vanishes: sc_j (q + hi) alone
+    out0 = oracle.dequant_block("q5_k", F16_ONE + F16_ZERO + SCALES_BOTH + qh + bytes([0x21] * 128))
+    assert out0[0] == 17.0 and out0[1] == 1.0 and out0[32] == 4.0 and out0[32 + 1] == 36.0 and out0[128 + 4] == 289.0
+
+
+def test_q4_0_nibble_order_hand_derived():
+    # d = 1; byte i = i | (15 - i) << 4: element i = i - 8, element 16 + i = 7 - i
+    block = F16_ONE + bytes(i | ((15 - i) << 4) for i in range(16))
+    out = oracle.dequant_block("q4_0", block)
+    want = [-8, -7, -6, -5, -4, -3, -2, -1, 0, 1, 2, 3, 4, 5, 6, 7,
+            7, 6, 5, 4, 3, 2, 1, 0, -1, -2, -3, -4, -5, -6, -7, -8]
+    assert np.array_equal(out, np.array(want, np.float32))
+    # d = 0.5 halves every value; bytes 0x0F / 0xF0 give 7 / -8 and -8 / 7
+    out = oracle.dequant_block("q4_0", F16_HALF + bytes([0x0F, 0xF0] * 8))
+    assert np.array_equal(out, np.array([3.5, -4.0] * 8 + [-4.0, 3.5] * 8, np.float32))
+
+
+def test_q5_0_single_high_bits_hand_derived():
+    # d = 1; qh bits 3 and 20 set (little-endian u32 0x00100008): element 3
+    # (low nibble of byte 3) and element 20 (high nibble of byte 4) get +16
+    block = F16_ONE + bytes([0x08, 0x00, 0x10, 0x00]) + bytes(i | ((15 - i) << 4) for i in range(16))
+    out = oracle.dequant_block("q5_0", block)
+    want = [-16, -15, -14, 3, -12, -11, -10, -9, -8, -7, -6, -5, -4, -3, -2, -1,
+            -1, -2, -3, -4, 11, -6, -7, -8, -9, -10, -11, -12, -13, -14, -15, -16]
+    assert np.array_equal(out, np.array(want, np.float32))
+    # every qh bit set: q - 16 + 16 = the nibble itself
+    out = oracle.dequant_block("q5_0", F16_ONE + b"\xff\xff\xff\xff" + bytes([0x0F, 0xF0] * 8))
+    assert np.array_equal(out, np.array([15.0, 0.0] * 8 + [0.0, 15.0] * 8, np.float32))
+
+
 # ------------------------------------- independent restatements ----------
 
 @pytest.mark.parametrize("qtype", [8, 2, 6, 12, 13, 14])
