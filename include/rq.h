@@ -26,7 +26,18 @@
  *       GGUF bytes already in device memory, same error rules.
  *   rq_linear
  *       `QMatMul::forward` as called by `Weights::linear`
- *       (crates/runtimed-model/src/weights/linear_layer.rs:45-52).
+ *       (crates/runtimed-model/src/weights/linear_layer.rs:45-52), with the
+ *       last-dimension check of linear_layer.rs:88-96 (ModelError::Shape).
+ *   rq_linear_bias
+ *       `Weights::linear_bias` (linear_layer.rs:107-118) on a quantized
+ *       weight: the linear and the bias's broadcast add in one launch.
+ *   rq_linear_multi
+ *       consecutive `Weights::linear` / `linear_bias` calls on one input, as
+ *       the q/k/v and gate/up projections of qwen2.rs:99-125 and
+ *       gemma4.rs:118-156 make them: one launch where the shapes allow.
+ *   rq_bias_add
+ *       the `broadcast_add` of linear_bias (linear_layer.rs:111-115) for an
+ *       output that another path produced (FP8, Marlin).
  *   rq_fp8_quantize, rq_fp8_gemm
  *       `SubstratePort::fp8_gemm` (crates/runtimed-model/src/substrate/port.rs:73)
  *       -> `ops::fp8_gemm` (crates/runtimed-model/src/ops/fp8_gemm.rs:77-191),
@@ -73,7 +84,7 @@
 extern "C" {
 #endif
 
-#define RQ_ABI_VERSION 1
+#define RQ_ABI_VERSION 2
 
 /* Block formats, numbered as GgmlDtype (crates/runtimed-gguf/src/quant/dtype.rs:6-24). */
 typedef enum rq_qtype {
@@ -162,7 +173,9 @@ int rq_dequant_f32(const rq_weight *w, float *dev_out, void *stream);
  * of Weights::embed / Weights::candidate_weights (embed_layer.rs:16-84,
  * QMatMul::embedding).  ids are in host memory and may be reused when the
  * call returns; an id >= n gives RQ_E_ARG and nothing is written; n_ids == 0
- * is a no-op.  Requires k % 4 == 0 (RQ_E_UNSUPPORTED otherwise). */
+ * is a no-op.  Requires k % 4 == 0 (RQ_E_UNSUPPORTED otherwise).  Not for
+ * stream capture (a captured copy would read the caller's host buffer when
+ * the graph runs): a capturing stream gives RQ_E_ARG. */
 int rq_embedding(const rq_weight *w, const uint32_t *ids, int64_t n_ids, float *dev_out, void *stream);
 
 /* Decode a flat GGUF block stream that already sits in device memory, with
@@ -174,9 +187,41 @@ int rq_dequant_tensor(int qtype, const void *dev_bytes, size_t nbytes, size_t n_
 
 /* y[m, n] = sum_k x[m, k] * W[n, k] for an m x k activation (row-major, type
  * xtype in {F32, F16, BF16}) into y (row-major m x n, type ytype in {F32, F16,
- * BF16}).  Accumulation is in f32.  m = 0 is a no-op. */
-int rq_linear(const rq_weight *w, const void *x, int xtype, int64_t m, void *y, int ytype,
+ * BF16}).  Accumulation is in f32.  k is the activation's last dimension: a
+ * k that differs from the weight's gives RQ_E_SHAPE and launches nothing
+ * (linear_layer.rs:88-96).  m = 0 is a no-op.  x may have any alignment (an
+ * x that is not 16-byte aligned is first copied, m*k elements, into the
+ * stream's workspace).  Scratch comes from a per-(device, stream) workspace
+ * that the library keeps between calls: a graph captured from a stream
+ * refers to that stream's workspace, so it must not run concurrently with
+ * other librq calls on the stream it was captured from. */
+int rq_linear(const rq_weight *w, const void *x, int xtype, int64_t m, int64_t k, void *y, int ytype,
               void *stream);
+
+/* rq_linear plus a bias of n values (type btype in {F32, F16, BF16}, device
+ * memory) added to every row, as linear_bias does (the bias cast to y's
+ * type, then added).  The add happens in the kernels' epilogues: y =
+ * acc + (bias as ytype), rounded once to ytype.  For F32 outputs that is the
+ * reference's sum exactly; for BF16 / F16 outputs it may differ by one unit
+ * in the last place from linear_bias's two roundings (rq_linear followed by
+ * rq_bias_add reproduces those).  A null bias is rq_linear. */
+int rq_linear_bias(const rq_weight *w, const void *x, int xtype, int64_t m, int64_t k, const void *bias, int btype,
+                   void *y, int ytype, void *stream);
+
+/* count linears on one activation x [m, k]: ys[i][m, n_i] = x W_i^T
+ * (+ biases[i] when biases and biases[i] are not null, all of type btype).
+ * Every weight lives on one device and has k inputs (RQ_E_SHAPE
+ * otherwise).  At m = 1 and 2, runs of up to 8 consecutive weights of one
+ * format whose rows hold at most 64 pieces (k <= 2048 for Q4_K / Q5_K /
+ * Q8_0 / Q4_0 / Q5_0, k <= 4096 for Q6_K) take one launch; other weights
+ * take the launches rq_linear_bias would make.  Each output equals that
+ * call's output bit for bit (the same kernels compute every row). */
+int rq_linear_multi(int count, const rq_weight *const *ws, const void *x, int xtype, int64_t m, int64_t k,
+                    const void *const *biases, int btype, void *const *ys, int ytype, void *stream);
+
+/* y[m, n] += bias[n] in y's type (type ytype, device memory, row-major):
+ * the bias cast to ytype, the sum rounded to ytype (linear_layer.rs:111-115). */
+int rq_bias_add(void *y, int ytype, int64_t m, int64_t n, const void *bias, int btype, void *stream);
 
 /* Encode an m x k activation (F32, F16 or BF16) to e4m3 codes xq (m*k bytes)
  * and per-row scales xscale (m floats) according to `mode` (RQ_FP8_UNSCALED
@@ -188,7 +233,7 @@ int rq_fp8_quantize(const void *x, int xtype, int64_t m, int64_t k, int mode, ui
  * CDNA4 fp8 matrix cores with f32 accumulation.  w is n x k e4m3 codes,
  * w_scale has n floats (or NULL for all ones, linear_layer.rs:82-85).  If
  * xtype is RQ_F8E4M3, x holds codes used as they are (sx = 1); otherwise x is
- * encoded first according to `mode`, in stream-ordered scratch memory.
+ * encoded first according to `mode`, into the stream's workspace.
  * ytype is F32, F16 or BF16. */
 int rq_fp8_gemm(const void *x, int xtype, int64_t m, const uint8_t *w, const float *w_scale,
                 int64_t n, int64_t k, void *y, int ytype, int mode, void *stream);
@@ -228,8 +273,8 @@ int rq_marlin_linear(const uint32_t *packed, const float *scales, int64_t n, int
  * max(max|t[:, h, :]| / (448 | 127), 1e-8) (NaN elements ignored) and
  * q (b*h*sd bytes) = f32_to_fp8_e4m3(t / s) or (i8)clamp(round(t / s),
  * -128, 127) (NaN -> 0).  RQ_KV_F16: q holds b*h*sd f16 (t cast, round to
- * nearest even) and every scale is 1.  Scratch for the per-head maxima is
- * stream-ordered. */
+ * nearest even) and every scale is 1.  The per-head partial maxima live in
+ * the stream's workspace. */
 int rq_kv_quantize(const void *t, int ttype, int64_t b, int64_t h, int64_t sd, int mode, void *q,
                    float *scales, void *stream);
 

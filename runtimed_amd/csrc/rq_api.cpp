@@ -219,16 +219,19 @@ int rq_embedding(const rq_weight *w, const uint32_t *ids, int64_t n_ids, float *
   int rc = hip_check(hipSetDevice(w->device), "hipSetDevice");
   if (rc) return rc;
   const hipStream_t s = as_stream(stream);
-  uint32_t *dids = nullptr;
-  rc = hip_check(hipMallocAsync(reinterpret_cast<void **>(&dids), (size_t)n_ids * sizeof(uint32_t), s),
-                 "hipMallocAsync");
-  if (rc) return rc;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return set_error(RQ_E_ARG, "rq_embedding reads host ids and cannot be captured into a graph");
+  }
+  WsLease ws(w->device, s);
+  uint32_t *dids = static_cast<uint32_t *>(ws.get((size_t)n_ids * sizeof(uint32_t), &rc));
+  if (!dids) return rc;
   // From pageable memory the copy returns once the ids are staged, so the
   // caller's buffer may be reused on return.
   rc = hip_check(hipMemcpyAsync(dids, ids, (size_t)n_ids * sizeof(uint32_t), hipMemcpyHostToDevice, s),
                  "hipMemcpyAsync");
   if (!rc) rc = launch_gather_rows(w, dids, n_ids, dev_out, s);
-  (void)hipFreeAsync(dids, s);
   return rc;
 }
 
@@ -244,30 +247,108 @@ int rq_dequant_tensor(int qtype, const void *dev_bytes, size_t nbytes, size_t n_
                             n_elements / (uint64_t)g.elems, dev_out, as_stream(stream));
 }
 
-int rq_linear(const rq_weight *w, const void *x, int xtype, int64_t m, void *y, int ytype,
-              void *stream) {
-  g_last_error.clear();
+static size_t ftype_bytes(int t) { return t == RQ_F32 ? 4 : 2; }
+
+// Argument checks shared by the linear entry points (linear_layer.rs:88-96
+// for the width rule).
+static int linear_checks(const rq_weight *w, int xtype, int64_t m, int64_t k, const void *bias, int btype,
+                         int ytype) {
   if (!w) return set_error(RQ_E_ARG, "weight is null");
   if (!valid_ftype(xtype)) return set_error(RQ_E_ARG, "activation type %d not supported", xtype);
   if (!valid_ftype(ytype)) return set_error(RQ_E_ARG, "output type %d not supported", ytype);
+  if (bias && !valid_ftype(btype)) return set_error(RQ_E_ARG, "bias type %d not supported", btype);
+  if (k != w->k)
+    return set_error(RQ_E_SHAPE, "linear: expected last dim %lld, got %lld", (long long)w->k, (long long)k);
   if (m < 0) return set_error(RQ_E_SHAPE, "negative row count %lld", (long long)m);
+  return RQ_OK;
+}
+
+// x as the fused kernels read it: 16-byte aligned, else an aligned copy of
+// its m * k elements in the workspace.
+static const void *aligned_x(const void *x, int xtype, int64_t m, int64_t k, hipStream_t s, WsLease &ws, int *rc) {
+  if (reinterpret_cast<uintptr_t>(x) % 16 == 0) return x;
+  const size_t bytes = (size_t)m * (size_t)k * ftype_bytes(xtype);
+  void *p = ws.get(bytes, rc);
+  if (!p) return nullptr;
+  *rc = hip_check(hipMemcpyAsync(p, x, bytes, hipMemcpyDeviceToDevice, s), "hipMemcpyAsync");
+  return *rc ? nullptr : p;
+}
+
+// One weight: the fused kernels, or the generic one for shapes they do not take.
+static int linear_one(const rq_weight *w, const void *xa, int xtype, int64_t m, const Out &o, hipStream_t s,
+                      WsLease &ws) {
+  int rc = launch_linear_fused(w, xa, xtype, m, o, s, ws);
+  if (rc == RQ_E_UNSUPPORTED) rc = launch_linear_generic(w, xa, xtype, m, o, s);
+  return rc;
+}
+
+int rq_linear_bias(const rq_weight *w, const void *x, int xtype, int64_t m, int64_t k, const void *bias, int btype,
+                   void *y, int ytype, void *stream) {
+  g_last_error.clear();
+  int rc = linear_checks(w, xtype, m, k, bias, btype, ytype);
+  if (rc) return rc;
   if (m == 0) return RQ_OK;
   if (!x || !y) return set_error(RQ_E_ARG, "null activation or output");
-  int rc = hip_check(hipSetDevice(w->device), "hipSetDevice");
+  rc = hip_check(hipSetDevice(w->device), "hipSetDevice");
   if (rc) return rc;
-  hipStream_t s = as_stream(stream);
-  rc = launch_linear_fused(w, x, xtype, m, y, ytype, s);
-  if (rc != RQ_E_UNSUPPORTED) return rc;
-  // No fused kernel for this format or shape: decode to f32 in stream-ordered
-  // scratch, then multiply.
-  float *tmp = nullptr;
-  const uint64_t bytes = (uint64_t)w->n * (uint64_t)w->k * sizeof(float);
-  rc = hip_check(hipMallocAsync(reinterpret_cast<void **>(&tmp), bytes, s), "hipMallocAsync");
+  const hipStream_t s = as_stream(stream);
+  WsLease ws(w->device, s);
+  const void *xa = aligned_x(x, xtype, m, k, s, ws, &rc);
+  if (!xa) return rc;
+  return linear_one(w, xa, xtype, m, Out{y, bias, ytype, btype}, s, ws);
+}
+
+int rq_linear(const rq_weight *w, const void *x, int xtype, int64_t m, int64_t k, void *y, int ytype,
+              void *stream) {
+  return rq_linear_bias(w, x, xtype, m, k, nullptr, RQ_F32, y, ytype, stream);
+}
+
+int rq_linear_multi(int count, const rq_weight *const *wts, const void *x, int xtype, int64_t m, int64_t k,
+                    const void *const *biases, int btype, void *const *ys, int ytype, void *stream) {
+  g_last_error.clear();
+  if (count < 0) return set_error(RQ_E_ARG, "negative count %d", count);
+  if (count == 0) return RQ_OK;
+  if (!wts || !ys) return set_error(RQ_E_ARG, "null weight or output array");
+  for (int i = 0; i < count; ++i) {
+    const void *b = biases ? biases[i] : nullptr;
+    const int rc = linear_checks(wts[i], xtype, m, k, b, btype, ytype);
+    if (rc) return rc;
+    if (wts[i]->device != wts[0]->device) return set_error(RQ_E_ARG, "weights on different devices");
+    if (m > 0 && !ys[i]) return set_error(RQ_E_ARG, "null output %d", i);
+  }
+  if (m == 0) return RQ_OK;
+  if (!x) return set_error(RQ_E_ARG, "null activation");
+  int rc = hip_check(hipSetDevice(wts[0]->device), "hipSetDevice");
   if (rc) return rc;
-  rc = launch_dequant_weight(w, tmp, s);
-  if (!rc) rc = launch_linear_dense_f32(tmp, w->n, w->k, x, xtype, m, y, ytype, s);
-  const int rc2 = hip_check(hipFreeAsync(tmp, s), "hipFreeAsync");
-  return rc ? rc : rc2;
+  const hipStream_t s = as_stream(stream);
+  WsLease ws(wts[0]->device, s);
+  const void *xa = aligned_x(x, xtype, m, k, s, ws, &rc);
+  if (!xa) return rc;
+  Out outs[kMultiMax];
+  for (int i = 0; i < count;) {
+    // A run of consecutive weights of one format (at most kMultiMax).
+    int j = i + 1;
+    while (j < count && j - i < kMultiMax && wts[j]->qtype == wts[i]->qtype) ++j;
+    for (int t = i; t < j; ++t) outs[t - i] = Out{ys[t], biases ? biases[t] : nullptr, ytype, btype};
+    rc = j - i > 1 ? launch_linear_multi(wts + i, j - i, xa, xtype, m, outs, s) : RQ_E_UNSUPPORTED;
+    if (rc == RQ_E_UNSUPPORTED) {
+      rc = RQ_OK;
+      for (int t = i; t < j && !rc; ++t) rc = linear_one(wts[t], xa, xtype, m, outs[t - i], s, ws);
+    }
+    if (rc) return rc;
+    i = j;
+  }
+  return RQ_OK;
+}
+
+int rq_bias_add(void *y, int ytype, int64_t m, int64_t n, const void *bias, int btype, void *stream) {
+  g_last_error.clear();
+  if (!valid_ftype(ytype)) return set_error(RQ_E_ARG, "output type %d not supported", ytype);
+  if (!valid_ftype(btype)) return set_error(RQ_E_ARG, "bias type %d not supported", btype);
+  if (m < 0 || n < 0) return set_error(RQ_E_SHAPE, "bad shape [%lld, %lld]", (long long)m, (long long)n);
+  if (m == 0 || n == 0) return RQ_OK;
+  if (!y || !bias) return set_error(RQ_E_ARG, "null argument");
+  return launch_bias_add(y, ytype, m, n, bias, btype, as_stream(stream));
 }
 
 int rq_fp8_quantize(const void *x, int xtype, int64_t m, int64_t k, int mode, uint8_t *xq,
@@ -304,16 +385,17 @@ int rq_fp8_gemm(const void *x, int xtype, int64_t m, const uint8_t *w, const flo
   if (m == 0) return RQ_OK;
   if (!x || !w || !y) return set_error(RQ_E_ARG, "null argument");
   hipStream_t s = as_stream(stream);
-  const uint64_t qbytes = ((uint64_t)m * (uint64_t)k + 255) & ~(uint64_t)255;
-  uint8_t *scratch = nullptr;
-  int rc = hip_check(hipMallocAsync(reinterpret_cast<void **>(&scratch), qbytes + (uint64_t)m * 4, s),
-                     "hipMallocAsync");
+  int dev = 0;
+  int rc = hip_check(hipGetDevice(&dev), "hipGetDevice");
   if (rc) return rc;
+  const uint64_t qbytes = ((uint64_t)m * (uint64_t)k + 255) & ~(uint64_t)255;
+  WsLease ws(dev, s);
+  uint8_t *scratch = static_cast<uint8_t *>(ws.get(qbytes + (uint64_t)m * 4, &rc));
+  if (!scratch) return rc;
   float *xs = reinterpret_cast<float *>(scratch + qbytes);
   rc = launch_fp8_quantize(x, xtype, m, k, mode, scratch, xs, s);
   if (!rc) rc = launch_fp8_gemm(scratch, xs, m, w, w_scale, n, k, y, ytype, s);
-  const int rc2 = hip_check(hipFreeAsync(scratch, s), "hipFreeAsync");
-  return rc ? rc : rc2;
+  return rc;
 }
 
 int rq_marlin_repack(const void *w, int wtype, const float *scales, int64_t n, int64_t k, uint32_t *packed,
@@ -366,7 +448,11 @@ int rq_kv_quantize(const void *t, int ttype, int64_t b, int64_t h, int64_t sd, i
     return hip_check(e, "hipMemcpyAsync");
   }
   if (!t || !q) return set_error(RQ_E_ARG, "null argument");
-  return launch_kv_quantize(t, ttype, b, h, sd, mode, q, scales, as_stream(stream));
+  int dev = 0;
+  const int rc = hip_check(hipGetDevice(&dev), "hipGetDevice");
+  if (rc) return rc;
+  WsLease ws(dev, as_stream(stream));
+  return launch_kv_quantize(t, ttype, b, h, sd, mode, q, scales, as_stream(stream), ws);
 }
 
 int rq_kv_dequantize(const void *q, int mode, const float *scales, int64_t b, int64_t h, int64_t sd, void *out,

@@ -256,6 +256,49 @@ __global__ __launch_bounds__(kThreads) void k_gather_rows(const uint8_t *__restr
   }
 }
 
+// y[m, n] = x W^T for any shape and alignment (the shapes the fused kernels
+// do not take): one wave per weight row, the lanes striding over k, each
+// weight decoded exactly from its flat quad (the element picked from the
+// four), four activation rows per pass over the row, f32 accumulation.  A
+// fallback: every weight is decoded ceil(m / 4) times.
+template <int QT>
+__global__ __launch_bounds__(kThreads) void k_linear_generic(const uint8_t *__restrict__ data,
+                                                            const uint8_t *__restrict__ aux,
+                                                            const void *__restrict__ x, int xtype, int64_t m,
+                                                            const Out o, int64_t n, int64_t k) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nw = (int64_t)gridDim.x * (kThreads / 64);
+  for (int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6); row < n; row += nw) {
+    for (int64_t m0 = 0; m0 < m; m0 += 4) {
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int64_t c = lane; c < k; c += 64) {
+        const uint64_t e = (uint64_t)row * (uint64_t)k + (uint64_t)c;
+        const float4 q = quad_handle<QT>(data, aux, e >> 2);
+        const int sub = (int)(e & 3);
+        const float wv = sub == 0 ? q.x : sub == 1 ? q.y : sub == 2 ? q.z : q.w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (m0 + i < m) acc[i] = fmaf(wv, load_as_f32(x, xtype, (m0 + i) * k + c), acc[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = acc[i];
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+        if (lane == 0 && m0 + i < m) store_linear(o, m0 + i, n, row, v);
+      }
+    }
+  }
+}
+
+// linear_bias's broadcast add (linear_layer.rs:111-115) on an output that is
+// already in y: the bias cast to y's type, the sum rounded to y's type.
+__global__ __launch_bounds__(kThreads) void k_bias_add(void *__restrict__ y, int ytype, int64_t mn, int64_t n,
+                                                      const void *__restrict__ bias, int btype) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < mn; i += stride)
+    store_out(y, ytype, i, load_as_f32(y, ytype, i) + round_as(ytype, load_as_f32(bias, btype, i % n)));
+}
+
 unsigned grid_for(uint64_t items) {
   const uint64_t want = (items + kThreads - 1) / kThreads;
   return (unsigned)(want < 65536 ? (want ? want : 1) : 65536);
@@ -311,6 +354,30 @@ int launch_gather_rows(const rq_weight *w, const uint32_t *dev_ids, int64_t n_id
   return by_qtype<GatherK>(w->qtype, dim3(grid_for((uint64_t)n_ids * (uint64_t)kq)), s, (const uint8_t *)w->data,
                            (const uint8_t *)(w->data + w->aux_off), dev_ids, n_ids, kq,
                            reinterpret_cast<float4 *>(out));
+}
+
+int launch_linear_generic(const rq_weight *w, const void *x, int xtype, int64_t m, const Out &o, hipStream_t s) {
+  int64_t blocks = (w->n + 3) / 4;
+  if (blocks > 8192) blocks = 8192;
+  const dim3 grid((unsigned)blocks), block(kThreads);
+  const uint8_t *aux = w->data + w->aux_off;
+  switch (w->qtype) {
+    case RQ_Q4_K: hipLaunchKernelGGL(k_linear_generic<RQ_Q4_K>, grid, block, 0, s, w->data, aux, x, xtype, m, o, w->n, w->k); break;
+    case RQ_Q5_K: hipLaunchKernelGGL(k_linear_generic<RQ_Q5_K>, grid, block, 0, s, w->data, aux, x, xtype, m, o, w->n, w->k); break;
+    case RQ_Q8_0: hipLaunchKernelGGL(k_linear_generic<RQ_Q8_0>, grid, block, 0, s, w->data, aux, x, xtype, m, o, w->n, w->k); break;
+    case RQ_Q6_K: hipLaunchKernelGGL(k_linear_generic<RQ_Q6_K>, grid, block, 0, s, w->data, aux, x, xtype, m, o, w->n, w->k); break;
+    case RQ_Q4_0: hipLaunchKernelGGL(k_linear_generic<RQ_Q4_0>, grid, block, 0, s, w->data, aux, x, xtype, m, o, w->n, w->k); break;
+    case RQ_Q5_0: hipLaunchKernelGGL(k_linear_generic<RQ_Q5_0>, grid, block, 0, s, w->data, aux, x, xtype, m, o, w->n, w->k); break;
+    default: return set_error(RQ_E_UNSUPPORTED, "no decoder for qtype %d", w->qtype);
+  }
+  return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "linear launch failed");
+}
+
+int launch_bias_add(void *y, int ytype, int64_t m, int64_t n, const void *bias, int btype, hipStream_t s) {
+  const uint64_t mn = (uint64_t)m * (uint64_t)n;
+  if (mn == 0) return RQ_OK;
+  hipLaunchKernelGGL(k_bias_add, dim3(grid_for(mn)), dim3(kThreads), 0, s, y, ytype, (int64_t)mn, n, bias, btype);
+  return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "bias add launch failed");
 }
 
 }  // namespace rq

@@ -100,17 +100,45 @@ __device__ __forceinline__ void tile_col_scales(const float *ws, int64_t n, int6
   }
 }
 
-// Writes the 32 x 32 tile at (row0, col0) of y[m, n] (row stride n) as
+// Biases of the same four columns, rounded to the output type (0 where there
+// is none), with one branch on the bias type for all four.
+__device__ __forceinline__ void tile_col_bias(const Out &o, int64_t n, int64_t col0, int lane, float (&bb)[4]) {
+  const int64_t c0 = col0 + (lane & 28);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) bb[j] = 0.0f;
+  if (!o.bias) return;
+  if (o.btype == RQ_F32) {
+    const float *b = static_cast<const float *>(o.bias);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bb[j] = b[c0 + j < n ? c0 + j : n - 1];
+  } else {
+    const uint16_t *b = static_cast<const uint16_t *>(o.bias);
+    const bool bf = o.btype == RQ_BF16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u = b[c0 + j < n ? c0 + j : n - 1];
+      bb[j] = bf ? __uint_as_float(u << 16) : f16_bits_to_f32(u);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) bb[j] = round_as(o.ytype, bb[j]);
+}
+
+// Writes the 32 x 32 tile at (row0, col0) of o.y[m, n] (row stride n) as
 // acc * (xs[row] * ws[col]) when SCALED (a null xs or ws counts as 1), else
-// as acc.  sx, sw: the lane's scales from tile_row_scales / tile_col_scales
-// (read only when SCALED).  vec: y is 16-byte aligned and n % 4 == 0.  Tiles
-// not wholly inside y, or not vec, take the per-element path.
+// as acc, plus the bias of its column (with_bias).  sx, sw, bb: the lane's
+// scales and rounded biases from tile_row_scales / tile_col_scales /
+// tile_col_bias (scales read only when SCALED; biases 0 when o has none, so
+// the add stays one unconditional instruction in the unrolled epilogues).  vec: y is 16-byte aligned
+// and n % 4 == 0.  Tiles not wholly inside y, or not vec, take the
+// per-element path.
 template <bool SCALED>
-__device__ __forceinline__ void store_tile32(const rq_f32x16 &acc, void *y, int ytype, int64_t m,
-                                             int64_t n, int64_t row0, int64_t col0, const float (&sx)[4],
-                                             const float (&sw)[4], const float *xs, const float *ws,
-                                             int lane, bool vec) {
+__device__ __forceinline__ void store_tile32(const rq_f32x16 &acc, const Out &o, int64_t m, int64_t n, int64_t row0,
+                                             int64_t col0, const float (&sx)[4], const float (&sw)[4],
+                                             const float (&bb)[4], const float *xs, const float *ws, int lane,
+                                             bool vec) {
   const int h = lane >> 5;
+  const int ytype = o.ytype;
   if (vec && row0 + 32 <= m && col0 + 32 <= n) {
     const int t = lane & 3;
     const int64_t col = col0 + (lane & 28);
@@ -125,18 +153,23 @@ __device__ __forceinline__ void store_tile32(const rq_f32x16 &acc, void *y, int 
         v2 *= sx[g] * sw[2];
         v3 *= sx[g] * sw[3];
       }
-      store_four(y, ytype, row * n + col, v0, v1, v2, v3);
+      v0 += bb[0];
+      v1 += bb[1];
+      v2 += bb[2];
+      v3 += bb[3];
+      store_four(o.y, ytype, row * n + col, v0, v1, v2, v3);
     });
   } else {
     const int64_t col = col0 + (lane & 31);
     const float swe = (SCALED && ws && col < n) ? ws[col] : 1.0f;
+    const float be = (o.bias && col < n) ? round_as(ytype, load_as_f32(o.bias, o.btype, col)) : 0.0f;
     static_for<16>([&](auto R) {
       constexpr int r = decltype(R)::value;
       const int64_t row = row0 + 8 * (r / 4) + 4 * h + (r % 4);
       if (row < m && col < n) {
         float v = acc[r];
         if (SCALED) v *= (xs ? xs[row] : 1.0f) * swe;
-        store_one(y, ytype, row * n + col, v);
+        store_one(o.y, ytype, row * n + col, v + be);
       }
     });
   }
@@ -154,10 +187,12 @@ __device__ __forceinline__ void store_tile32(const rq_f32x16 &acc, void *y, int 
 // instruction.
 
 // A wave's 128 x 128 block (4 x 4 MFMA tiles of 32 x 32, rows rb.., columns
-// cb.. of the staged tile) into T; values scaled by sx * sw when SCALED.
+// cb.. of the staged tile) into T; values scaled by sx * sw when SCALED,
+// plus the biases bb (rounded as tile_col_bias leaves them; 0 without one).
 template <bool SCALED>
 __device__ __forceinline__ void stage_block_2b(const rq_f32x16 (&acc)[4][4], uint8_t *T, int rb, int cb, int ytype,
-                                               const float (&sx)[4][4], const float (&sw)[4][4], int lane) {
+                                               const float (&sx)[4][4], const float (&sw)[4][4],
+                                               const float (&bb)[4][4], int lane) {
   const int h = lane >> 5, t = lane & 3;
   static_for<4>([&](auto I) {
     static_for<4>([&](auto J) {
@@ -172,6 +207,10 @@ __device__ __forceinline__ void stage_block_2b(const rq_f32x16 (&acc)[4][4], uin
           v2 *= sx[I][g] * sw[J][2];
           v3 *= sx[I][g] * sw[J][3];
         }
+        v0 += bb[J][0];
+        v1 += bb[J][1];
+        v2 += bb[J][2];
+        v3 += bb[J][3];
         const int r = rb + 32 * I + 8 * g + 4 * h + t;
         const int c = cb + 32 * J + (lane & 28);  // first of 4 columns
         const uint32_t lo = ytype == RQ_BF16 ? pack_bf16x2(v0, v1) : pack_f16x2(v0, v1);

@@ -171,10 +171,12 @@ __global__ __launch_bounds__(256) void k_fp8_gemm_mfma(const uint8_t *__restrict
   for (int i = 0; i < MI; ++i) tile_row_scales(xs, m, m0 + wm * (BM / WM) + i * 32, lane, sx[i]);
 #pragma unroll
   for (int j = 0; j < NI; ++j) tile_col_scales(ws, n, n0 + wn * (BN / WN) + j * 32, lane, sw[j]);
+  const Out o{y, nullptr, ytype, 0};
+  const float nob[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   static_for<MI>([&](auto I) {
     static_for<NI>([&](auto J) {
-      store_tile32<true>(acc[I][J], y, ytype, m, n, m0 + wm * (BM / WM) + I * 32,
-                         n0 + wn * (BN / WN) + J * 32, sx[I], sw[J], xs, ws, lane, vec);
+      store_tile32<true>(acc[I][J], o, m, n, m0 + wm * (BM / WM) + I * 32, n0 + wn * (BN / WN) + J * 32, sx[I],
+                         sw[J], nob, xs, ws, lane, vec);
     });
   });
 }
@@ -306,15 +308,18 @@ __global__ __launch_bounds__(256) void k_fp8_gemm_pipe(const uint8_t *__restrict
   for (int j = 0; j < 4; ++j) tile_col_scales(ws, n, n0 + 128 * wn + j * 32, lane, sw[j]);
   if (ytype != RQ_F32 && vec && n % 8 == 0 && m0 + 256 <= m && n0 + 256 <= n) {
     __syncthreads();  // every wave's stage reads are done
-    stage_block_2b<true>(acc, SM, 128 * wm, 128 * wn, ytype, sx, sw, lane);
+    const float nob[4][4] = {};
+    stage_block_2b<true>(acc, SM, 128 * wm, 128 * wn, ytype, sx, sw, nob, lane);
     __syncthreads();
     store_staged_2b(SM, y, n, m0, n0, threadIdx.x);
     return;
   }
+  const Out o{y, nullptr, ytype, 0};
+  const float nob[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   static_for<4>([&](auto I) {
     static_for<4>([&](auto J) {
-      store_tile32<true>(acc[I][J], y, ytype, m, n, m0 + 128 * wm + I * 32, n0 + 128 * wn + J * 32,
-                         sx[I], sw[J], xs, ws, lane, vec);
+      store_tile32<true>(acc[I][J], o, m, n, m0 + 128 * wm + I * 32, n0 + 128 * wn + J * 32, sx[I], sw[J], nob, xs,
+                         ws, lane, vec);
     });
   });
 }

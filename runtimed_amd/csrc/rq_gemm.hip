@@ -47,8 +47,8 @@ template <class F, int BM, int BN, int WM, int WN, int D>
 __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restrict__ w,
                                                        const uint8_t *__restrict__ aux,
                                                        const uint16_t *__restrict__ x, int64_t m,
-                                                       int64_t n, int64_t k, void *__restrict__ y,
-                                                       int ytype, int64_t steps, float *__restrict__ part) {
+                                                       int64_t n, int64_t k, const Out o, int64_t steps,
+                                                       float *__restrict__ part) {
   constexpr int NT = 64 * WM * WN;
   static_assert(BN * 2 == NT, "one weight piece per thread");
   constexpr int MI = BM / WM / 32, NI = BN / WN / 32;
@@ -150,14 +150,17 @@ __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restric
     });
   }
 
-  void *out = part ? static_cast<void *>(part + (int64_t)blockIdx.z * m * n) : y;
-  const int otype = part ? (int)RQ_F32 : ytype;
-  const bool vec = vec_stores_ok(out, n);
+  // Split K: f32 partials without the bias (k_splitk_sum adds it).
+  const Out out = part ? Out{part + (int64_t)blockIdx.z * m * n, nullptr, RQ_F32, 0} : o;
+  const bool vec = vec_stores_ok(out.y, n);
   const float one[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  float bb[NI][4];  // loaded before the first store
+#pragma unroll
+  for (int j = 0; j < NI; ++j) tile_col_bias(out, n, n0 + wn * (BN / WN) + j * 32, lane, bb[j]);
   static_for<MI>([&](auto I) {
     static_for<NI>([&](auto J) {
-      store_tile32<false>(acc[I][J], out, otype, m, n, m0 + wm * (BM / WM) + I * 32,
-                          n0 + wn * (BN / WN) + J * 32, one, one, nullptr, nullptr, lane, vec);
+      store_tile32<false>(acc[I][J], out, m, n, m0 + wm * (BM / WM) + I * 32, n0 + wn * (BN / WN) + J * 32, one,
+                          one, bb[J], nullptr, nullptr, lane, vec);
     });
   });
 }
@@ -252,7 +255,7 @@ __device__ __forceinline__ void wait_lds_all() { asm volatile("s_waitcnt lgkmcnt
 template <class F>
 __global__ __launch_bounds__(256) void k_qgemm_pipe(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
                                                     const uint16_t *__restrict__ x, int64_t m, int64_t n,
-                                                    int64_t k, void *__restrict__ y, int ytype) {
+                                                    int64_t k, const Out o) {
   // four stages, one array: after the loop it holds the staged output tile
   __shared__ __attribute__((aligned(1024))) uint8_t SM[4 * P_STAGE];
   uint8_t *const S0 = SM, *const S1 = SM + P_STAGE, *const S2 = SM + 2 * P_STAGE, *const S3 = SM + 3 * P_STAGE;
@@ -358,31 +361,36 @@ __global__ __launch_bounds__(256) void k_qgemm_pipe(const uint8_t *__restrict__ 
     step(t + 3, std::integral_constant<int, 3>{});
   }
 
-  const bool vec = vec_stores_ok(y, n);
-  if (ytype != RQ_F32 && vec && n % 8 == 0 && m0 + 256 <= m && n0 + 256 <= n) {
+  const bool vec = vec_stores_ok(o.y, n);
+  float bb[4][4];  // biases, loaded before the first store
+#pragma unroll
+  for (int j = 0; j < 4; ++j) tile_col_bias(o, n, n0 + 128 * wn + j * 32, lane, bb[j]);
+  if (o.ytype != RQ_F32 && vec && n % 8 == 0 && m0 + 256 <= m && n0 + 256 <= n) {
     __syncthreads();  // every wave's stage reads are done
     const float ones[4][4] = {};
-    stage_block_2b<false>(acc, SM, 128 * wm, 128 * wn, ytype, ones, ones, lane);
+    stage_block_2b<false>(acc, SM, 128 * wm, 128 * wn, o.ytype, ones, ones, bb, lane);
     __syncthreads();
-    store_staged_2b(SM, y, n, m0, n0, tid);
+    store_staged_2b(SM, o.y, n, m0, n0, tid);
     return;
   }
   const float one[4] = {1.0f, 1.0f, 1.0f, 1.0f};
   static_for<4>([&](auto I) {
     static_for<4>([&](auto J) {
-      store_tile32<false>(acc[I][J], y, ytype, m, n, m0 + 128 * wm + I * 32, n0 + 128 * wn + J * 32, one, one,
+      store_tile32<false>(acc[I][J], o, m, n, m0 + 128 * wm + I * 32, n0 + 128 * wn + J * 32, one, one, bb[J],
                           nullptr, nullptr, lane, vec);
     });
   });
 }
 
-// y = sum over s < splits of part[s] (f32 partials of m * n outputs).
+// y = sum over s < splits of part[s] (f32 partials of m * n outputs), with
+// o's bias.
 __global__ __launch_bounds__(256) void k_splitk_sum(const float *__restrict__ part, int splits, int64_t mn,
-                                                    void *__restrict__ y, int ytype) {
+                                                    int64_t n, const Out o) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < mn; i += (int64_t)gridDim.x * 256) {
     float v = part[i];
     for (int s = 1; s < splits; ++s) v += part[s * mn + i];
-    store_one(y, ytype, i, v);
+    if (o.bias) v = with_bias(v, load_as_f32(o.bias, o.btype, i % n), o.ytype);
+    store_one(o.y, o.ytype, i, v);
   }
 }
 
@@ -396,7 +404,8 @@ int splits_for(int64_t tiles, int64_t nk) {
 }
 
 template <class F, int BM, int BN, int WM, int WN, int D = 3>
-int launch(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s, int sp_force = 0) {
+int launch(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease &ws,
+           int sp_force = 0) {
   const int64_t nk = wt->k / BK;
   const int64_t gx = (wt->n + BN - 1) / BN, gy = (m + BM - 1) / BM;
   const int sp = sp_force > 0 ? sp_force : splits_for(gx * gy, nk);
@@ -404,67 +413,63 @@ int launch(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hi
   const int used = (int)((nk + steps - 1) / steps);  // splits that own at least one step
   float *part = nullptr;
   if (used > 1) {
-    if (hipMallocAsync(reinterpret_cast<void **>(&part), (size_t)used * m * wt->n * sizeof(float), s) !=
-        hipSuccess)
-      return set_error(RQ_E_NOMEM, "split-K workspace of %d x %lld x %lld f32", used, (long long)m,
-                       (long long)wt->n);
+    int rc = RQ_OK;
+    part = static_cast<float *>(ws.get((size_t)used * m * wt->n * sizeof(float), &rc));
+    if (!part) return rc;
   }
   const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)used);
   hipLaunchKernelGGL((k_qgemm<F, BM, BN, WM, WN, D>), grid, dim3(64 * WM * WN), 0, s, wt->data,
-                     wt->data + wt->aux_off, static_cast<const uint16_t *>(x), m, wt->n, wt->k, y,
-                     ytype, steps, part);
+                     wt->data + wt->aux_off, static_cast<const uint16_t *>(x), m, wt->n, wt->k, o, steps, part);
   if (part) {
     const int64_t mn = m * wt->n;
     const int64_t blocks = (mn + 255) / 256 < 4096 ? (mn + 255) / 256 : 4096;
-    hipLaunchKernelGGL(k_splitk_sum, dim3((unsigned)blocks), dim3(256), 0, s, part, used, mn, y, ytype);
-    (void)hipFreeAsync(part, s);
+    hipLaunchKernelGGL(k_splitk_sum, dim3((unsigned)blocks), dim3(256), 0, s, part, used, mn, wt->n, o);
   }
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemm launch failed");
 }
 
 template <class F>
-int launch_pipe(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {
+int launch_pipe(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s) {
   const dim3 grid((unsigned)((wt->n + 255) / 256), (unsigned)((m + 255) / 256));
   hipLaunchKernelGGL((k_qgemm_pipe<F>), grid, dim3(256), 0, s, wt->data, wt->data + wt->aux_off,
-                     static_cast<const uint16_t *>(x), m, wt->n, wt->k, y, ytype);
+                     static_cast<const uint16_t *>(x), m, wt->n, wt->k, o);
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemm launch failed");
 }
 
 template <class F>
-int by_m(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {
-  if (m <= 64) return launch<F, 64, 128, 2, 2>(wt, x, m, y, ytype, s);
+int by_m(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease &ws) {
+  if (m <= 64) return launch<F, 64, 128, 2, 2>(wt, x, m, o, s, ws);
   // 256 x 256 tiles when they still give every CU a workgroup (pipelined
   // when K is a multiple of 128), else 128 x 128.
   const int64_t big_tiles = ((m + 255) / 256) * ((wt->n + 255) / 256);
-  if (big_tiles >= 256 && wt->k % 128 == 0) return launch_pipe<F>(wt, x, m, y, ytype, s);
-  if (big_tiles >= 256) return launch<F, 256, 256, 2, 4, 1>(wt, x, m, y, ytype, s);
+  if (big_tiles >= 256 && wt->k % 128 == 0) return launch_pipe<F>(wt, x, m, o, s);
+  if (big_tiles >= 256) return launch<F, 256, 256, 2, 4, 1>(wt, x, m, o, s, ws);
   // Fewer than 128 tiles of 128 x 128 (2048-wide layers at M = 512): short K
   // takes 64 x 64 tiles of two waves (256 workgroups); long K keeps 128 x 128
   // and splits K four ways (at most, 32 K-steps per split).  Measured on the
   // 2048 / 8192 prefill shapes: q/k/o 36 -> 26 us (64 x 128) -> 25.3 us
   // (64 x 64), v Q6_K 28.2 -> 27.2 us, down 67 -> 53 us.
   const int64_t tiles128 = ((m + 127) / 128) * ((wt->n + 127) / 128), nk = wt->k / BK;
-  if (tiles128 < 128 && nk <= 32) return launch<F, 64, 64, 2, 1>(wt, x, m, y, ytype, s);
+  if (tiles128 < 128 && nk <= 32) return launch<F, 64, 64, 2, 1>(wt, x, m, o, s, ws);
   if (tiles128 < 128 && nk >= 64) {
     const int sp = (int)(nk / 32 < 4 ? nk / 32 : 4);
-    return launch<F, 128, 128, 2, 2>(wt, x, m, y, ytype, s, sp);
+    return launch<F, 128, 128, 2, 2>(wt, x, m, o, s, ws, sp);
   }
-  return launch<F, 128, 128, 2, 2>(wt, x, m, y, ytype, s);
+  return launch<F, 128, 128, 2, 2>(wt, x, m, o, s, ws);
 }
 
 }  // namespace
 
 // bf16 activations, m > 1, k % 64 == 0, 16-byte aligned x.
-int launch_linear_mfma(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype,
-                       hipStream_t s) {
+int launch_linear_mfma(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease &ws) {
   if (wt->k % 64 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
   switch (wt->qtype) {
-    case RQ_Q4_K: return by_m<FmtQ4K>(wt, x, m, y, ytype, s);
-    case RQ_Q6_K: return by_m<FmtQ6KG>(wt, x, m, y, ytype, s);
-    case RQ_Q8_0: return by_m<FmtQ8>(wt, x, m, y, ytype, s);
-    case RQ_Q5_K: return by_m<FmtQ5K>(wt, x, m, y, ytype, s);
-    case RQ_Q4_0: return by_m<FmtQx0<false>>(wt, x, m, y, ytype, s);
-    case RQ_Q5_0: return by_m<FmtQx0<true>>(wt, x, m, y, ytype, s);
+    case RQ_Q4_K: return by_m<FmtQ4K>(wt, x, m, o, s, ws);
+    case RQ_Q6_K: return by_m<FmtQ6KG>(wt, x, m, o, s, ws);
+    case RQ_Q8_0: return by_m<FmtQ8>(wt, x, m, o, s, ws);
+    case RQ_Q5_K: return by_m<FmtQ5K>(wt, x, m, o, s, ws);
+    case RQ_Q4_0: return by_m<FmtQx0<false>>(wt, x, m, o, s, ws);
+    case RQ_Q5_0: return by_m<FmtQx0<true>>(wt, x, m, o, s, ws);
     default: return RQ_E_UNSUPPORTED;
   }
 }

@@ -197,6 +197,18 @@ __device__ __forceinline__ void load_piece_x(const void *x, int xtype, const flo
   else load_run<16>(x, xtype, F::run_off(p, r), dst);
 }
 
+// Weights that share one activation block x and one format, in one launch
+// of the segment kernel: entry j covers the row groups [g_end[j - 1],
+// g_end[j]) of the grid (g_end[-1] = 0), its own rows, output and bias.
+struct SegSet {
+  const uint8_t *w[kMultiMax];
+  const uint8_t *aux[kMultiMax];
+  Out o[kMultiMax];
+  int64_t n[kMultiMax];
+  int64_t g_end[kMultiMax];
+  int count;
+};
+
 // M = MR (1 or 2), rows of at most 64 pieces: every lane owns one piece
 // position; its activations (MR rows) are loaded once into registers, and a
 // piece's weights are converted once for the MR dot products.  A row sits on an aligned
@@ -205,13 +217,21 @@ __device__ __forceinline__ void load_piece_x(const void *x, int xtype, const flo
 // and the first row's weight loads right behind them, so x is staged in LDS
 // while the weights are still in flight.  A workgroup walking several row
 // groups issues the next group's loads before it computes the current one.
-template <class F, int XR, int MR>
-__global__ __launch_bounds__(256) void k_gemv_m1(const uint8_t *__restrict__ w,
-                                                const uint8_t *__restrict__ aux,
-                                                const void *__restrict__ x, int xtype,
-                                                void *__restrict__ y, int ytype, int64_t n,
-                                                int64_t k, int seg_log2, int rows_per_wg, int64_t groups,
-                                                int mrows) {
+// MULTI: the grid covers the row groups of every weight of `set` (one group
+// per workgroup); otherwise entry 0 alone, with set.g_end[0] groups.
+template <class F, int XR, int MR, bool MULTI>
+__global__ __launch_bounds__(256) void k_gemv_m1(const SegSet set, const void *__restrict__ x, int xtype,
+                                                int64_t k, int seg_log2, int rows_per_wg, int mrows) {
+  int j = 0;
+  int64_t g0 = 0;
+  if constexpr (MULTI) {
+    while (j + 1 < set.count && (int64_t)blockIdx.x >= set.g_end[j]) ++j;
+    g0 = j ? set.g_end[j - 1] : 0;
+  }
+  const uint8_t *__restrict__ w = set.w[j];
+  const uint8_t *__restrict__ aux = set.aux[j];
+  const Out o = set.o[j];
+  const int64_t n = set.n[j], groups = set.g_end[j] - g0;
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int P = (int)(k / F::PE);
   const int row_in_wg = wv * (64 >> seg_log2) + (lane >> seg_log2);
@@ -222,8 +242,12 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const uint8_t *__restrict__ w,
   // (the prefetched row too) before the next use.  Dead lanes and rows past
   // n contribute nothing (the dot product is selected away).
   const int pl = live ? p : P - 1;
-  int64_t g = blockIdx.x;
+  int64_t g = (int64_t)blockIdx.x - g0;
   int64_t row = g * rows_per_wg + row_in_wg;
+  // The bias of this lane's row, loaded ahead of x and the weights (a
+  // uniform branch; every later wait for x covers it).
+  float bv = 0.0f;
+  if (o.bias) bv = load_as_f32(o.bias, o.btype, row < n ? row : n - 1);
   extern __shared__ __attribute__((aligned(16))) float xs_dyn[];
   // MR activation rows (x is [MR][k], contiguous) as one run of chunks; row
   // i of the LDS copy starts at i * xstride.
@@ -255,7 +279,7 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const uint8_t *__restrict__ w,
     }
 
   // Dot products, segment totals and stores of one row group.
-  auto emit = [&](const typename F::Piece &pc, int64_t r) {
+  auto emit = [&](const typename F::Piece &pc, int64_t r, float b) {
     float dr[MR];
     if constexpr (MR > 1 && has_dot_rows<F>::value) {
       F::template dot_rows<MR>(pc, xv, sx, dr);
@@ -269,23 +293,25 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const uint8_t *__restrict__ w,
       float acc = (live && r < n) ? d : 0.0f;
       const int seg = 1 << seg_log2;
       acc = seg_sum(acc, seg);
-      if ((lane & (seg - 1)) == seg - 1 && r < n && i < mrows) store_out(y, ytype, i * n + r, acc);
+      if (o.bias) acc = with_bias(acc, b, o.ytype);
+      if ((lane & (seg - 1)) == seg - 1 && r < n && i < mrows) store_out(o.y, o.ytype, i * n + r, acc);
     }
   };
   // One row group per workgroup (every decode-sized matrix): no prefetch.
   // A next-row load in the last pass is never used, and the wave still has
   // to wait for it before it can end.
-  if (groups <= (int64_t)gridDim.x) {
-    emit(cur, row);
+  if (MULTI || groups <= (int64_t)gridDim.x) {
+    emit(cur, row, bv);
     return;
   }
   for (; g < groups; g += gridDim.x) {
     const int64_t gn = g + gridDim.x;
     const int64_t row_n = gn * rows_per_wg + row_in_wg;
     const typename F::Piece nxt = F::load(w, aux, (gn < groups && row_n < n) ? row_n : (row < n ? row : n - 1), k, pl);
-    emit(cur, row);
+    emit(cur, row, bv);
     cur = nxt;
     row = row_n;
+    if (o.bias) bv = load_as_f32(o.bias, o.btype, row < n ? row : n - 1);
   }
 }
 
@@ -310,8 +336,7 @@ constexpr int long_xr() {
 template <class F, int PPL, int WPG, int D>
 __global__ __launch_bounds__(64 * WPG) void k_gemv_long(const uint8_t *__restrict__ w,
                                                         const uint8_t *__restrict__ aux, const void *__restrict__ x,
-                                                        int xtype, void *__restrict__ y, int ytype, int64_t n,
-                                                        int64_t k, bool xlds) {
+                                                        int xtype, const Out o, int64_t n, int64_t k, bool xlds) {
   constexpr int XR = long_xr<F, PPL, WPG>();
   const int lane = threadIdx.x & 63;
   const int P = (int)(k / F::PE);
@@ -371,7 +396,7 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv_long(const uint8_t *__restric
       acc += lane + 64 * i < P ? d : 0.0f;
     }
     acc = seg_sum(acc, 64);
-    if (lane == 63 && r < n) store_out(y, ytype, r, acc);
+    if (lane == 63 && r < n) store_linear(o, 0, n, r, acc);
   };
   // Groups of D rows: every group but the last refills its slots.
   const int64_t rows = row0 < n ? (n - row0 + nw - 1) / nw : 0;  // rows of this wave
@@ -437,8 +462,8 @@ constexpr int kTeamMax = 16;
 
 template <class F, int D, int MR>
 __global__ __launch_bounds__(1024) void k_gemv_team(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
-                                                   const void *__restrict__ x, int xtype, void *__restrict__ y,
-                                                   int ytype, int64_t n, int64_t k) {
+                                                   const void *__restrict__ x, int xtype, const Out o, int64_t n,
+                                                   int64_t k) {
   __shared__ float red[MR][kTeamRows][kTeamMax];
   const int lane = threadIdx.x & 63, tm = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int team = (int)(blockDim.x >> 6);
@@ -510,7 +535,7 @@ __global__ __launch_bounds__(1024) void k_gemv_team(const uint8_t *__restrict__ 
     const int i = t / rows, ir = t - i * rows;
     float tot = red[i][ir][0];
     for (int q = 1; q < team; ++q) tot += red[i][ir][q];
-    store_out(y, ytype, i * n + r0 + (int64_t)ir * stride, tot);
+    store_linear(o, i, n, r0 + (int64_t)ir * stride, tot);
   }
 }
 
@@ -520,8 +545,8 @@ template <class F, int PPL>
 __global__ __launch_bounds__(kThreads) void k_gemv_multi(const uint8_t *__restrict__ w,
                                                         const uint8_t *__restrict__ aux,
                                                         const void *__restrict__ x, int xtype,
-                                                        int64_t m, void *__restrict__ y, int ytype,
-                                                        int64_t n, int64_t k, int seg_log2) {
+                                                        int64_t m, const Out o, int64_t n, int64_t k,
+                                                        int seg_log2) {
   const int lane = threadIdx.x & 63;
   const int seg = lane >> seg_log2, sl = lane & ((1 << seg_log2) - 1);
   const int rg = 64 >> seg_log2;
@@ -559,32 +584,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_multi(const uint8_t *__restri
         }
       }
       for (int off = 32 >> (6 - seg_log2); off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-      if (sl == 0 && row < n) store_out(y, ytype, mi * n + row, acc);
-    }
-  }
-}
-
-// Dense f32 weights (the decode-then-multiply path for shapes without a fused
-// kernel): one wave per output row, lanes stride over k.
-__global__ __launch_bounds__(kThreads) void k_dense_f32(const float *__restrict__ w, int64_t n,
-                                                       int64_t k, const void *__restrict__ x,
-                                                       int xtype, int64_t m, void *__restrict__ y,
-                                                       int ytype) {
-  const int lane = threadIdx.x & 63;
-  const int64_t nw = (int64_t)gridDim.x * (kThreads / 64);
-  for (int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6); row < n; row += nw) {
-    const float *wr = w + row * k;
-    for (int64_t mi = 0; mi < m; ++mi) {
-      float acc = 0.0f;
-      for (int64_t t = lane; t < k; t += 64) {
-        float xv;
-        if (xtype == RQ_F32) xv = static_cast<const float *>(x)[mi * k + t];
-        else if (xtype == RQ_BF16) xv = bf16_bits_to_f32(static_cast<const uint16_t *>(x)[mi * k + t]);
-        else xv = (float)static_cast<const _Float16 *>(x)[mi * k + t];
-        acc = fmaf(wr[t], xv, acc);
-      }
-      for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-      if (lane == 0) store_out(y, ytype, mi * n + row, acc);
+      if (sl == 0 && row < n) store_linear(o, mi, n, row, acc);
     }
   }
 }
@@ -596,20 +596,19 @@ int ceil_log2(int v) {
 }
 
 template <class F, int PPL>
-int run_multi(const rq_weight *wt, const void *x, int xtype, int64_t m, void *y, int ytype,
-              int seg_log2, hipStream_t s) {
+int run_multi(const rq_weight *wt, const void *x, int xtype, int64_t m, const Out &o, int seg_log2, hipStream_t s) {
   const int rg = 64 >> seg_log2;
   const int64_t groups = (wt->n + rg - 1) / rg;
   const int64_t waves_per_block = kThreads / 64;
   int64_t blocks = (groups + waves_per_block - 1) / waves_per_block;
   if (blocks > 8192) blocks = 8192;
   hipLaunchKernelGGL((k_gemv_multi<F, PPL>), dim3((unsigned)blocks), dim3(kThreads), 0, s, wt->data,
-                     wt->data + wt->aux_off, x, xtype, m, y, ytype, wt->n, wt->k, seg_log2);
+                     wt->data + wt->aux_off, x, xtype, m, o, wt->n, wt->k, seg_log2);
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }
 
 template <class F, int PPL>
-int run_long(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s) {
+int run_long(const rq_weight *wt, const void *x, int xtype, const Out &o, hipStream_t s) {
   // 16 waves per CU walking rows, each with two rows of weight loads in
   // flight (measured best of 8 / 16 / 24 / 32 waves per CU).
   const int64_t waves = wt->n < 256 * 16 ? wt->n : 256 * 16;
@@ -624,43 +623,21 @@ int run_long(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, 
     // 11.9 (three rows) and 13.4 (four), whose registers leave room for one
     // eight-wave workgroup per CU instead of two.
     hipLaunchKernelGGL((k_gemv_long<F, PPL, 8, 2>), dim3(blocks), dim3(512), xb, s, wt->data, wt->data + wt->aux_off,
-                       x, xtype, y, ytype, wt->n, wt->k, xb != 0);
+                       x, xtype, o, wt->n, wt->k, xb != 0);
   } else {
     const unsigned blocks = (unsigned)((waves + 3) / 4);
     if (long_xr<F, PPL, 4>() > 0 && !xb) return RQ_E_UNSUPPORTED;
     hipLaunchKernelGGL((k_gemv_long<F, PPL, 4, 2>), dim3(blocks), dim3(256), xb, s, wt->data, wt->data + wt->aux_off,
-                       x, xtype, y, ytype, wt->n, wt->k, xb != 0);
+                       x, xtype, o, wt->n, wt->k, xb != 0);
   }
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
-}
-
-template <class F, int MR>
-int run_seg(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s, int mrows = MR);
-template <class F, int MR>
-int run_team(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s);
-
-template <class F>
-int run_m1(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s) {
-  const int P = (int)(wt->k / F::PE);
-  // Long rows on many rows: one wave per row walking the rows.
-  if (P > 64 && wt->n >= 4096) {
-    switch ((P + 63) / 64) {
-      case 2: return run_long<F, 2>(wt, x, xtype, y, ytype, s);
-      case 3: return run_long<F, 3>(wt, x, xtype, y, ytype, s);
-      case 4: return run_long<F, 4>(wt, x, xtype, y, ytype, s);
-      default: break;
-    }
-  }
-  // Other long rows: a team of waves per row.
-  if (P > 64) return run_team<F, 1>(wt, x, xtype, y, ytype, s);
-  return run_seg<F, 1>(wt, x, xtype, y, ytype, s);
 }
 
 // Rows of more than 64 pieces, MR activation rows: a team of waves per row,
 // each workgroup walking up to kTeamRows rows; about 512 workgroups
 // (measured best of 128-2048 on 896 x 4864, 2048 x 8192 and 4096 x 14336).
 template <class F, int MR>
-int run_team(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s) {
+int run_team(const rq_weight *wt, const void *x, int xtype, const Out &o, hipStream_t s) {
   const int P = (int)(wt->k / F::PE);
   const int team = (P + 63) / 64;
   if (team > kTeamMax) return RQ_E_UNSUPPORTED;
@@ -669,77 +646,138 @@ int run_team(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, 
   const int64_t grid = (wt->n + per - 1) / per;
   if (grid > 0x7FFFFFFF) return RQ_E_UNSUPPORTED;
   hipLaunchKernelGGL((k_gemv_team<F, 2, MR>), dim3((unsigned)grid), dim3(64 * team), 0, s, wt->data,
-                     wt->data + wt->aux_off, x, xtype, y, ytype, wt->n, wt->k);
+                     wt->data + wt->aux_off, x, xtype, o, wt->n, wt->k);
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }
 
-// Rows of at most 64 pieces, MR activation rows: the segment kernel.
-template <class F, int MR>
-int run_seg(const rq_weight *wt, const void *x, int xtype, void *y, int ytype, hipStream_t s, int mrows) {
-  const int P = (int)(wt->k / F::PE);
-  const int seg_log2 = ceil_log2(P < 16 ? 16 : P);
-  const int rows_per_wg = 4 * (64 >> seg_log2);
-  const int64_t groups = (wt->n + rows_per_wg - 1) / rows_per_wg;
-  const unsigned blocks = (unsigned)(groups < 16384 ? groups : 16384);
-  // k <= 64 pieces always fits the LDS copy of x (x is 16-byte aligned here);
-  // chunks of x per thread: at most MR 64 PE / 4 / 256 = 4 MR.
-  const size_t xb = MR * xlds_bytes(wt->k);
-  const int per = (x_chunks(mrows * wt->k, xtype) + 255) / 256;
-#define RQ_M1(XR)                                                                                               \
-  hipLaunchKernelGGL((k_gemv_m1<F, XR, MR>), dim3(blocks), dim3(256), xb, s, wt->data, wt->data + wt->aux_off, \
-                     x, xtype, y, ytype, wt->n, wt->k, seg_log2, rows_per_wg, groups, mrows)
+// Segment layout of a row of P <= 64 pieces: seg = max(16, next_pow2(P))
+// lanes a row, four waves a workgroup.
+struct SegGeo {
+  int seg_log2, rows_per_wg;
+};
+SegGeo seg_geo(int P) {
+  const int l = ceil_log2(P < 16 ? 16 : P);
+  return {l, 4 * (64 >> l)};
+}
+
+// The segment kernel on a set of weights (x 16-byte aligned; k <= 64 pieces
+// always fits the LDS copy of x).  Chunks of x per thread: at most
+// MR 64 PE / 4 / 256 = 4 MR.
+template <class F, int MR, bool MULTI>
+int launch_seg(const SegSet &set, int64_t k, unsigned blocks, const void *x, int xtype, int mrows, hipStream_t s) {
+  const SegGeo geo = seg_geo((int)(k / F::PE));
+  const size_t xb = MR * xlds_bytes(k);
+  const int per = (x_chunks(mrows * k, xtype) + 255) / 256;
+#define RQ_M1(XR)                                                                                           \
+  hipLaunchKernelGGL((k_gemv_m1<F, XR, MR, MULTI>), dim3(blocks), dim3(256), xb, s, set, x, xtype, k,       \
+                     geo.seg_log2, geo.rows_per_wg, mrows)
   if (per <= 1) {
     RQ_M1(1);
   } else if (per <= 2) {
     RQ_M1(2);
   } else if constexpr (MR == 1) {
     RQ_M1(4);
-  } else if constexpr (MR == 2) {
-    if (per <= 4) RQ_M1(4);
-    else RQ_M1(8);
-  } else {  // four rows of two-run formats: k <= 2048, at most 8 chunks a thread
+  } else {  // two rows, or four slots of two-run formats: k <= 2048, at most 8 chunks a thread
     if (per <= 4) RQ_M1(4);
     else RQ_M1(8);
   }
+#undef RQ_M1
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }
 
+// Rows of at most 64 pieces, MR activation rows: the segment kernel.
+template <class F, int MR>
+int run_seg(const rq_weight *wt, const void *x, int xtype, const Out &o, hipStream_t s, int mrows = MR) {
+  const SegGeo geo = seg_geo((int)(wt->k / F::PE));
+  SegSet set{};
+  set.w[0] = wt->data;
+  set.aux[0] = wt->data + wt->aux_off;
+  set.o[0] = o;
+  set.n[0] = wt->n;
+  set.g_end[0] = (wt->n + geo.rows_per_wg - 1) / geo.rows_per_wg;
+  set.count = 1;
+  const unsigned blocks = (unsigned)(set.g_end[0] < 16384 ? set.g_end[0] : 16384);
+  return launch_seg<F, MR, false>(set, wt->k, blocks, x, xtype, mrows, s);
+}
+
+template <class F>
+int run_m1(const rq_weight *wt, const void *x, int xtype, const Out &o, hipStream_t s) {
+  const int P = (int)(wt->k / F::PE);
+  // Long rows on many rows: one wave per row walking the rows.
+  if (P > 64 && wt->n >= 4096) {
+    switch ((P + 63) / 64) {
+      case 2: return run_long<F, 2>(wt, x, xtype, o, s);
+      case 3: return run_long<F, 3>(wt, x, xtype, o, s);
+      case 4: return run_long<F, 4>(wt, x, xtype, o, s);
+      default: break;
+    }
+  }
+  // Other long rows: a team of waves per row.
+  if (P > 64) return run_team<F, 1>(wt, x, xtype, o, s);
+  return run_seg<F, 1>(wt, x, xtype, o, s);
+}
+
 template <class F, int MAXPPL>
-int dispatch_fmt(const rq_weight *wt, const void *x, int xtype, int64_t m, void *y, int ytype,
-                 hipStream_t s) {
+int dispatch_fmt(const rq_weight *wt, const void *x, int xtype, int64_t m, const Out &o, hipStream_t s) {
   if (wt->k % F::PE != 0) return RQ_E_UNSUPPORTED;
-  if (m == 1) return run_m1<F>(wt, x, xtype, y, ytype, s);
+  if (m == 1) return run_m1<F>(wt, x, xtype, o, s);
   const int P = (int)(wt->k / F::PE);
   // Two activation rows on the segment kernel: each weight decoded once,
   // one FMA per weight and row.
-  if (m == 2 && P <= 64 && wt->k % 8 == 0) return run_seg<F, 2>(wt, x, xtype, y, ytype, s);
+  if (m == 2 && P <= 64 && wt->k % 8 == 0) return run_seg<F, 2>(wt, x, xtype, o, s);
   // Three f32 / f16 rows: four row slots (two-run formats; Q6_K's four runs
   // a piece would not fit four rows of activations in registers).
   if constexpr (F::RUNS == 2) {
-    if ((m == 3 || m == 4) && P <= 64 && wt->k % 8 == 0) return run_seg<F, 4>(wt, x, xtype, y, ytype, s, (int)m);
+    if ((m == 3 || m == 4) && P <= 64 && wt->k % 8 == 0) return run_seg<F, 4>(wt, x, xtype, o, s, (int)m);
   }
   // (Q6_K's four runs a piece leave no registers for a second row in a
   // sixteen-wave team.)
   if constexpr (F::RUNS == 2) {
     if (m == 2 && P > 64 && wt->n < 4096 && (P + 63) / 64 <= kTeamMax && wt->k % 8 == 0)
-      return run_team<F, 2>(wt, x, xtype, y, ytype, s);
+      return run_team<F, 2>(wt, x, xtype, o, s);
   }
-  if (P <= 32) return run_multi<F, 1>(wt, x, xtype, m, y, ytype, ceil_log2(P), s);
+  if (P <= 32) return run_multi<F, 1>(wt, x, xtype, m, o, ceil_log2(P), s);
   const int ppl = (P + 63) / 64;
   if (ppl > MAXPPL) return RQ_E_UNSUPPORTED;
   switch (ppl) {
-    case 1: return run_multi<F, 1>(wt, x, xtype, m, y, ytype, 6, s);
-    case 2: return run_multi<F, (MAXPPL >= 2 ? 2 : 1)>(wt, x, xtype, m, y, ytype, 6, s);
-    case 3: return run_multi<F, (MAXPPL >= 3 ? 3 : 1)>(wt, x, xtype, m, y, ytype, 6, s);
-    case 4: return run_multi<F, (MAXPPL >= 4 ? 4 : 1)>(wt, x, xtype, m, y, ytype, 6, s);
+    case 1: return run_multi<F, 1>(wt, x, xtype, m, o, 6, s);
+    case 2: return run_multi<F, (MAXPPL >= 2 ? 2 : 1)>(wt, x, xtype, m, o, 6, s);
+    case 3: return run_multi<F, (MAXPPL >= 3 ? 3 : 1)>(wt, x, xtype, m, o, 6, s);
+    case 4: return run_multi<F, (MAXPPL >= 4 ? 4 : 1)>(wt, x, xtype, m, o, 6, s);
     default: return RQ_E_UNSUPPORTED;
   }
 }
 
+// Several weights of format F sharing x (equal k, rows of at most 64
+// pieces, M = 1 or 2): the row groups of all of them in one grid.
+template <class F>
+int run_seg_set(const rq_weight *const *w, int count, const void *x, int xtype, int64_t m, const Out *o,
+                hipStream_t s) {
+  const int64_t k = w[0]->k;
+  if (k % F::PE != 0) return RQ_E_UNSUPPORTED;
+  const int P = (int)(k / F::PE);
+  if (P > 64 || (m == 2 && k % 8 != 0)) return RQ_E_UNSUPPORTED;
+  const SegGeo geo = seg_geo(P);
+  SegSet set{};
+  int64_t total = 0;
+  for (int j = 0; j < count; ++j) {
+    set.w[j] = w[j]->data;
+    set.aux[j] = w[j]->data + w[j]->aux_off;
+    set.o[j] = o[j];
+    set.n[j] = w[j]->n;
+    total += (w[j]->n + geo.rows_per_wg - 1) / geo.rows_per_wg;
+    set.g_end[j] = total;
+  }
+  set.count = count;
+  if (total > 0x7FFFFFFF) return RQ_E_UNSUPPORTED;
+  if (m == 1) return launch_seg<F, 1, true>(set, k, (unsigned)total, x, xtype, 1, s);
+  return launch_seg<F, 2, true>(set, k, (unsigned)total, x, xtype, 2, s);
+}
+
 }  // namespace
 
-int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m, void *y,
-                        int ytype, hipStream_t s) {
+int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m, const Out &o, hipStream_t s,
+                        WsLease &ws) {
   // The fused kernels read activations with 8- or 16-byte vector loads.
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
   // bf16 activations with m > 1 run on the matrix cores: up to 64 rows with
@@ -757,68 +795,83 @@ int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m
                             (wt->qtype == RQ_Q4_K || wt->qtype == RQ_Q6_K || wt->qtype == RQ_Q8_0 ||
                              wt->qtype == RQ_Q5_K || wt->qtype == RQ_Q4_0 || wt->qtype == RQ_Q5_0);
   if (m > 1 && xtype == RQ_BF16 && !two_rows_seg) {
-    int rc = m <= 64 ? launch_linear_smallm(wt, x, m, y, ytype, s) : RQ_E_UNSUPPORTED;
-    if (rc == RQ_E_UNSUPPORTED) rc = launch_linear_mfma(wt, x, m, y, ytype, s);
+    int rc = m <= 64 ? launch_linear_smallm(wt, x, m, o, s) : RQ_E_UNSUPPORTED;
+    if (rc == RQ_E_UNSUPPORTED) rc = launch_linear_mfma(wt, x, m, o, s, ws);
     if (rc != RQ_E_UNSUPPORTED) return rc;
   }
   // f32 / f16 activations with 4 <= m <= 64: exact-f32 weights on the f32
   // matrix cores (16 MFMAs of K = 4 per 64-element chunk; at m = 2..3 the
   // VALU kernels' few FMAs per weight are cheaper: 37 vs 47 us per 0.5B
   // layer at m = 2, 150 vs 54 us at m = 16).
-  if (m >= 4 && m <= 64 && (xtype == RQ_F32 || xtype == RQ_F16)) {
-    const int rc = launch_linear_smallm_f32(wt, x, xtype, m, y, ytype, s);
+  const bool f32x = xtype == RQ_F32 || xtype == RQ_F16;
+  if (m >= 4 && m <= 64 && f32x) {
+    const int rc = launch_linear_smallm_f32(wt, x, xtype, m, o, s);
     if (rc != RQ_E_UNSUPPORTED) return rc;
   }
   // More rows (prefill with f32 activations, the reference's compute type):
   // the same kernel on slices of 64 activation rows (the weights are read
   // once per slice, mostly from cache), a last slice of 2 or 3 rows on the
   // VALU kernel and a single row on the GEMV.
-  if (m > 64 && (xtype == RQ_F32 || xtype == RQ_F16) && wt->k % 64 == 0 &&
-      reinterpret_cast<uintptr_t>(x) % 16 == 0) {
-    const size_t xb = xtype == RQ_F32 ? 4 : 2, yb = ytype == RQ_F32 ? 4 : 2;
+  if (m > 64 && f32x && wt->k % 64 == 0) {
+    const size_t xb = xtype == RQ_F32 ? 4 : 2, yb = o.ytype == RQ_F32 ? 4 : 2;
     for (int64_t r0 = 0; r0 < m; r0 += 64) {
       const int64_t mm = m - r0 < 64 ? m - r0 : 64;
       const void *xs = static_cast<const uint8_t *>(x) + (size_t)r0 * (size_t)wt->k * xb;
-      void *ys = static_cast<uint8_t *>(y) + (size_t)r0 * (size_t)wt->n * yb;
-      const int rc = mm >= 4 ? launch_linear_smallm_f32(wt, xs, xtype, mm, ys, ytype, s)
-                             : launch_linear_fused(wt, xs, xtype, mm, ys, ytype, s);
+      Out os = o;
+      os.y = static_cast<uint8_t *>(o.y) + (size_t)r0 * (size_t)wt->n * yb;
+      const int rc = mm >= 4 ? launch_linear_smallm_f32(wt, xs, xtype, mm, os, s)
+                             : launch_linear_fused(wt, xs, xtype, mm, os, s, ws);
       if (rc) return rc;
     }
     return RQ_OK;
   }
+  int rc;
   switch (wt->qtype) {
     case RQ_Q4_K:
       // Pieces must not straddle rows: rows start on 64-element chunk bounds.
-      if (wt->k % 64 != 0) return RQ_E_UNSUPPORTED;
-      return dispatch_fmt<FmtQ4K, 4>(wt, x, xtype, m, y, ytype, s);
+      rc = wt->k % 64 ? RQ_E_UNSUPPORTED : dispatch_fmt<FmtQ4K, 4>(wt, x, xtype, m, o, s);
+      break;
     case RQ_Q6_K:
-      if (wt->k % 128 != 0) return RQ_E_UNSUPPORTED;
-      return dispatch_fmt<FmtQ6K, 2>(wt, x, xtype, m, y, ytype, s);
+      rc = wt->k % 128 ? RQ_E_UNSUPPORTED : dispatch_fmt<FmtQ6K, 2>(wt, x, xtype, m, o, s);
+      break;
     case RQ_Q8_0:
-      if (wt->k % 64 != 0) return RQ_E_UNSUPPORTED;
-      return dispatch_fmt<FmtQ8, 4>(wt, x, xtype, m, y, ytype, s);
+      rc = wt->k % 64 ? RQ_E_UNSUPPORTED : dispatch_fmt<FmtQ8, 4>(wt, x, xtype, m, o, s);
+      break;
     case RQ_Q5_K:
-      if (wt->k % 64 != 0) return RQ_E_UNSUPPORTED;
-      return dispatch_fmt<FmtQ5K, 4>(wt, x, xtype, m, y, ytype, s);
+      rc = wt->k % 64 ? RQ_E_UNSUPPORTED : dispatch_fmt<FmtQ5K, 4>(wt, x, xtype, m, o, s);
+      break;
     case RQ_Q4_0:
-      if (wt->k % 64 != 0) return RQ_E_UNSUPPORTED;
-      return dispatch_fmt<FmtQx0<false>, 4>(wt, x, xtype, m, y, ytype, s);
+      rc = wt->k % 64 ? RQ_E_UNSUPPORTED : dispatch_fmt<FmtQx0<false>, 4>(wt, x, xtype, m, o, s);
+      break;
     case RQ_Q5_0:
-      if (wt->k % 64 != 0) return RQ_E_UNSUPPORTED;
-      return dispatch_fmt<FmtQx0<true>, 4>(wt, x, xtype, m, y, ytype, s);
+      rc = wt->k % 64 ? RQ_E_UNSUPPORTED : dispatch_fmt<FmtQx0<true>, 4>(wt, x, xtype, m, o, s);
+      break;
     default:
       return RQ_E_UNSUPPORTED;
   }
+  // Two or three f32 / f16 rows on rows too long for the VALU layouts: the
+  // f32 matrix-core kernel takes every format and length (k % 64 == 0).
+  if (rc == RQ_E_UNSUPPORTED && f32x && m >= 2 && m <= 3) rc = launch_linear_smallm_f32(wt, x, xtype, m, o, s);
+  return rc;
 }
 
-int launch_linear_dense_f32(const float *w, int64_t n, int64_t k, const void *x, int xtype,
-                            int64_t m, void *y, int ytype, hipStream_t s) {
-  int64_t blocks = (n + 3) / 4;
-  if (blocks > 8192) blocks = 8192;
-  if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(k_dense_f32, dim3((unsigned)blocks), dim3(kThreads), 0, s, w, n, k, x, xtype,
-                     m, y, ytype);
-  return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "dense launch failed");
+int launch_linear_multi(const rq_weight *const *w, int count, const void *x, int xtype, int64_t m, const Out *o,
+                        hipStream_t s) {
+  if (count < 1 || count > kMultiMax || (m != 1 && m != 2)) return RQ_E_UNSUPPORTED;
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
+  const int qt = w[0]->qtype;
+  const int64_t k = w[0]->k;
+  for (int j = 1; j < count; ++j)
+    if (w[j]->qtype != qt || w[j]->k != k) return RQ_E_UNSUPPORTED;
+  switch (qt) {
+    case RQ_Q4_K: return k % 64 ? RQ_E_UNSUPPORTED : run_seg_set<FmtQ4K>(w, count, x, xtype, m, o, s);
+    case RQ_Q6_K: return k % 128 ? RQ_E_UNSUPPORTED : run_seg_set<FmtQ6K>(w, count, x, xtype, m, o, s);
+    case RQ_Q8_0: return k % 64 ? RQ_E_UNSUPPORTED : run_seg_set<FmtQ8>(w, count, x, xtype, m, o, s);
+    case RQ_Q5_K: return k % 64 ? RQ_E_UNSUPPORTED : run_seg_set<FmtQ5K>(w, count, x, xtype, m, o, s);
+    case RQ_Q4_0: return k % 64 ? RQ_E_UNSUPPORTED : run_seg_set<FmtQx0<false>>(w, count, x, xtype, m, o, s);
+    case RQ_Q5_0: return k % 64 ? RQ_E_UNSUPPORTED : run_seg_set<FmtQx0<true>>(w, count, x, xtype, m, o, s);
+    default: return RQ_E_UNSUPPORTED;
+  }
 }
 
 }  // namespace rq

@@ -66,6 +66,52 @@ hipStream_t as_stream(void *s);
 int upload_blocks(int qtype, const uint8_t *src, uint64_t nblocks, int bbytes, uint8_t *dptr, uint64_t aux_off,
                   int device);
 
+// ---- the output side of a linear call ----
+//
+// y[m, n] (row stride n) of type ytype, plus an optional per-column bias of
+// n values of type btype (F32, F16 or BF16): linear_bias's broadcast add
+// (linear_layer.rs:107-118) fused into the epilogue of every kernel.
+struct Out {
+  void *y;
+  const void *bias;  // null: no bias
+  int ytype;
+  int btype;
+};
+
+// ---- workspace: device memory that outlives a call ----
+//
+// One buffer per (device, stream), grown on demand and reused by every later
+// call on that stream, so the split-K partials, activation copies and FP8
+// scratch of a call cost no allocation.  A lease holds the (device, stream)
+// slot for the duration of one entry point's launches (two threads issuing
+// to one stream take turns; their kernels still run in stream order).  Under
+// stream capture a buffer that is already large enough is used as it is (the
+// graph then refers to it, and it is never freed); a larger need is met by a
+// stream-ordered allocation that becomes part of the graph.  A replaced
+// buffer is freed in stream order when the lease ends, unless a captured
+// graph may refer to it.  The slot is taken at the first get().
+class WsLease {
+ public:
+  WsLease(int device, hipStream_t s);
+  ~WsLease();
+  WsLease(const WsLease &) = delete;
+  WsLease &operator=(const WsLease &) = delete;
+  // `bytes` of device memory (256-byte aligned) for this call; null with
+  // *rc set (and the error message) on failure.  Earlier pointers of the same
+  // lease stay valid.
+  void *get(size_t bytes, int *rc);
+
+ private:
+  void acquire();
+  struct Slot *slot_ = nullptr;
+  int device_;
+  hipStream_t s_;
+  bool capturing_ = false;
+  size_t used_ = 0;
+  void *async_[4] = {nullptr, nullptr, nullptr, nullptr};  // freed in stream order when the lease ends
+  int n_async_ = 0;
+};
+
 // ---- launchers (each returns RQ_OK or an error code and message) ----
 int launch_dequant_weight(const rq_weight *w, float *out, hipStream_t s);
 // Rows dev_ids[0 .. n_ids) of a handle (every id < n, k % 4 == 0) as f32.
@@ -73,25 +119,35 @@ int launch_gather_rows(const rq_weight *w, const uint32_t *dev_ids, int64_t n_id
                        hipStream_t s);
 int launch_dequant_raw(int qtype, const uint8_t *src, uint64_t nblocks, float *out,
                        hipStream_t s);
-// Fused matmul on a handle; returns RQ_E_UNSUPPORTED when the handle's
-// shape has no fused kernel (the caller then takes the decode path).
-int launch_linear_fused(const rq_weight *w, const void *x, int xtype, int64_t m, void *y,
-                        int ytype, hipStream_t s);
+// Fused matmul on a handle (x 16-byte aligned); returns RQ_E_UNSUPPORTED
+// when the handle's shape has no fused kernel (the caller then takes the
+// generic kernel).
+int launch_linear_fused(const rq_weight *w, const void *x, int xtype, int64_t m, const Out &o, hipStream_t s,
+                        WsLease &ws);
+// One launch for several weights of one format sharing x (count <= kMultiMax,
+// equal k): M = 1 and M = 2 on the segment layout.  RQ_E_UNSUPPORTED when
+// the shapes take another layout (the caller then launches them one by one).
+constexpr int kMultiMax = 8;
+int launch_linear_multi(const rq_weight *const *w, int count, const void *x, int xtype, int64_t m, const Out *o,
+                        hipStream_t s);
 // MFMA GEMM for bf16 activations and m > 1 (RQ_E_UNSUPPORTED if the shape or
 // format has no tiled kernel).
-int launch_linear_mfma(const rq_weight *w, const void *x, int64_t m, void *y, int ytype,
-                       hipStream_t s);
+int launch_linear_mfma(const rq_weight *w, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease &ws);
 // Matrix-core kernel for bf16 activations and 2 <= m <= 64 (speculative
 // verify), RQ_E_UNSUPPORTED outside that or for formats it has no decoder for.
-int launch_linear_smallm(const rq_weight *w, const void *x, int64_t m, void *y, int ytype,
-                         hipStream_t s);
+int launch_linear_smallm(const rq_weight *w, const void *x, int64_t m, const Out &o, hipStream_t s);
 // The same for f32 / f16 activations on the f32 matrix cores with exact f32
 // weights (f32 accumulation).
-int launch_linear_smallm_f32(const rq_weight *wt, const void *x, int xtype, int64_t m, void *y, int ytype,
+int launch_linear_smallm_f32(const rq_weight *wt, const void *x, int xtype, int64_t m, const Out &o,
                              hipStream_t s);
-// y = x * W^T with W dense f32 [n, k] in device memory.
-int launch_linear_dense_f32(const float *w, int64_t n, int64_t k, const void *x, int xtype,
-                            int64_t m, void *y, int ytype, hipStream_t s);
+// Every shape and alignment: exact f32 weights decoded element by element
+// from the handle, f32 accumulation (the shapes the fused kernels do not
+// take: rows cut inside a 64-element chunk, rows longer than the GEMV
+// layouts hold).
+int launch_linear_generic(const rq_weight *w, const void *x, int xtype, int64_t m, const Out &o, hipStream_t s);
+// y[m, n] = (y as ytype) + (bias as ytype): linear_bias's broadcast add
+// (linear_layer.rs:111-115) on an output that is already there.
+int launch_bias_add(void *y, int ytype, int64_t m, int64_t n, const void *bias, int btype, hipStream_t s);
 int launch_fp8_quantize(const void *x, int xtype, int64_t m, int64_t k, int mode, uint8_t *xq,
                         float *xs, hipStream_t s);
 int launch_fp8_gemm(const uint8_t *xq, const float *xs, int64_t m, const uint8_t *w,
@@ -106,7 +162,7 @@ int launch_marlin_linear(const uint32_t *packed, const float *s, int64_t n, int6
                          int64_t m, void *y, int ytype, hipStream_t st);
 // Paged-KV block quantizer (arguments validated by the caller).
 int launch_kv_quantize(const void *t, int ttype, int64_t b, int64_t h, int64_t sd, int mode, void *q,
-                       float *scales, hipStream_t s);
+                       float *scales, hipStream_t s, WsLease &ws);
 int launch_kv_dequantize(const void *q, int mode, const float *scales, int64_t b, int64_t h, int64_t sd, void *out,
                          int otype, hipStream_t s);
 
@@ -150,6 +206,40 @@ __device__ __forceinline__ void store_out(void *y, int ytype, int64_t idx, float
   } else {
     static_cast<_Float16 *>(y)[idx] = (_Float16)v;
   }
+}
+
+// A dense value of type t (F32, F16 or BF16) at index i, as f32.
+__device__ __forceinline__ float load_as_f32(const void *p, int t, int64_t i) {
+  if (t == RQ_F32) return static_cast<const float *>(p)[i];
+  if (t == RQ_BF16) return bf16_bits_to_f32(static_cast<const uint16_t *>(p)[i]);
+  return (float)static_cast<const _Float16 *>(p)[i];
+}
+
+// v rounded to the output type and widened back (exact for F32).  Both
+// roundings are computed and one is selected: no branches in the unrolled
+// epilogues that use it.
+__device__ __forceinline__ float round_as(int ytype, float v) {
+  const float b = bf16_bits_to_f32(f32_to_bf16_bits(v));
+  const float h = (float)(_Float16)v;
+  return ytype == RQ_F32 ? v : (ytype == RQ_BF16 ? b : h);
+}
+
+// Bias of output column col as f32 (0 without a bias).
+__device__ __forceinline__ float bias_at(const Out &o, int64_t col) {
+  return o.bias ? load_as_f32(o.bias, o.btype, col) : 0.0f;
+}
+
+// linear_bias (linear_layer.rs:107-118) adds the bias cast to y's dtype to
+// linear's result cast to y's dtype.  Fused into an epilogue, the f32 sum
+// acc + (bias as ytype) is rounded once by the store: for f32 outputs that
+// is the reference's acc + b exactly; for bf16 / f16 outputs it can differ
+// from the reference's two roundings by one unit in the last place of y
+// (and is the nearer of the two to the exact sum).
+__device__ __forceinline__ float with_bias(float acc, float b, int ytype) { return acc + round_as(ytype, b); }
+
+// Output (row, col) of a linear call, with its bias.
+__device__ __forceinline__ void store_linear(const Out &o, int64_t row, int64_t n, int64_t col, float acc) {
+  store_out(o.y, o.ytype, row * n + col, o.bias ? with_bias(acc, load_as_f32(o.bias, o.btype, col), o.ytype) : acc);
 }
 
 // Load 4 consecutive activations starting at element idx (idx % 4 == 0) as f32.

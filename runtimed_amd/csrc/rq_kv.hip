@@ -210,7 +210,7 @@ void launch_decode(bool vec, dim3 grid, hipStream_t s, const void *q, const floa
 }  // namespace
 
 int launch_kv_quantize(const void *t, int ttype, int64_t b, int64_t h, int64_t sd, int mode, void *q,
-                       float *scales, hipStream_t s) {
+                       float *scales, hipStream_t s, WsLease &ws) {
   int64_t xb = 0;
   const int64_t per = slab_split(sd, &xb);
   const dim3 grid((unsigned)xb, (unsigned)(b * h < KV_MAX_SLABS_Y ? b * h : KV_MAX_SLABS_Y));
@@ -225,25 +225,21 @@ int launch_kv_quantize(const void *t, int ttype, int64_t b, int64_t h, int64_t s
   int64_t P = (per_head + 4095) / 4096;
   if (P > KV_MAX_PARTS) P = KV_MAX_PARTS;
   const int64_t chunk = ((per_head + P - 1) / P + 3) & ~(int64_t)3;
-  float *part = nullptr;
-  hipError_t e = hipMallocAsync(reinterpret_cast<void **>(&part), (size_t)(h * P) * sizeof(float), s);
-  if (e != hipSuccess)
-    return set_error(e == hipErrorOutOfMemory ? RQ_E_NOMEM : RQ_E_DEVICE, "hipMallocAsync: %s",
-                     hipGetErrorString(e));
+  int rc = RQ_OK;
+  float *part = static_cast<float *>(ws.get((size_t)(h * P) * sizeof(float), &rc));
+  if (!part) return rc;
   if (vec)
     hipLaunchKernelGGL(k_kv_absmax<true>, dim3((unsigned)P, (unsigned)h), dim3(KV_THREADS), 0, s, t, ttype, b, h, sd,
                        chunk, part);
   else
     hipLaunchKernelGGL(k_kv_absmax<false>, dim3((unsigned)P, (unsigned)h), dim3(KV_THREADS), 0, s, t, ttype, b, h,
                        sd, chunk, part);
-  int rc = last_launch("kv absmax");
+  rc = last_launch("kv absmax");
   if (!rc) {
     if (mode == RQ_KV_FP8) launch_encode<RQ_KV_FP8>(vec, grid, s, t, ttype, b, h, sd, part, (int)P, per, q, scales);
     else launch_encode<RQ_KV_INT8>(vec, grid, s, t, ttype, b, h, sd, part, (int)P, per, q, scales);
     rc = last_launch("kv encode");
   }
-  e = hipFreeAsync(part, s);
-  if (!rc && e != hipSuccess) rc = set_error(RQ_E_DEVICE, "hipFreeAsync: %s", hipGetErrorString(e));
   return rc;
 }
 

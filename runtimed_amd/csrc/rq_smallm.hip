@@ -302,7 +302,7 @@ __device__ __forceinline__ void mma_chunk(const typename C::Chunk &c, const XFra
 // rows 4 (l / 16) + i.  Thread t sums one lane slot of one column tile.
 template <int MT, int NW>
 __device__ __forceinline__ void reduce_store(f32x4 (&part)[NW][MT][64], const f32x4 (&acc)[MT], int wave, int lane,
-                                             int64_t m, int64_t n, int64_t n0, void *y, int ytype) {
+                                             int64_t m, int64_t n, int64_t n0, const Out &o) {
 #pragma unroll
   for (int ct = 0; ct < MT; ++ct) part[wave][ct][lane] = acc[ct];
   __syncthreads();
@@ -316,7 +316,7 @@ __device__ __forceinline__ void reduce_store(f32x4 (&part)[NW][MT][64], const f3
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int64_t nr = n0 + 4 * (l >> 4) + i;
-        if (nr < n) store_one(y, ytype, mr * n + nr, v[i]);
+        if (nr < n) store_one(o.y, o.ytype, mr * n + nr, o.bias ? with_bias(v[i], bias_at(o, nr), o.ytype) : v[i]);
       }
     }
   }
@@ -331,8 +331,8 @@ __device__ __forceinline__ void reduce_store(f32x4 (&part)[NW][MT][64], const f3
 // loop top.  Chunks past the end load a valid chunk again and are masked.
 template <class C, int MT, int NW, int B>
 __global__ __launch_bounds__(64 * NW) void k_smallm(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
-                                                    const uint16_t *__restrict__ x, int64_t m,
-                                                    void *__restrict__ y, int ytype, int64_t n, int64_t k) {
+                                                    const uint16_t *__restrict__ x, int64_t m, const Out o,
+                                                    int64_t n, int64_t k) {
   __shared__ f32x4 part[NW][MT][64];
   const int lane = threadIdx.x & 63, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -372,7 +372,7 @@ __global__ __launch_bounds__(64 * NW) void k_smallm(const uint8_t *__restrict__ 
     }
   }
 
-  reduce_store<MT, NW>(part, acc, wave, lane, m, n, n0, y, ytype);
+  reduce_store<MT, NW>(part, acc, wave, lane, m, n, n0, o);
 }
 
 // ---- f32 / f16 activations ------------------------------------------------
@@ -429,8 +429,8 @@ __device__ __forceinline__ void mma_chunk_f32(const typename C::Chunk &c, const 
 
 template <class C, int MT, int NW, int B, int XT>
 __global__ __launch_bounds__(64 * NW) void k_smallm_f32(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
-                                                        const uint8_t *__restrict__ x, int64_t m,
-                                                        void *__restrict__ y, int ytype, int64_t n, int64_t k) {
+                                                        const uint8_t *__restrict__ x, int64_t m, const Out o,
+                                                        int64_t n, int64_t k) {
   __shared__ f32x4 part[NW][MT][64];
   const int lane = threadIdx.x & 63, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -467,11 +467,11 @@ __global__ __launch_bounds__(64 * NW) void k_smallm_f32(const uint8_t *__restric
     }
   }
 
-  reduce_store<MT, NW>(part, acc, wave, lane, m, n, n0, y, ytype);
+  reduce_store<MT, NW>(part, acc, wave, lane, m, n, n0, o);
 }
 
 template <class C, int MT, int XT>
-int run_mt_f32(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {
+int run_mt_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s) {
   constexpr int B = MT == 1 ? 4 : (MT == 2 ? 2 : 1);
   const dim3 grid((unsigned)((wt->n + 15) / 16));
   const uint8_t *aux = wt->data + wt->aux_off;
@@ -480,29 +480,29 @@ int run_mt_f32(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype
   // M = 32 24.6 -> 20.8; four column tiles and the bf16 kernel were slower).
   if (MT <= 2 && wt->k / 64 > 4 * B)
     hipLaunchKernelGGL((k_smallm_f32<C, MT, 16, (MT == 1 ? 2 : 1), XT>), grid, dim3(1024), 0, s, wt->data, aux,
-                       static_cast<const uint8_t *>(x), m, y, ytype, wt->n, wt->k);
+                       static_cast<const uint8_t *>(x), m, o, wt->n, wt->k);
   else
     hipLaunchKernelGGL((k_smallm_f32<C, MT, 4, B, XT>), grid, dim3(256), 0, s, wt->data, aux,
-                       static_cast<const uint8_t *>(x), m, y, ytype, wt->n, wt->k);
+                       static_cast<const uint8_t *>(x), m, o, wt->n, wt->k);
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "small-M launch failed");
 }
 
 template <class C, int XT>
-int run_f32(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {
-  if (m <= 16) return run_mt_f32<C, 1, XT>(wt, x, m, y, ytype, s);
-  if (m <= 32) return run_mt_f32<C, 2, XT>(wt, x, m, y, ytype, s);
-  return run_mt_f32<C, 4, XT>(wt, x, m, y, ytype, s);
+int run_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s) {
+  if (m <= 16) return run_mt_f32<C, 1, XT>(wt, x, m, o, s);
+  if (m <= 32) return run_mt_f32<C, 2, XT>(wt, x, m, o, s);
+  return run_mt_f32<C, 4, XT>(wt, x, m, o, s);
 }
 
 template <int XT>
-int dispatch_f32(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {
+int dispatch_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s) {
   switch (wt->qtype) {
-    case RQ_Q4_K: return run_f32<SmQ4K, XT>(wt, x, m, y, ytype, s);
-    case RQ_Q6_K: return run_f32<SmQ6K, XT>(wt, x, m, y, ytype, s);
-    case RQ_Q8_0: return run_f32<SmQ8, XT>(wt, x, m, y, ytype, s);
-    case RQ_Q5_K: return run_f32<SmQ5K, XT>(wt, x, m, y, ytype, s);
-    case RQ_Q4_0: return run_f32<SmQx0<false>, XT>(wt, x, m, y, ytype, s);
-    case RQ_Q5_0: return run_f32<SmQx0<true>, XT>(wt, x, m, y, ytype, s);
+    case RQ_Q4_K: return run_f32<SmQ4K, XT>(wt, x, m, o, s);
+    case RQ_Q6_K: return run_f32<SmQ6K, XT>(wt, x, m, o, s);
+    case RQ_Q8_0: return run_f32<SmQ8, XT>(wt, x, m, o, s);
+    case RQ_Q5_K: return run_f32<SmQ5K, XT>(wt, x, m, o, s);
+    case RQ_Q4_0: return run_f32<SmQx0<false>, XT>(wt, x, m, o, s);
+    case RQ_Q5_0: return run_f32<SmQx0<true>, XT>(wt, x, m, o, s);
     default: return RQ_E_UNSUPPORTED;
   }
 }
@@ -513,44 +513,45 @@ int dispatch_f32(const rq_weight *wt, const void *x, int64_t m, void *y, int yty
 // More waves per workgroup or deeper batches were slower: the masked
 // chunks of a partly filled batch cost as much decode as real ones.
 template <class C, int MT>
-int run_mt(const rq_weight *wt, const uint16_t *x, int64_t m, void *y, int ytype, hipStream_t s) {
+int run_mt(const rq_weight *wt, const uint16_t *x, int64_t m, const Out &o, hipStream_t s) {
   constexpr int B = MT == 4 ? 1 : 4;
   const dim3 grid((unsigned)((wt->n + 15) / 16));
   const uint8_t *aux = wt->data + wt->aux_off;
-  hipLaunchKernelGGL((k_smallm<C, MT, 4, B>), grid, dim3(256), 0, s, wt->data, aux, x, m, y, ytype, wt->n, wt->k);
+  hipLaunchKernelGGL((k_smallm<C, MT, 4, B>), grid, dim3(256), 0, s, wt->data, aux, x, m, o, wt->n, wt->k);
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "small-M launch failed");
 }
 
 template <class C>
-int run(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {
+int run(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s) {
   const uint16_t *xb = static_cast<const uint16_t *>(x);
-  if (m <= 16) return run_mt<C, 1>(wt, xb, m, y, ytype, s);
-  if (m <= 32) return run_mt<C, 2>(wt, xb, m, y, ytype, s);
-  return run_mt<C, 4>(wt, xb, m, y, ytype, s);
+  if (m <= 16) return run_mt<C, 1>(wt, xb, m, o, s);
+  if (m <= 32) return run_mt<C, 2>(wt, xb, m, o, s);
+  return run_mt<C, 4>(wt, xb, m, o, s);
 }
 
 }  // namespace
 
 // f32 / f16 activations, 2 <= m <= 64, k % 64 == 0, 16-byte aligned x
-// (dispatched from m = 4).
-int launch_linear_smallm_f32(const rq_weight *wt, const void *x, int xtype, int64_t m, void *y, int ytype,
+// (dispatched from m = 4, and at m = 2..3 for rows the VALU layouts do not
+// take).
+int launch_linear_smallm_f32(const rq_weight *wt, const void *x, int xtype, int64_t m, const Out &o,
                              hipStream_t s) {
   if (m < 2 || m > 64 || wt->k % 64 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
-  if (xtype == RQ_F32) return dispatch_f32<RQ_F32>(wt, x, m, y, ytype, s);
-  if (xtype == RQ_F16) return dispatch_f32<RQ_F16>(wt, x, m, y, ytype, s);
+  if (xtype == RQ_F32) return dispatch_f32<RQ_F32>(wt, x, m, o, s);
+  if (xtype == RQ_F16) return dispatch_f32<RQ_F16>(wt, x, m, o, s);
   return RQ_E_UNSUPPORTED;
 }
 
 // bf16 activations, 2 <= m <= 64, k % 64 == 0, 16-byte aligned x.
-int launch_linear_smallm(const rq_weight *wt, const void *x, int64_t m, void *y, int ytype, hipStream_t s) {
+int launch_linear_smallm(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s) {
   if (m < 2 || m > 64 || wt->k % 64 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
   switch (wt->qtype) {
-    case RQ_Q4_K: return run<SmQ4K>(wt, x, m, y, ytype, s);
-    case RQ_Q6_K: return run<SmQ6K>(wt, x, m, y, ytype, s);
-    case RQ_Q8_0: return run<SmQ8>(wt, x, m, y, ytype, s);
-    case RQ_Q5_K: return run<SmQ5K>(wt, x, m, y, ytype, s);
-    case RQ_Q4_0: return run<SmQx0<false>>(wt, x, m, y, ytype, s);
-    case RQ_Q5_0: return run<SmQx0<true>>(wt, x, m, y, ytype, s);
+    case RQ_Q4_K: return run<SmQ4K>(wt, x, m, o, s);
+    case RQ_Q6_K: return run<SmQ6K>(wt, x, m, o, s);
+    case RQ_Q8_0: return run<SmQ8>(wt, x, m, o, s);
+    case RQ_Q5_K: return run<SmQ5K>(wt, x, m, o, s);
+    case RQ_Q4_0: return run<SmQx0<false>>(wt, x, m, o, s);
+    case RQ_Q5_0: return run<SmQx0<true>>(wt, x, m, o, s);
     default: return RQ_E_UNSUPPORTED;
   }
 }

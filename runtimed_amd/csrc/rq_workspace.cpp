@@ -1,0 +1,151 @@
+// rq_workspace.cpp -- per-(device, stream) device memory that outlives a call.
+//
+// The entry points that need scratch (split-K partials of the tiled GEMM, an
+// aligned copy of the activations, FP8 activation codes, embedding ids, the
+// KV quantizer's partial maxima) take it from their stream's workspace
+// instead of allocating per call: a stream-ordered allocation and free
+// around a kernel cost 12-17 us per call on MI355X, more than many of the
+// kernels they serve.
+//
+// Rules (rq_internal.h, WsLease):
+//  * one buffer per (device, stream); hipStreamPerThread is keyed per thread,
+//    since that handle names a different stream on every thread;
+//  * a lease holds the slot's mutex while one entry point enqueues its
+//    launches, so calls from several threads on one stream do not interleave
+//    their use of the buffer (their kernels run in stream order anyway);
+//  * growth allocates a larger buffer in stream order; the old one is freed
+//    in stream order when the lease ends (after every launch of the call that
+//    may still use it), unless a captured graph may refer to it, in which
+//    case it is kept until the process ends;
+//  * under stream capture a large enough buffer is used as it is and marked
+//    as referred to by a graph; a larger need is met by a stream-ordered
+//    allocation and free that become nodes of the graph.
+#include <map>
+#include <mutex>
+#include <thread>
+#include <tuple>
+
+#include "rq_internal.h"
+
+namespace rq {
+
+struct Slot {
+  std::mutex mu;
+  void *ptr = nullptr;
+  size_t bytes = 0;
+  bool graph_ref = false;  // a captured graph may refer to ptr: never free it
+};
+
+namespace {
+
+struct Key {
+  int device;
+  hipStream_t stream;
+  std::thread::id thread;
+  bool operator<(const Key &o) const {
+    return std::tie(device, stream, thread) < std::tie(o.device, o.stream, o.thread);
+  }
+};
+
+std::mutex g_slots_mu;
+
+// Slots live until the process ends (their buffers may be referred to by
+// graphs that outlive any owner here).
+std::map<Key, Slot *> &slots() {
+  static auto *m = new std::map<Key, Slot *>();
+  return *m;
+}
+
+Slot *slot_for(int device, hipStream_t s) {
+  const Key key{device, s, s == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id()};
+  std::lock_guard<std::mutex> g(g_slots_mu);
+  Slot *&p = slots()[key];
+  if (!p) p = new Slot();
+  return p;
+}
+
+constexpr size_t kGrain = 2u << 20;  // buffers grow in 2 MiB steps (at least doubling)
+
+}  // namespace
+
+WsLease::WsLease(int device, hipStream_t s) : device_(device), s_(s) {}
+
+// The slot is taken at the first request, so calls that need no scratch
+// (every decode GEMV) cost nothing here.
+void WsLease::acquire() {
+  slot_ = slot_for(device_, s_);
+  slot_->mu.lock();
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s_, &st) != hipSuccess) {
+    // An error here (the legacy stream while another stream captures in
+    // global mode) means launches would fail too; treat it as capture so
+    // that nothing grows, and let the launch report it.
+    (void)hipGetLastError();
+    capturing_ = true;
+  } else {
+    capturing_ = st == hipStreamCaptureStatusActive;
+  }
+}
+
+WsLease::~WsLease() {
+  for (int i = 0; i < n_async_; ++i) (void)hipFreeAsync(async_[i], s_);
+  if (slot_) slot_->mu.unlock();
+}
+
+void *WsLease::get(size_t bytes, int *rc) {
+  if (!slot_) acquire();
+  bytes = (bytes + 255) & ~(size_t)255;
+  if (bytes == 0) bytes = 256;
+  if (capturing_) {
+    if (slot_->ptr && used_ + bytes <= slot_->bytes) {
+      slot_->graph_ref = true;
+      void *p = static_cast<uint8_t *>(slot_->ptr) + used_;
+      used_ += bytes;
+      return p;
+    }
+    if (n_async_ == 4) {
+      *rc = set_error(RQ_E_NOMEM, "more than four workspace requests in one call");
+      return nullptr;
+    }
+    void *p = nullptr;
+    const hipError_t e = hipMallocAsync(&p, bytes, s_);
+    if (e != hipSuccess) {
+      *rc = set_error(e == hipErrorOutOfMemory ? RQ_E_NOMEM : RQ_E_DEVICE, "workspace of %zu bytes: %s", bytes,
+                      hipGetErrorString(e));
+      return nullptr;
+    }
+    async_[n_async_++] = p;
+    return p;
+  }
+  if (!slot_->ptr || used_ + bytes > slot_->bytes) {
+    size_t want = used_ + bytes > 2 * slot_->bytes ? used_ + bytes : 2 * slot_->bytes;
+    want = (want + kGrain - 1) / kGrain * kGrain;
+    void *p = nullptr;
+    const hipError_t e = hipMallocAsync(&p, want, s_);
+    if (e != hipSuccess) {
+      *rc = set_error(e == hipErrorOutOfMemory ? RQ_E_NOMEM : RQ_E_DEVICE, "workspace of %zu bytes: %s", want,
+                      hipGetErrorString(e));
+      return nullptr;
+    }
+    // The old buffer may still serve launches of this call (earlier
+    // requests) and of earlier calls: freed in stream order at the end of
+    // this lease, or kept if a graph may refer to it.
+    if (slot_->ptr && !slot_->graph_ref) {
+      if (n_async_ == 4) {
+        (void)hipFreeAsync(p, s_);
+        *rc = set_error(RQ_E_NOMEM, "more than four workspace requests in one call");
+        return nullptr;
+      }
+      async_[n_async_++] = slot_->ptr;
+    }
+    slot_->ptr = p;
+    slot_->bytes = want;
+    slot_->graph_ref = false;
+    used_ = 0;
+  }
+  void *p = static_cast<uint8_t *>(slot_->ptr) + used_;
+  used_ += bytes;
+  return p;
+}
+
+}  // namespace rq

@@ -38,6 +38,22 @@ size_t product(const std::vector<size_t> &d) {
   return p;
 }
 
+// A dense F32 / F16 / BF16 tensor as F32 on its device (the to_dtype(F32) of
+// fp8_gemm.rs and fp8_weight.rs:87-91).  16-bit values widen exactly: a
+// zero F32 tensor plus the values through rq_bias_add (0 + b is b).
+Tensor as_f32(const Tensor &t, const char *what) {
+  if (t.dtype() == DType::F32) return t;
+  const int bt = dtype_rq(t.dtype());
+  if (bt != RQ_F16 && bt != RQ_BF16)
+    throw ModelError(ModelError::Config, std::string(what) + ": dtype cannot be read as F32");
+  Tensor out = Tensor::zeros(t.dims(), DType::F32, t.device());
+  if (t.elem_count()) {
+    hip_ok(hipSetDevice(t.device()), "hipSetDevice");
+    rq_ok(rq_bias_add(out.data(), RQ_F32, 1, (int64_t)t.elem_count(), t.data(), bt, nullptr), what);
+  }
+  return out;
+}
+
 // GgmlDtype::block (dtype.rs:49-64)
 bool block_geometry(uint32_t t, size_t *elems, size_t *bytes) {
   switch (t) {
@@ -297,8 +313,25 @@ Tensor QMatMul::forward(const Tensor &x, void *stream) const {
   auto dims = leading(x.dims());
   dims.push_back(n_);
   Tensor y = Tensor::zeros(dims, x.dtype(), device_);
-  rq_ok(rq_linear(w_.get(), x.data(), xt, (int64_t)(x.elem_count() / k_), y.data(), xt, stream), "linear",
-        {k_}, x.dims());
+  rq_ok(rq_linear(w_.get(), x.data(), xt, (int64_t)(x.elem_count() / k_), (int64_t)x.dims().back(), y.data(), xt,
+                  stream),
+        "linear", {k_}, x.dims());
+  return y;
+}
+
+Tensor QMatMul::forward_bias(const Tensor &x, const Tensor &bias, void *stream) const {
+  if (x.dims().empty() || x.dims().back() != k_) throw ModelError::shape("qmatmul", {k_}, x.dims());
+  if (bias.elem_count() != n_) throw ModelError::shape("bias", {n_}, bias.dims());
+  const int xt = dtype_rq(x.dtype()), bt = dtype_rq(bias.dtype());
+  if (xt != RQ_F32 && xt != RQ_F16 && xt != RQ_BF16) throw ModelError(ModelError::Config, "activation dtype not supported");
+  if (bt != RQ_F32 && bt != RQ_F16 && bt != RQ_BF16) throw ModelError(ModelError::Config, "bias dtype not supported");
+  if (bias.device() != device_) throw ModelError(ModelError::Config, "bias on another device");
+  auto dims = leading(x.dims());
+  dims.push_back(n_);
+  Tensor y = Tensor::zeros(dims, x.dtype(), device_);
+  rq_ok(rq_linear_bias(w_.get(), x.data(), xt, (int64_t)(x.elem_count() / k_), (int64_t)x.dims().back(),
+                       bias.data(), bt, y.data(), xt, stream),
+        "linear_bias", {k_}, x.dims());
   return y;
 }
 
@@ -335,12 +368,15 @@ Tensor HipSubstrate::fp8_gemm(const Tensor &x, const Tensor &w, const Tensor *sc
   auto dims = leading(x.dims());
   dims.push_back(n);
   Tensor y = Tensor::zeros(dims, out_dt, w.device());
-  Tensor per_row;
+  Tensor per_row, s32;
   const float *sp = nullptr;
+  // The scale is read as F32 whatever its dtype (fp8_gemm.rs converts it
+  // with to_dtype(F32)).
+  if (scale && (scale->elem_count() == n || scale->elem_count() == 1)) s32 = as_f32(*scale, "fp8_scale");
   if (scale && scale->elem_count() == n) {
-    sp = static_cast<const float *>(scale->data());
+    sp = static_cast<const float *>(s32.data());
   } else if (scale && scale->elem_count() == 1) {  // per-tensor scale (fp8_gemm.rs:128-132)
-    const float s = scale->to_vec<float>().at(0);
+    const float s = s32.to_vec<float>().at(0);
     std::vector<float> v(n, s);
     per_row = Tensor::from_host(v.data(), {n}, DType::F32, w.device());
     sp = static_cast<const float *>(per_row.data());
@@ -426,6 +462,11 @@ Fp8Weight Fp8Weight::create(Tensor weight, Tensor scale, size_t in_dim, size_t o
     throw ModelError::shape("fp8_weight", {out_dim, in_dim}, weight.dims());
   if (scale.dims() != std::vector<size_t>{out_dim} && scale.dims() != std::vector<size_t>{out_dim, 1})
     throw ModelError::shape("fp8_scale", {out_dim}, scale.dims());
+  const int st = dtype_rq(scale.dtype());
+  if (st != RQ_F32 && st != RQ_F16 && st != RQ_BF16)
+    throw ModelError(ModelError::Config, "fp8_scale: dtype cannot be read as F32");
+  // Kept in its own dtype (resident_bytes counts it so, fp8_weight.rs:63-66);
+  // fp8_gemm reads it as F32.
   Fp8Weight f;
   f.weight_ = std::move(weight);
   f.scale_ = std::move(scale);
@@ -510,10 +551,7 @@ size_t Weights::resident_bytes() const {
 
 Tensor Weights::get(const std::string &name) const {
   auto it = map_.find(name);
-  if (it != map_.end()) {
-    if (it->second.dtype() == DType::F32) return it->second;
-    throw ModelError(ModelError::Config, "get: only f32 dense tensors are served here: " + name);
-  }
+  if (it != map_.end()) return as_f32(it->second, "get");  // store.rs:79-86: dense tensors read as F32
   auto q = q_map_.find(name);
   if (q != q_map_.end()) return q->second->dequantize();
   throw ModelError(ModelError::MissingWeight, "missing weight: " + name);
@@ -594,6 +632,23 @@ Tensor Weights::linear(const Tensor &x, const std::string &name) const {
     return substrate_->marlin_gemv(x, MarlinWeight::create(*packed, *scales, x_in, out_dim));
   }
   return linear_dense(x, name);
+}
+
+Tensor Weights::linear_bias(const Tensor &x, const std::string &name, const std::string *bias) const {
+  if (!bias) return linear(x, name);
+  const Tensor b = get(*bias);
+  auto q = q_map_.find(name);
+  if (q != q_map_.end()) return q->second->forward_bias(x, b);
+  // Other paths: the linear, then the bias cast to y's dtype and added.
+  Tensor y = linear(x, name);
+  const size_t n = y.dims().empty() ? 0 : y.dims().back();
+  if (b.elem_count() != n) throw ModelError::shape(*bias, {n}, b.dims());
+  const int bt = dtype_rq(b.dtype()), yt = dtype_rq(y.dtype());
+  if (bt != RQ_F32 && bt != RQ_F16 && bt != RQ_BF16) throw ModelError(ModelError::Config, "bias dtype not supported");
+  hip_ok(hipSetDevice(y.device()), "hipSetDevice");
+  rq_ok(rq_bias_add(y.data(), yt, (int64_t)(n ? y.elem_count() / n : 0), (int64_t)n, b.data(), bt, nullptr),
+        "linear_bias");
+  return y;
 }
 
 Tensor Weights::linear_dense(const Tensor &x, const std::string &name) const {

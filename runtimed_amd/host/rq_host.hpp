@@ -119,6 +119,9 @@ class QMatMul {
  public:
   QMatMul(int qtype, const void *blocks, size_t nbytes, size_t n, size_t k, int device);
   Tensor forward(const Tensor &x, void *stream = nullptr) const;  // y = x W^T
+  // y = x W^T + bias, linear_bias's add in the same launch (bias [n], F32 /
+  // F16 / BF16, cast to y's dtype before the add).
+  Tensor forward_bias(const Tensor &x, const Tensor &bias, void *stream = nullptr) const;
   Tensor dequantize(void *stream = nullptr) const;                // [n, k] f32
   // Rows ids of the dequantized matrix, [ids.size(), k] f32 (QMatMul::embedding).
   Tensor embedding(const std::vector<uint32_t> &ids, void *stream = nullptr) const;
@@ -206,6 +209,9 @@ class Weights {
   static Weights load(const GgufFile &file, int device);
 
   Tensor linear(const Tensor &x, const std::string &name) const;        // linear_layer.rs:45-66
+  // linear_layer.rs:107-118: linear, plus the tensor named *bias (if not
+  // null) cast to y's dtype and broadcast-added; fused for quantized weights.
+  Tensor linear_bias(const Tensor &x, const std::string &name, const std::string *bias) const;
   Tensor linear_dense(const Tensor &x, const std::string &name) const;  // linear_layer.rs:68-105
   Tensor get(const std::string &name) const;                            // store.rs:78-101
   // embed_layer.rs:16-57: rows ids as f32 [1, ids.size(), hidden].

@@ -69,7 +69,10 @@ def lib() -> ctypes.CDLL:
         L.rq_dequant_f32.argtypes = [vp, vp, vp]
         L.rq_dequant_tensor.argtypes = [i32, vp, sz, sz, vp, vp]
         L.rq_embedding.argtypes = [vp, vp, i64, vp, vp]
-        L.rq_linear.argtypes = [vp, vp, i32, i64, vp, i32, vp]
+        L.rq_linear.argtypes = [vp, vp, i32, i64, i64, vp, i32, vp]
+        L.rq_linear_bias.argtypes = [vp, vp, i32, i64, i64, vp, i32, vp, i32, vp]
+        L.rq_linear_multi.argtypes = [i32, vp, vp, i32, i64, i64, vp, i32, vp, i32, vp]
+        L.rq_bias_add.argtypes = [vp, i32, i64, i64, vp, i32, vp]
         L.rq_fp8_quantize.argtypes = [vp, i32, i64, i64, i32, vp, vp, vp]
         L.rq_fp8_gemm.argtypes = [vp, i32, i64, vp, vp, i64, i64, vp, i32, i32, vp]
         L.rq_fp8_gemm_q.argtypes = [vp, vp, i64, vp, vp, i64, i64, vp, i32, vp]
@@ -79,7 +82,8 @@ def lib() -> ctypes.CDLL:
         L.rq_kv_quantize.argtypes = [vp, i32, i64, i64, i64, i32, vp, vp, vp]
         L.rq_kv_dequantize.argtypes = [vp, i32, vp, i64, i64, i64, vp, i32, vp]
         for f in ("rq_weight_create", "rq_weight_info", "rq_dequant_f32", "rq_dequant_tensor",
-                  "rq_linear", "rq_fp8_quantize", "rq_fp8_gemm", "rq_fp8_gemm_q"):
+                  "rq_linear", "rq_linear_bias", "rq_linear_multi", "rq_bias_add", "rq_fp8_quantize",
+                  "rq_fp8_gemm", "rq_fp8_gemm_q"):
             getattr(L, f).restype = i32
         _lib = L
     return _lib
@@ -153,18 +157,52 @@ class QWeight:
         return out
 
     def forward(self, x: torch.Tensor, out_dtype: Optional[torch.dtype] = None,
-                out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """y = x W^T over the last dimension of x (linear_layer.rs:45-52)."""
-        if x.shape[-1] != self.k:
-            raise RqError(-4, f"expected last dim {self.k}, got {list(x.shape)}")
+                out: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """y = x W^T (+ bias) over the last dimension of x (linear_layer.rs:45-52,
+        107-118).  A last dimension other than k raises Shape from the library
+        (linear_layer.rs:88-96)."""
+        k = x.shape[-1] if x.dim() else 0
         if not x.is_contiguous():
             x = x.contiguous()
-        rows = x.numel() // self.k if self.k else 0
+        rows = x.numel() // k if k else 0
         if out is None:
             out = torch.empty((*x.shape[:-1], self.n), dtype=out_dtype or x.dtype, device=x.device)
-        check(lib().rq_linear(self._h, _ptr(x), ftype(x.dtype), rows, _ptr(out), ftype(out.dtype),
-                              _stream(x.device)))
+        if bias is None:
+            check(lib().rq_linear(self._h, _ptr(x), ftype(x.dtype), rows, k, _ptr(out), ftype(out.dtype),
+                                  _stream(x.device)))
+        else:
+            check(lib().rq_linear_bias(self._h, _ptr(x), ftype(x.dtype), rows, k, _ptr(bias), ftype(bias.dtype),
+                                       _ptr(out), ftype(out.dtype), _stream(x.device)))
         return out
+
+
+def linear_multi(weights, x: torch.Tensor, biases=None, out_dtype: Optional[torch.dtype] = None):
+    """Several linears on one input (q/k/v, gate/up: qwen2.rs:99-125) through
+    rq_linear_multi; returns the outputs in order."""
+    k = x.shape[-1]
+    x = x.contiguous()
+    rows = x.numel() // k if k else 0
+    outs = [torch.empty((*x.shape[:-1], w.n), dtype=out_dtype or x.dtype, device=x.device) for w in weights]
+    count = len(weights)
+    hs = (ctypes.c_void_p * count)(*[w.handle.value for w in weights])
+    ys = (ctypes.c_void_p * count)(*[o.data_ptr() for o in outs])
+    btype = F32
+    bs = None
+    if biases is not None:
+        present = [b for b in biases if b is not None]
+        btype = ftype(present[0].dtype) if present else F32
+        bs = (ctypes.c_void_p * count)(*[(b.data_ptr() if b is not None else 0) for b in biases])
+    check(lib().rq_linear_multi(count, hs, _ptr(x), ftype(x.dtype), rows, k, bs, btype, ys,
+                                ftype(outs[0].dtype) if outs else F32, _stream(x.device)))
+    return outs
+
+
+def bias_add(y: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
+    """y += bias over the last dimension, in y's dtype (linear_layer.rs:111-115)."""
+    n = y.shape[-1]
+    check(lib().rq_bias_add(_ptr(y), ftype(y.dtype), y.numel() // n if n else 0, n, _ptr(bias.contiguous()),
+                            ftype(bias.dtype), _stream(y.device)))
+    return y
 
 
 def dequant_tensor(qtype: int, dev_bytes: torch.Tensor, n_elements: int) -> torch.Tensor:

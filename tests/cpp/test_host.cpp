@@ -386,6 +386,45 @@ static void gpu_tests() {
     auto e = expect_throw<ModelError>([&] { weights.linear(bad, "blk.0.attn_q.weight"); });
     CHECK(e.kind == ModelError::Shape);
   });
+  run("linear_bias_quantized_and_fp8", [] {  // linear_layer.rs:107-118
+    // Quantized: the bias (F16, as the CUDA store keeps dense tensors) rides
+    // in the kernel's epilogue; FP8: linear, then the broadcast add.
+    auto blocks = q8_rows({{1, 2, 3}, {4, 5, 6}});
+    const _Float16 bh[2] = {(_Float16)0.5f, (_Float16)-2.0f};
+    std::vector<uint8_t> wb(2 * 32, 0x38);  // e4m3 1.0
+    std::unordered_map<std::string, Tensor> map;
+    map["b"] = Tensor::from_host(bh, {2}, DType::F16, 0);
+    map["f8"] = Tensor::from_host(wb.data(), {2, 32}, DType::F8E4M3, 0);
+    auto w = Weights::from_quantized(0, map, {{"q", std::make_shared<QMatMul>(8, blocks.data(), blocks.size(), 2, 32, 0)}});
+    std::vector<float> xv(64, 0.0f);
+    xv[0] = xv[1] = xv[2] = 1.0f;        // row 0: [6, 15] before the bias
+    xv[32] = 2.0f;                        // row 1: [2, 8]
+    auto x = Tensor::from_host(xv.data(), {2, 32}, DType::F32, 0);
+    const std::string bname = "b";
+    auto yq = w.linear_bias(x, "q", &bname).to_vec<float>();
+    CHECK((yq == std::vector<float>{6.5f, 13.0f, 2.5f, 6.0f}));
+    CHECK((w.linear_bias(x, "q", nullptr).to_vec<float>() == std::vector<float>{6, 15, 2, 8}));
+    auto y8 = w.linear_bias(x, "f8", &bname).to_vec<float>();  // sum of x + bias
+    CHECK((y8 == std::vector<float>{3.5f, 1.0f, 2.5f, 0.0f}));
+    const std::string missing = "nope";
+    auto e = expect_throw<ModelError>([&] { w.linear_bias(x, "q", &missing); });
+    CHECK(e.kind == ModelError::MissingWeight);
+  });
+  run("fp8_scale_bf16_per_row_and_per_tensor", [] {  // fp8_gemm.rs: the scale is read as F32
+    std::vector<uint8_t> wv{0x38, 0x00, 0x00, 0x40};  // [[1, 0], [0, 2]]
+    std::vector<float> xv{1, 2, 3, 4};
+    auto x = Tensor::from_host(xv.data(), {2, 2}, DType::F32, 0);
+    auto w = Tensor::from_host(wv.data(), {2, 2}, DType::F8E4M3, 0);
+    const uint16_t row_bf16[2] = {0x4000, 0x3F00};  // 2.0, 0.5
+    auto s_row = Tensor::from_host(row_bf16, {2}, DType::BF16, 0);
+    CHECK((HipSubstrate().fp8_gemm(x, w, &s_row).to_vec<float>() == std::vector<float>{2, 2, 6, 4}));
+    const uint16_t one_bf16[1] = {0x4040};  // 3.0
+    auto s_one = Tensor::from_host(one_bf16, {1}, DType::BF16, 0);
+    CHECK((HipSubstrate().fp8_gemm(x, w, &s_one).to_vec<float>() == std::vector<float>{3, 12, 9, 24}));
+    auto f = Fp8Weight::create(w, s_row, 2, 2);
+    CHECK(f.resident_bytes() == 4 + 2 * 2);  // the scale keeps its dtype (fp8_weight.rs:63-66)
+    CHECK((f.forward(x, HipSubstrate()).to_vec<float>() == std::vector<float>{2, 2, 6, 4}));
+  });
   run("cuda_fp8_gemm_runs_or_skips", [] {  // fp8_gemm.rs:209-230
     std::vector<uint8_t> xb(16 * 16, 0x38), wb(16 * 16, 0x38);
     std::vector<float> sv(16);

@@ -24,7 +24,7 @@ def test_header_declares_the_boundary():
     for s in ("rq_weight_create", "rq_weight_destroy", "rq_dequant_f32", "rq_dequant_tensor",
               "rq_linear", "rq_fp8_gemm", "rq_fp8_quantize", "rq_last_error", "rq_embedding",
               "rq_marlin_repack", "rq_marlin_dequant", "rq_marlin_linear", "rq_kv_quantize",
-              "rq_kv_dequantize"):
+              "rq_kv_dequantize", "rq_linear_bias", "rq_linear_multi", "rq_bias_add"):
         assert s in syms
 
 
@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert rq.lib().rq_abi_version() == 1
+    assert rq.lib().rq_abi_version() == 2
 
 
 def _create(qtype, data, n, k):
@@ -71,7 +71,18 @@ def test_null_and_enum_checks():
     assert L.rq_weight_info(None, None) == -5
     assert L.rq_dequant_f32(None, None, None) == -5
     assert L.rq_embedding(None, None, 1, None, None) == -5
-    assert L.rq_linear(None, None, 0, 1, None, 0, None) == -5
+    assert L.rq_linear(None, None, 0, 1, 256, None, 0, None) == -5
+    assert L.rq_linear_bias(None, None, 0, 1, 256, None, 0, None, 0, None) == -5
+    # rq_linear_multi: nothing to do, a negative count, null arrays
+    assert L.rq_linear_multi(0, None, None, 0, 1, 256, None, 0, None, 0, None) == 0
+    assert L.rq_linear_multi(-1, None, None, 0, 1, 256, None, 0, None, 0, None) == -5
+    assert L.rq_linear_multi(2, None, None, 0, 1, 256, None, 0, None, 0, None) == -5
+    # rq_bias_add: enum, shape and null checks before any device work
+    assert L.rq_bias_add(None, 99, 1, 4, None, 0, None) == -5
+    assert L.rq_bias_add(None, 0, 1, 4, None, 77, None) == -5
+    assert L.rq_bias_add(None, 0, -1, 4, None, 0, None) == -4
+    assert L.rq_bias_add(None, 0, 0, 4, None, 0, None) == 0
+    assert L.rq_bias_add(None, 0, 2, 4, None, 0, None) == -5
     assert L.rq_fp8_quantize(None, 0, 1, 16, 7, None, None, None) == -5  # bad mode
     assert L.rq_fp8_gemm(None, 99, 1, None, None, 16, 16, None, 0, 1, None) == -5
     assert L.rq_dequant_tensor(3, None, 0, 32, None, None) == -1
