@@ -238,6 +238,22 @@ int rq_fp8_quantize(const void *x, int xtype, int64_t m, int64_t k, int mode, ui
 int rq_fp8_gemm(const void *x, int xtype, int64_t m, const uint8_t *w, const float *w_scale,
                 int64_t n, int64_t k, void *y, int ytype, int mode, void *stream);
 
+/* rq_fp8_gemm that allocates nothing.  NO COUNTERPART IN THE REFERENCE: it
+ * is for callers that cannot allocate device memory -- code under HIP graph
+ * capture that must not record allocations, tight serving loops, harnesses
+ * that forbid hipMalloc.  Same arguments, kernels and results as
+ * rq_fp8_gemm; the activation codes and per-row scales go to a fixed
+ * scratch array of RQ_NOALLOC_SCRATCH_BYTES in the library, one per GPU,
+ * held until the process ends.  Activations that need more
+ * (align256(m * k) + 4 m bytes; 2048 x 4096 needs 8 MiB + 8 KiB) give
+ * RQ_E_ARG and launch nothing; e4m3 activations need no scratch.  Every call
+ * on one GPU shares that GPU's array: calls that overlap on a GPU (other
+ * streams, or replays of a graph holding this call beside eager calls) race
+ * on it. */
+#define RQ_NOALLOC_SCRATCH_BYTES (16u << 20)
+int rq_fp8_gemm_noalloc(const void *x, int xtype, int64_t m, const uint8_t *w, const float *w_scale,
+                        int64_t n, int64_t k, void *y, int ytype, int mode, void *stream);
+
 /* The GEMM proper on codes already encoded by rq_fp8_quantize (xscale may be
  * NULL for all ones). */
 int rq_fp8_gemm_q(const uint8_t *xq, const float *xscale, int64_t m, const uint8_t *w,

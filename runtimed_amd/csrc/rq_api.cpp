@@ -29,6 +29,21 @@ int set_error(int code, const char *fmt, ...) {
 
 hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
 
+void clear_error() { g_last_error.clear(); }
+
+int fp8_gemm_checks(int xtype, int64_t m, int64_t n, int64_t k, int ytype, int mode) {
+  clear_error();
+  if (xtype != RQ_F8E4M3 && xtype != RQ_F32 && xtype != RQ_F16 && xtype != RQ_BF16)
+    return set_error(RQ_E_ARG, "activation type %d not supported", xtype);
+  if (ytype != RQ_F32 && ytype != RQ_F16 && ytype != RQ_BF16)
+    return set_error(RQ_E_ARG, "output type %d not supported", ytype);
+  if (xtype != RQ_F8E4M3 && mode != RQ_FP8_UNSCALED && mode != RQ_FP8_PER_TOKEN)
+    return set_error(RQ_E_ARG, "bad fp8 mode %d", mode);
+  if (m < 0 || n <= 0 || k <= 0)
+    return set_error(RQ_E_SHAPE, "bad shape m=%lld n=%lld k=%lld", (long long)m, (long long)n, (long long)k);
+  return RQ_OK;
+}
+
 bool geometry(int qtype, Geometry *g) {
   switch (qtype) {
     case RQ_Q4_0: *g = {32, 18}; return true;

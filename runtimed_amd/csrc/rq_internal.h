@@ -59,7 +59,10 @@ struct Geometry {
 bool geometry(int qtype, Geometry *g);
 
 int set_error(int code, const char *fmt, ...);
+void clear_error();
 hipStream_t as_stream(void *s);
+// rq_fp8_gemm's argument rules (types, mode, shape); clears the last error.
+int fp8_gemm_checks(int xtype, int64_t m, int64_t n, int64_t k, int ytype, int mode);
 
 // Host-to-device upload of nblocks GGUF blocks into a handle's layout
 // (pinned double-buffered DMA; split layouts scattered on the device).

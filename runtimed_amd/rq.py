@@ -76,6 +76,7 @@ def lib() -> ctypes.CDLL:
         L.rq_fp8_quantize.argtypes = [vp, i32, i64, i64, i32, vp, vp, vp]
         L.rq_fp8_gemm.argtypes = [vp, i32, i64, vp, vp, i64, i64, vp, i32, i32, vp]
         L.rq_fp8_gemm_q.argtypes = [vp, vp, i64, vp, vp, i64, i64, vp, i32, vp]
+        L.rq_fp8_gemm_noalloc.argtypes = [vp, i32, i64, vp, vp, i64, i64, vp, i32, i32, vp]
         L.rq_marlin_repack.argtypes = [vp, i32, vp, i64, i64, vp, vp]
         L.rq_marlin_dequant.argtypes = [vp, vp, i64, i64, vp, vp]
         L.rq_marlin_linear.argtypes = [vp, vp, i64, i64, vp, i32, i64, vp, i32, vp]
@@ -83,7 +84,7 @@ def lib() -> ctypes.CDLL:
         L.rq_kv_dequantize.argtypes = [vp, i32, vp, i64, i64, i64, vp, i32, vp]
         for f in ("rq_weight_create", "rq_weight_info", "rq_dequant_f32", "rq_dequant_tensor",
                   "rq_linear", "rq_linear_bias", "rq_linear_multi", "rq_bias_add", "rq_fp8_quantize",
-                  "rq_fp8_gemm", "rq_fp8_gemm_q"):
+                  "rq_fp8_gemm", "rq_fp8_gemm_q", "rq_fp8_gemm_noalloc"):
             getattr(L, f).restype = i32
         _lib = L
     return _lib
