@@ -154,6 +154,51 @@ def extra_decode_fused(torch, rq, synth, layers, steps, warmup, dev):
             "us_per_layer": round(ms * 1e3 / layers, 2)}
 
 
+def extra_decode_multi(torch, rq, W, steps, warmup, dev):
+    """The headline's 7 GEMVs per layer on the same 128 weight copies, issued
+    as the reference's layer issues them: q/k/v and gate/up each share their
+    input (qwen2.rs:99-125), so each triple / pair is one rq_linear_multi
+    call (one launch, separate weights and outputs), o and down one call
+    each: 4 launches per layer, same bytes."""
+    x896 = torch.from_numpy(synth_act(1, 896)).to(dev)
+    x4864 = torch.from_numpy(synth_act(2, 4864)).to(dev)
+    ys = {name: torch.empty((1, n), dtype=torch.float32, device=dev) for name, n, k in LAYER}
+    sets = [([lw["q"], lw["k"], lw["v"]], [lw["o"]], [lw["gate"], lw["up"]], [lw["down"]]) for lw in W]
+    outs = ([ys["q"], ys["k"], ys["v"]], [ys["o"]], [ys["gate"], ys["up"]], [ys["down"]])
+
+    def token():
+        for layer in sets:
+            for ws, yl, x in zip(layer, outs, (x896, x896, x896, x4864)):
+                rq.linear_multi_into(ws, x, yl)
+
+    g = capture(torch, token)
+    ms = Timer(torch).replay(g, steps, warmup)
+    del g
+    value = layer_bytes() * len(W) / (ms * 1e-3) / 1e9
+    return {"workload": "decode layer set, q/k/v and gate/up through rq_linear_multi (4 launches per layer, "
+                        "same 7 weights and outputs)",
+            "GB/s": round(value, 1), "frac_hbm": round(value / HBM_PEAK_GBS, 4),
+            "us_per_layer": round(ms * 1e3 / len(W), 2)}
+
+
+def synth_act(seed, k):
+    from runtimed_amd import synth
+
+    return synth.activations(seed, 1, k)
+
+
+def host_cpu():
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model, os.cpu_count() or 1
+
+
 def cpu_baseline(oracle, synth, budget_s):
     """Oracle dequant (load time) + f32 GEMV over the dequantized layer."""
     threads = cpu_threads()
@@ -184,8 +229,10 @@ def cpu_baseline(oracle, synth, budget_s):
     per_layer = el / (passes * copies)
     gbs = layer_bytes() / per_layer / 1e9
     w_bytes = sum(n * k // 256 * Q4K_BLOCK for _, n, k in LAYER)
+    model, nproc = host_cpu()
     return {
         "value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "cpu_model": model, "nproc": nproc,
         "sample": f"{passes} passes over {copies} Qwen2-0.5B Q4_K layers (7 f32 GEMVs each on "
                   f"oracle-dequantized weights, blocked OpenMP SGEMV, {threads} threads); "
                   f"{el:.1f} s",
@@ -226,29 +273,39 @@ def extra_large_gemv(torch, rq, synth, dev, steps, warmup):
             "GB/s": round(b / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
-def extra_verify(torch, rq, W, dev, steps, warmup, dtype=None, ms_list=(1, 2, 4, 8, 16, 64)):
+def extra_verify(torch, rq, W, dev, steps, warmup, dtype=None, ms_list=(1, 2, 4, 8, 16, 64), multi=False):
+    """The verify sweep over all layer copies: 7 rq_linear calls per layer,
+    or (multi) q/k/v and gate/up each through one rq_linear_multi call."""
     dt = dtype if dtype is not None else torch.bfloat16
     eb = 4 if dt == torch.float32 else 2
     out = []
     for m in ms_list:
         xs = {k: torch.randn((m, k), device=dev).to(dt) for k in (896, 4864)}
         ys = {name: torch.empty((m, n), dtype=dt, device=dev) for name, n, k in LAYER}
+        groups = (("q", "k", "v"), ("o",), ("gate", "up"), ("down",))
 
         def tok():
             for lw in W:
+                if multi:
+                    for grp in groups:
+                        k = lw[grp[0]].k
+                        rq.linear_multi_into([lw[nm] for nm in grp], xs[k], [ys[nm] for nm in grp])
+                    continue
                 for name, n, k in LAYER:
                     lw[name].forward(xs[k], out=ys[name])
 
         g = capture(torch, tok)
         ms = Timer(torch).replay(g, max(2, steps // 4), 1)
-        b = layer_bytes(eb, eb, m) * len(W)
+        b = layer_bytes(eb, eb, m) * len(W)  # 128 layer copies: >= 1.08 GB a replay
         fl = 2.0 * m * sum(n * k for _, n, k in LAYER) * len(W)
         out.append({"m": m, "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
                     "TFLOP/s": round(fl / (ms * 1e-3) / 1e12, 3),
                     "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
         del g
     name = "bf16" if dt == torch.bfloat16 else "f32 (the reference's compute type)"
-    return {"workload": f"verify sweep, Qwen2-0.5B Q4_K layer, {name} activations", "sweep": out}
+    how = "q/k/v and gate/up through rq_linear_multi (4 launches a layer)" if multi else "7 launches a layer"
+    return {"workload": f"verify sweep, Qwen2-0.5B Q4_K layer, {name} activations, {len(W)} layer copies, {how}",
+            "sweep": out}
 
 
 def extra_prefill(torch, rq, synth, dev, steps, warmup, f32=False):
@@ -312,9 +369,13 @@ def extra_fp8(torch, rq, synth, dev, steps, warmup):
     ms_q = t.replay(gq, steps, warmup)
     gg = capture(torch, gemm)
     ms_g = t.replay(gg, steps, warmup)
-    tf = 2.0 * m * n * k / (ms_g * 1e-3) / 1e12
-    return {"workload": "FP8 e4m3 GEMM 2048x14336x4096, per-token activation scales, bf16 out",
-            "gemm_ms": round(ms_g, 4), "TFLOP/s": round(tf, 1), "frac_mfma_fp8": round(tf / FP8_PEAK_TFLOPS, 4),
+    gb = capture(torch, lambda: rq.fp8_gemm(x, wq, ws, mode=rq.FP8_PER_TOKEN, out=y))
+    ms_b = t.replay(gb, steps, warmup)
+    tf = 2.0 * m * n * k / (ms_b * 1e-3) / 1e12
+    tf_g = 2.0 * m * n * k / (ms_g * 1e-3) / 1e12
+    return {"workload": "FP8 e4m3 GEMM 2048x14336x4096, per-token activation quantize + GEMM, bf16 out",
+            "ms": round(ms_b, 4), "TFLOP/s": round(tf, 1), "frac_mfma_fp8": round(tf / FP8_PEAK_TFLOPS, 4),
+            "gemm_only_ms": round(ms_g, 4), "gemm_only_TFLOP/s": round(tf_g, 1),
             "quantize_ms": round(ms_q, 4)}
 
 
@@ -537,6 +598,29 @@ def mode_prefill_head(torch, rq, synth, dev, steps):
     print(json.dumps({"mode": "prefill-head", "launches": steps}), flush=True)
 
 
+def mode_verify(torch, rq, synth, dev, steps, m, layers=128, xdt="bf16", multi=False):
+    """Only the verify sweep at one M: the 7 GEMMs of `layers` layer copies
+    (q/k/v and gate/up through rq_linear_multi with multi), eager launches
+    (for traces and counters)."""
+    blocks = {name: synth.q4_k_blocks(100 + i, n * k // 256) for i, (name, n, k) in enumerate(LAYER)}
+    W = [{name: rq.QWeight(rq.Q4_K, blocks[name], n, k) for name, n, k in LAYER} for _ in range(layers)]
+    dt = torch.bfloat16 if xdt == "bf16" else torch.float32
+    xs = {k: torch.randn((m, k), device=dev).to(dt) for k in (896, 4864)}
+    ys = {name: torch.empty((m, n), dtype=dt, device=dev) for name, n, k in LAYER}
+    groups = (("q", "k", "v"), ("o",), ("gate", "up"), ("down",))
+    for _ in range(steps):
+        for lw in W:
+            if multi:
+                for grp in groups:
+                    rq.linear_multi_into([lw[nm] for nm in grp], xs[lw[grp[0]].k], [ys[nm] for nm in grp])
+                continue
+            for name, n, k in LAYER:
+                lw[name].forward(xs[k], out=ys[name])
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "verify", "m": m, "multi": multi, "launches": steps * layers * (4 if multi else 7)}),
+          flush=True)
+
+
 def traffic_from_profile():
     p = ROOT / "profiles" / "traffic_q4k_gate_gemv.json"
     if p.exists():
@@ -556,7 +640,10 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
-    ap.add_argument("--mode", choices=["full", "gate", "copy", "fp8", "prefill-head", "gemv-large"], default="full",
+    ap.add_argument("--m", type=int, default=16, help="activation rows of --mode verify")
+    ap.add_argument("--multi", action="store_true", help="--mode verify through rq_linear_multi")
+    ap.add_argument("--mode", choices=["full", "gate", "copy", "fp8", "prefill-head", "gemv-large", "verify"],
+                    default="full",
                     help="gate: only the dominant GEMV; copy: counter calibration copy")
     ap.add_argument("--eager", action="store_true", help="gate mode without a HIP graph")
     args = ap.parse_args()
@@ -582,6 +669,8 @@ def main():
         return mode_prefill_head(torch, rq, synth, dev, args.steps)
     if args.mode == "gemv-large":
         return mode_gemv_large(torch, rq, synth, dev, args.steps)
+    if args.mode == "verify":
+        return mode_verify(torch, rq, synth, dev, args.steps, args.m, multi=args.multi)
     log(f"decode workload: {args.layers} layer copies, steps={args.steps} warmup={args.warmup}")
     W, ms, gate_ms = decode_workload(torch, rq, synth, args.layers, args.steps, args.warmup, dev)
     step_bytes = layer_bytes() * args.layers
@@ -596,8 +685,11 @@ def main():
                                                                                args.warmup, dev)),
                          ("q8_0_gemv", lambda: extra_q8_gemv(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("q4_k_gemv_large", lambda: extra_large_gemv(torch, rq, synth, dev, args.steps, args.warmup)),
-                         ("verify", lambda: extra_verify(torch, rq, W[:32], dev, args.steps, args.warmup)),
-                         ("verify_f32", lambda: extra_verify(torch, rq, W[:32], dev, args.steps, args.warmup,
+                         ("decode_multi", lambda: extra_decode_multi(torch, rq, W, args.steps, args.warmup, dev)),
+                         ("verify", lambda: extra_verify(torch, rq, W, dev, args.steps, args.warmup)),
+                         ("verify_multi", lambda: extra_verify(torch, rq, W, dev, args.steps, args.warmup,
+                                                               multi=True)),
+                         ("verify_f32", lambda: extra_verify(torch, rq, W, dev, args.steps, args.warmup,
                                                              torch.float32, (2, 4, 16, 64))),
                          ("prefill_f32", lambda: extra_prefill(torch, rq, synth, dev, args.steps, args.warmup,
                                                                f32=True)),
@@ -645,6 +737,10 @@ def main():
                    "frac_hbm": round(value / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(gate_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gate_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
+                     "traffic_source": "stored: profiles/traffic_q4k_gate_gemv.json (rocprofv3 --pmc FETCH_SIZE "
+                                       "and WRITE_SIZE runs of bench.py --mode gate --eager, scaled by the same "
+                                       "counters on a 512 MiB copy)",
+                     "timing": "HIP events around graph replays of 128 launches on the replay stream",
                      "kernel": "k_gemv_m1<FmtQ4K,1> (gate/up 4864x896)",
                      "bytes_per_launch": gate_bytes, "us_per_launch": round(gate_ms * 1e3, 3)},
         "cpu_baseline": cpu,

@@ -211,11 +211,15 @@ int rq_linear_bias(const rq_weight *w, const void *x, int xtype, int64_t m, int6
 /* count linears on one activation x [m, k]: ys[i][m, n_i] = x W_i^T
  * (+ biases[i] when biases and biases[i] are not null, all of type btype).
  * Every weight lives on one device and has k inputs (RQ_E_SHAPE
- * otherwise).  At m = 1 and 2, runs of up to 8 consecutive weights of one
+ * otherwise).  At m = 1 and 2, runs of up to 4 consecutive weights of one
  * format whose rows hold at most 64 pieces (k <= 2048 for Q4_K / Q5_K /
- * Q8_0 / Q4_0 / Q5_0, k <= 4096 for Q6_K) take one launch; other weights
- * take the launches rq_linear_bias would make.  Each output equals that
- * call's output bit for bit (the same kernels compute every row). */
+ * Q8_0 / Q4_0 / Q5_0, k <= 4096 for Q6_K) take one launch, and so do bf16 activations
+ * with 3 <= m <= 64 (the small-M matrix-core kernel); other weights
+ * take the launches rq_linear_bias would make.  At m <= 2 each output equals
+ * that call's output bit for bit; with bf16 activations and 3 <= m <= 64
+ * the set may split K over a different number of workgroups than a single
+ * weight would, so sums can differ in their last bits (every result is
+ * deterministic: the same call gives the same bits). */
 int rq_linear_multi(int count, const rq_weight *const *ws, const void *x, int xtype, int64_t m, int64_t k,
                     const void *const *biases, int btype, void *const *ys, int ytype, void *stream);
 

@@ -345,7 +345,7 @@ int rq_linear_multi(int count, const rq_weight *const *wts, const void *x, int x
     int j = i + 1;
     while (j < count && j - i < kMultiMax && wts[j]->qtype == wts[i]->qtype) ++j;
     for (int t = i; t < j; ++t) outs[t - i] = Out{ys[t], biases ? biases[t] : nullptr, ytype, btype};
-    rc = j - i > 1 ? launch_linear_multi(wts + i, j - i, xa, xtype, m, outs, s) : RQ_E_UNSUPPORTED;
+    rc = j - i > 1 ? launch_linear_multi(wts + i, j - i, xa, xtype, m, outs, s, ws) : RQ_E_UNSUPPORTED;
     if (rc == RQ_E_UNSUPPORTED) {
       rc = RQ_OK;
       for (int t = i; t < j && !rc; ++t) rc = linear_one(wts[t], xa, xtype, m, outs[t - i], s, ws);

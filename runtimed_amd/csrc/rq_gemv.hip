@@ -197,41 +197,21 @@ __device__ __forceinline__ void load_piece_x(const void *x, int xtype, const flo
   else load_run<16>(x, xtype, F::run_off(p, r), dst);
 }
 
-// Weights that share one activation block x and one format, in one launch
-// of the segment kernel: entry j covers the row groups [g_end[j - 1],
-// g_end[j]) of the grid (g_end[-1] = 0), its own rows, output and bias.
-struct SegSet {
-  const uint8_t *w[kMultiMax];
-  const uint8_t *aux[kMultiMax];
-  Out o[kMultiMax];
-  int64_t n[kMultiMax];
-  int64_t g_end[kMultiMax];
-  int count;
-};
-
 // M = MR (1 or 2), rows of at most 64 pieces: every lane owns one piece
 // position; its activations (MR rows) are loaded once into registers, and a
 // piece's weights are converted once for the MR dot products.  A row sits on an aligned
 // segment of seg = max(16, next_pow2(P)) lanes (64/seg rows per wave).  The
-// loads of x (XR 16-byte chunks per thread, L2-resident) are issued first
-// and the first row's weight loads right behind them, so x is staged in LDS
-// while the weights are still in flight.  A workgroup walking several row
-// groups issues the next group's loads before it computes the current one.
-// MULTI: the grid covers the row groups of every weight of `set` (one group
-// per workgroup); otherwise entry 0 alone, with set.g_end[0] groups.
-template <class F, int XR, int MR, bool MULTI>
-__global__ __launch_bounds__(256) void k_gemv_m1(const SegSet set, const void *__restrict__ x, int xtype,
-                                                int64_t k, int seg_log2, int rows_per_wg, int mrows) {
-  int j = 0;
-  int64_t g0 = 0;
-  if constexpr (MULTI) {
-    while (j + 1 < set.count && (int64_t)blockIdx.x >= set.g_end[j]) ++j;
-    g0 = j ? set.g_end[j - 1] : 0;
-  }
-  const uint8_t *__restrict__ w = set.w[j];
-  const uint8_t *__restrict__ aux = set.aux[j];
-  const Out o = set.o[j];
-  const int64_t n = set.n[j], groups = set.g_end[j] - g0;
+// loads of x (XR 16-byte chunks per thread, L2-resident) are issued first,
+// then the bias of the lane's row, and the first row's weight loads right
+// behind them, so x is staged in LDS while the weights are still in flight.
+// A workgroup walking several row groups (g0 + blockIdx.x, + gridDim.x, ...
+// up to groups) issues the next group's loads before it computes the
+// current one.
+template <class F, int XR, int MR>
+__device__ __forceinline__ void gemv_seg(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
+                                         const void *__restrict__ x, int xtype, const Out &o, int64_t n, int64_t k,
+                                         int seg_log2, int rows_per_wg, int64_t g, int64_t groups, int mrows,
+                                         bool one_group) {
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int P = (int)(k / F::PE);
   const int row_in_wg = wv * (64 >> seg_log2) + (lane >> seg_log2);
@@ -242,12 +222,7 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const SegSet set, const void *_
   // (the prefetched row too) before the next use.  Dead lanes and rows past
   // n contribute nothing (the dot product is selected away).
   const int pl = live ? p : P - 1;
-  int64_t g = (int64_t)blockIdx.x - g0;
   int64_t row = g * rows_per_wg + row_in_wg;
-  // The bias of this lane's row, loaded ahead of x and the weights (a
-  // uniform branch; every later wait for x covers it).
-  float bv = 0.0f;
-  if (o.bias) bv = load_as_f32(o.bias, o.btype, row < n ? row : n - 1);
   extern __shared__ __attribute__((aligned(16))) float xs_dyn[];
   // MR activation rows (x is [MR][k], contiguous) as one run of chunks; row
   // i of the LDS copy starts at i * xstride.
@@ -256,6 +231,9 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const SegSet set, const void *_
   // mrows <= MR rows of x exist; loads clamp to them, and rows mrows .. MR - 1
   // of the LDS copy are neither written nor their results stored.
   load_x_chunks<XR>(x, xtype, mrows * (int)k, xc);
+  // The bias's bits (a uniform branch) behind x: a wait for x covers them.
+  uint32_t bv = 0;
+  if (o.bias) bv = bias_bits(o.bias, o.btype, row < n ? row : n - 1);
   __builtin_amdgcn_sched_barrier(0);
   typename F::Piece cur = F::load(w, aux, row < n ? row : n - 1, k, pl);
   __builtin_amdgcn_sched_barrier(0);
@@ -279,7 +257,7 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const SegSet set, const void *_
     }
 
   // Dot products, segment totals and stores of one row group.
-  auto emit = [&](const typename F::Piece &pc, int64_t r, float b) {
+  auto emit = [&](const typename F::Piece &pc, int64_t r, uint32_t b) {
     float dr[MR];
     if constexpr (MR > 1 && has_dot_rows<F>::value) {
       F::template dot_rows<MR>(pc, xv, sx, dr);
@@ -293,14 +271,14 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const SegSet set, const void *_
       float acc = (live && r < n) ? d : 0.0f;
       const int seg = 1 << seg_log2;
       acc = seg_sum(acc, seg);
-      if (o.bias) acc = with_bias(acc, b, o.ytype);
+      if (o.bias) acc = with_bias(acc, bias_bits_f32(b, o.btype), o.ytype);
       if ((lane & (seg - 1)) == seg - 1 && r < n && i < mrows) store_out(o.y, o.ytype, i * n + r, acc);
     }
   };
   // One row group per workgroup (every decode-sized matrix): no prefetch.
   // A next-row load in the last pass is never used, and the wave still has
   // to wait for it before it can end.
-  if (MULTI || groups <= (int64_t)gridDim.x) {
+  if (one_group) {
     emit(cur, row, bv);
     return;
   }
@@ -311,8 +289,29 @@ __global__ __launch_bounds__(256) void k_gemv_m1(const SegSet set, const void *_
     emit(cur, row, bv);
     cur = nxt;
     row = row_n;
-    if (o.bias) bv = load_as_f32(o.bias, o.btype, row < n ? row : n - 1);
+    if (o.bias) bv = bias_bits(o.bias, o.btype, row < n ? row : n - 1);
   }
+}
+
+// One weight: groups row groups over the grid.
+template <class F, int XR, int MR>
+__global__ __launch_bounds__(256) void k_gemv_m1(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
+                                                const void *__restrict__ x, int xtype, const Out o, int64_t n,
+                                                int64_t k, int seg_log2, int rows_per_wg, int64_t groups,
+                                                int mrows) {
+  gemv_seg<F, XR, MR>(w, aux, x, xtype, o, n, k, seg_log2, rows_per_wg, blockIdx.x, groups, mrows,
+                      groups <= (int64_t)gridDim.x);
+}
+
+// A set of weights sharing x: one row group per workgroup, the grid covering
+// every weight's groups (pick_entry chooses this workgroup's weight).
+template <class F, int XR, int MR>
+__global__ __launch_bounds__(256) void k_gemv_set(const WeightSet set, const void *__restrict__ x, int xtype,
+                                                 int64_t k, int seg_log2, int rows_per_wg, int mrows) {
+  const int bid = (int)blockIdx.x;
+  const SetEntry e = pick_entry(set, bid);
+  gemv_seg<F, XR, MR>(e.w, e.aux, x, xtype, e.o, e.n, k, seg_log2, rows_per_wg, bid - e.g0, e.g1 - e.g0, mrows,
+                      true);
 }
 
 // M = 1, long rows (P > 64 pieces): one wave per row, PPL pieces per lane
@@ -660,44 +659,37 @@ SegGeo seg_geo(int P) {
   return {l, 4 * (64 >> l)};
 }
 
-// The segment kernel on a set of weights (x 16-byte aligned; k <= 64 pieces
-// always fits the LDS copy of x).  Chunks of x per thread: at most
-// MR 64 PE / 4 / 256 = 4 MR.
-template <class F, int MR, bool MULTI>
-int launch_seg(const SegSet &set, int64_t k, unsigned blocks, const void *x, int xtype, int mrows, hipStream_t s) {
-  const SegGeo geo = seg_geo((int)(k / F::PE));
-  const size_t xb = MR * xlds_bytes(k);
+// The segment kernel (x 16-byte aligned; k <= 64 pieces always fits the LDS
+// copy of x).  Chunks of x per thread: at most MR 64 PE / 4 / 256 = 4 MR.
+template <class F, int MR>
+int xr_for(int64_t k, int xtype, int mrows) {
   const int per = (x_chunks(mrows * k, xtype) + 255) / 256;
-#define RQ_M1(XR)                                                                                           \
-  hipLaunchKernelGGL((k_gemv_m1<F, XR, MR, MULTI>), dim3(blocks), dim3(256), xb, s, set, x, xtype, k,       \
-                     geo.seg_log2, geo.rows_per_wg, mrows)
-  if (per <= 1) {
-    RQ_M1(1);
-  } else if (per <= 2) {
-    RQ_M1(2);
-  } else if constexpr (MR == 1) {
-    RQ_M1(4);
-  } else {  // two rows, or four slots of two-run formats: k <= 2048, at most 8 chunks a thread
-    if (per <= 4) RQ_M1(4);
-    else RQ_M1(8);
-  }
-#undef RQ_M1
-  return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
+  if (per <= 1) return 1;
+  if (per <= 2) return 2;
+  if (MR == 1 || per <= 4) return 4;
+  return 8;  // two rows, or four slots of two-run formats: k <= 2048, at most 8 chunks a thread
 }
+
+#define RQ_SEG_DISPATCH(KERN, XRV, ...)                      \
+  switch (XRV) {                                              \
+    case 1: hipLaunchKernelGGL((KERN<F, 1, MR>), __VA_ARGS__); break; \
+    case 2: hipLaunchKernelGGL((KERN<F, 2, MR>), __VA_ARGS__); break; \
+    case 4: hipLaunchKernelGGL((KERN<F, 4, MR>), __VA_ARGS__); break; \
+    default:                                                  \
+      if constexpr (MR > 1) hipLaunchKernelGGL((KERN<F, 8, MR>), __VA_ARGS__); \
+      break;                                                  \
+  }
 
 // Rows of at most 64 pieces, MR activation rows: the segment kernel.
 template <class F, int MR>
 int run_seg(const rq_weight *wt, const void *x, int xtype, const Out &o, hipStream_t s, int mrows = MR) {
   const SegGeo geo = seg_geo((int)(wt->k / F::PE));
-  SegSet set{};
-  set.w[0] = wt->data;
-  set.aux[0] = wt->data + wt->aux_off;
-  set.o[0] = o;
-  set.n[0] = wt->n;
-  set.g_end[0] = (wt->n + geo.rows_per_wg - 1) / geo.rows_per_wg;
-  set.count = 1;
-  const unsigned blocks = (unsigned)(set.g_end[0] < 16384 ? set.g_end[0] : 16384);
-  return launch_seg<F, MR, false>(set, wt->k, blocks, x, xtype, mrows, s);
+  const int64_t groups = (wt->n + geo.rows_per_wg - 1) / geo.rows_per_wg;
+  const unsigned blocks = (unsigned)(groups < 16384 ? groups : 16384);
+  const size_t xb = MR * xlds_bytes(wt->k);
+  RQ_SEG_DISPATCH(k_gemv_m1, (xr_for<F, MR>(wt->k, xtype, mrows)), dim3(blocks), dim3(256), xb, s, wt->data,
+                  wt->data + wt->aux_off, x, xtype, o, wt->n, wt->k, geo.seg_log2, geo.rows_per_wg, groups, mrows)
+  return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }
 
 template <class F>
@@ -749,7 +741,8 @@ int dispatch_fmt(const rq_weight *wt, const void *x, int xtype, int64_t m, const
 }
 
 // Several weights of format F sharing x (equal k, rows of at most 64
-// pieces, M = 1 or 2): the row groups of all of them in one grid.
+// pieces, M = 1 or 2, one output and bias type): the row groups of all of
+// them in one grid.
 template <class F>
 int run_seg_set(const rq_weight *const *w, int count, const void *x, int xtype, int64_t m, const Out *o,
                 hipStream_t s) {
@@ -758,20 +751,23 @@ int run_seg_set(const rq_weight *const *w, int count, const void *x, int xtype, 
   const int P = (int)(k / F::PE);
   if (P > 64 || (m == 2 && k % 8 != 0)) return RQ_E_UNSUPPORTED;
   const SegGeo geo = seg_geo(P);
-  SegSet set{};
+  WeightSet set;
   int64_t total = 0;
-  for (int j = 0; j < count; ++j) {
-    set.w[j] = w[j]->data;
-    set.aux[j] = w[j]->data + w[j]->aux_off;
-    set.o[j] = o[j];
-    set.n[j] = w[j]->n;
-    total += (w[j]->n + geo.rows_per_wg - 1) / geo.rows_per_wg;
-    set.g_end[j] = total;
+  const int rc = fill_set(set, w, count, o, [&](const rq_weight *wj) {
+    return (wj->n + geo.rows_per_wg - 1) / geo.rows_per_wg;
+  }, &total);
+  if (rc) return rc;
+  const size_t xb = (m == 1 ? 1 : 2) * xlds_bytes(k);
+  if (m == 1) {
+    constexpr int MR = 1;
+    RQ_SEG_DISPATCH(k_gemv_set, (xr_for<F, 1>(k, xtype, 1)), dim3((unsigned)total), dim3(256), xb, s, set, x, xtype,
+                    k, geo.seg_log2, geo.rows_per_wg, 1)
+  } else {
+    constexpr int MR = 2;
+    RQ_SEG_DISPATCH(k_gemv_set, (xr_for<F, 2>(k, xtype, 2)), dim3((unsigned)total), dim3(256), xb, s, set, x, xtype,
+                    k, geo.seg_log2, geo.rows_per_wg, 2)
   }
-  set.count = count;
-  if (total > 0x7FFFFFFF) return RQ_E_UNSUPPORTED;
-  if (m == 1) return launch_seg<F, 1, true>(set, k, (unsigned)total, x, xtype, 1, s);
-  return launch_seg<F, 2, true>(set, k, (unsigned)total, x, xtype, 2, s);
+  return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }
 
 }  // namespace
@@ -795,7 +791,7 @@ int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m
                             (wt->qtype == RQ_Q4_K || wt->qtype == RQ_Q6_K || wt->qtype == RQ_Q8_0 ||
                              wt->qtype == RQ_Q5_K || wt->qtype == RQ_Q4_0 || wt->qtype == RQ_Q5_0);
   if (m > 1 && xtype == RQ_BF16 && !two_rows_seg) {
-    int rc = m <= 64 ? launch_linear_smallm(wt, x, m, o, s) : RQ_E_UNSUPPORTED;
+    int rc = m <= 64 ? launch_linear_smallm(wt, x, m, o, s, &ws) : RQ_E_UNSUPPORTED;
     if (rc == RQ_E_UNSUPPORTED) rc = launch_linear_mfma(wt, x, m, o, s, ws);
     if (rc != RQ_E_UNSUPPORTED) return rc;
   }
@@ -856,13 +852,18 @@ int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m
 }
 
 int launch_linear_multi(const rq_weight *const *w, int count, const void *x, int xtype, int64_t m, const Out *o,
-                        hipStream_t s) {
-  if (count < 1 || count > kMultiMax || (m != 1 && m != 2)) return RQ_E_UNSUPPORTED;
+                        hipStream_t s, WsLease &ws) {
+  if (count < 1 || count > kMultiMax || m < 1) return RQ_E_UNSUPPORTED;
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
   const int qt = w[0]->qtype;
   const int64_t k = w[0]->k;
   for (int j = 1; j < count; ++j)
     if (w[j]->qtype != qt || w[j]->k != k) return RQ_E_UNSUPPORTED;
+  // bf16 activations beyond two rows: the small-M matrix-core kernel, as
+  // rq_linear takes them (two rows stay on the segment kernel below, or go
+  // one by one where rq_linear gives them other layouts).
+  if (xtype == RQ_BF16 && m >= 3 && m <= 64) return launch_linear_smallm_set(w, count, x, m, o, s, &ws);
+  if (m != 1 && m != 2) return RQ_E_UNSUPPORTED;
   switch (qt) {
     case RQ_Q4_K: return k % 64 ? RQ_E_UNSUPPORTED : run_seg_set<FmtQ4K>(w, count, x, xtype, m, o, s);
     case RQ_Q6_K: return k % 128 ? RQ_E_UNSUPPORTED : run_seg_set<FmtQ6K>(w, count, x, xtype, m, o, s);

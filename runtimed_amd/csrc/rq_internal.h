@@ -81,6 +81,111 @@ struct Out {
   int btype;
 };
 
+// ---- several weights in one launch ----
+//
+// Weights that share one activation block x, and one output and bias type:
+// entry j covers the workgroups [g_end[j - 1], g_end[j]) of the grid
+// (g_end[-1] = 0; entries past count hold g_end = INT32_MAX), with its own
+// rows, output and bias.  Kept small: a kernel's arguments are fetched
+// before anything else can start.
+constexpr int kMultiMax = 4;
+struct WeightSet {
+  const uint8_t *w[kMultiMax];
+  void *y[kMultiMax];
+  const void *bias[kMultiMax];
+  uint32_t aux_off[kMultiMax];
+  int32_t n[kMultiMax];
+  int32_t g_end[kMultiMax];
+  int count, ytype, btype;
+};
+
+// The entry of workgroup bid: its weight, aux array, output, rows and first
+// and end workgroup.  Every table value is pinned in a scalar register first
+// (an empty asm that takes them all), so the selects work on registers:
+// left alone, the compiler selects an address into the table and loads
+// through it, one more dependent round of argument fetches before any load
+// can be issued.  The selected pointers go back through the global address
+// space so that accesses through them stay global (not flat) instructions.
+struct SetEntry {
+  const uint8_t *w, *aux;
+  Out o;
+  int n, g0, g1;
+};
+__device__ __forceinline__ SetEntry pick_entry(const WeightSet &set, int bid) {
+  static_assert(kMultiMax == 4, "one asm statement pins the four entries");
+  uint64_t tw[4], ty[4], tb[4];
+  uint32_t ta[4];
+  int tn[4], te[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    tw[t] = reinterpret_cast<uint64_t>(set.w[t]);
+    ty[t] = reinterpret_cast<uint64_t>(set.y[t]);
+    tb[t] = reinterpret_cast<uint64_t>(set.bias[t]);
+    ta[t] = set.aux_off[t];
+    tn[t] = set.n[t];
+    te[t] = set.g_end[t];
+  }
+  asm volatile("" : "+s"(tw[0]), "+s"(tw[1]), "+s"(tw[2]), "+s"(tw[3]), "+s"(ty[0]), "+s"(ty[1]), "+s"(ty[2]),
+               "+s"(ty[3]), "+s"(tb[0]), "+s"(tb[1]), "+s"(tb[2]), "+s"(tb[3]), "+s"(ta[0]), "+s"(ta[1]),
+               "+s"(ta[2]), "+s"(ta[3]), "+s"(tn[0]), "+s"(tn[1]), "+s"(tn[2]), "+s"(tn[3]), "+s"(te[0]),
+               "+s"(te[1]), "+s"(te[2]), "+s"(te[3]));
+  uint64_t w = tw[0], y = ty[0], bias = tb[0];
+  uint32_t aux_off = ta[0];
+  int n = tn[0], g0 = 0, g1 = te[0];
+#pragma unroll
+  for (int t = 1; t < 4; ++t) {
+    const bool here = bid >= te[t - 1];
+    w = here ? tw[t] : w;
+    y = here ? ty[t] : y;
+    bias = here ? tb[t] : bias;
+    aux_off = here ? ta[t] : aux_off;
+    n = here ? tn[t] : n;
+    g0 = here ? te[t - 1] : g0;
+    g1 = here ? te[t] : g1;
+  }
+  typedef __attribute__((address_space(1))) uint8_t gbyte;
+  SetEntry e;
+  e.w = (const uint8_t *)(const gbyte *)w;
+  e.aux = e.w + aux_off;
+  e.o = Out{(void *)(gbyte *)y, (const void *)(const gbyte *)bias, set.ytype, set.btype};
+  e.n = n;
+  e.g0 = g0;
+  e.g1 = g1;
+  return e;
+}
+
+// Fills a WeightSet for count weights (workgroups per weight from wg_of),
+// or returns RQ_E_UNSUPPORTED (shapes beyond 32-bit fields, or outputs of
+// different types).
+template <class WG>
+__host__ int fill_set(WeightSet &set, const rq_weight *const *w, int count, const Out *o, WG &&wg_of,
+                      int64_t *total_out) {
+  set = WeightSet{};
+  int64_t total = 0;
+  bool have_bias = false;
+  for (int j = 0; j < count; ++j) {
+    if (w[j]->aux_off > 0xFFFFFFFFull || w[j]->n > 0x7FFFFFFF) return RQ_E_UNSUPPORTED;
+    if (o[j].ytype != o[0].ytype || (o[j].bias && have_bias && o[j].btype != set.btype)) return RQ_E_UNSUPPORTED;
+    set.w[j] = w[j]->data;
+    set.aux_off[j] = (uint32_t)w[j]->aux_off;
+    set.y[j] = o[j].y;
+    set.bias[j] = o[j].bias;
+    set.n[j] = (int32_t)w[j]->n;
+    total += wg_of(w[j]);
+    if (total > 0x7FFFFFFF) return RQ_E_UNSUPPORTED;
+    set.g_end[j] = (int32_t)total;
+    if (o[j].bias) {
+      set.btype = o[j].btype;
+      have_bias = true;
+    }
+  }
+  for (int j = count; j < kMultiMax; ++j) set.g_end[j] = 0x7FFFFFFF;
+  set.count = count;
+  set.ytype = o[0].ytype;
+  *total_out = total;
+  return RQ_OK;
+}
+
 // ---- workspace: device memory that outlives a call ----
 //
 // One buffer per (device, stream), grown on demand and reused by every later
@@ -103,6 +208,12 @@ class WsLease {
   // *rc set (and the error message) on failure.  Earlier pointers of the same
   // lease stay valid.
   void *get(size_t bytes, int *rc);
+  // kCounters u32 of the slot that are zero between calls: a kernel that
+  // counts in them must leave them zero when it ends.  Made (and zeroed)
+  // on the first request outside stream capture; null under capture before
+  // that, or on failure (the caller then takes a path without counters).
+  static constexpr int kCounters = 8192;
+  uint32_t *counters();
 
  private:
   void acquire();
@@ -128,17 +239,23 @@ int launch_dequant_raw(int qtype, const uint8_t *src, uint64_t nblocks, float *o
 int launch_linear_fused(const rq_weight *w, const void *x, int xtype, int64_t m, const Out &o, hipStream_t s,
                         WsLease &ws);
 // One launch for several weights of one format sharing x (count <= kMultiMax,
-// equal k): M = 1 and M = 2 on the segment layout.  RQ_E_UNSUPPORTED when
-// the shapes take another layout (the caller then launches them one by one).
-constexpr int kMultiMax = 8;
+// equal k, one output type): M = 1 and M = 2 on the segment layout, bf16
+// activations with 3 <= M <= 64 on the small-M matrix-core kernel.
+// RQ_E_UNSUPPORTED when the shapes take another path (the caller then
+// launches them one by one).
 int launch_linear_multi(const rq_weight *const *w, int count, const void *x, int xtype, int64_t m, const Out *o,
-                        hipStream_t s);
+                        hipStream_t s, WsLease &ws);
 // MFMA GEMM for bf16 activations and m > 1 (RQ_E_UNSUPPORTED if the shape or
 // format has no tiled kernel).
 int launch_linear_mfma(const rq_weight *w, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease &ws);
 // Matrix-core kernel for bf16 activations and 2 <= m <= 64 (speculative
 // verify), RQ_E_UNSUPPORTED outside that or for formats it has no decoder for.
-int launch_linear_smallm(const rq_weight *w, const void *x, int64_t m, const Out &o, hipStream_t s);
+// With a workspace (ws not null), few row tiles split K over several
+// workgroups (partials and counters in the workspace).
+int launch_linear_smallm(const rq_weight *w, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease *ws);
+// The same kernel on a set of weights sharing x (equal k).
+int launch_linear_smallm_set(const rq_weight *const *w, int count, const void *x, int64_t m, const Out *o,
+                             hipStream_t s, WsLease *ws);
 // The same for f32 / f16 activations on the f32 matrix cores with exact f32
 // weights (f32 accumulation).
 int launch_linear_smallm_f32(const rq_weight *wt, const void *x, int xtype, int64_t m, const Out &o,
@@ -225,6 +342,16 @@ __device__ __forceinline__ float round_as(int ytype, float v) {
   const float b = bf16_bits_to_f32(f32_to_bf16_bits(v));
   const float h = (float)(_Float16)v;
   return ytype == RQ_F32 ? v : (ytype == RQ_BF16 ? b : h);
+}
+
+// The raw bits of bias element i (a uniform branch on the type, no
+// conversion: a value converted right after its load would wait for it
+// there) and their f32 value.
+__device__ __forceinline__ uint32_t bias_bits(const void *b, int btype, int64_t i) {
+  return btype == RQ_F32 ? static_cast<const uint32_t *>(b)[i] : (uint32_t) static_cast<const uint16_t *>(b)[i];
+}
+__device__ __forceinline__ float bias_bits_f32(uint32_t v, int btype) {
+  return btype == RQ_F32 ? __uint_as_float(v) : (btype == RQ_BF16 ? __uint_as_float(v << 16) : f16_bits_to_f32(v));
 }
 
 // Bias of output column col as f32 (0 without a bias).

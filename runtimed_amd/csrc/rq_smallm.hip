@@ -22,6 +22,8 @@
 // summed through LDS.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "rq_epilogue.h"
 #include "rq_formats.h"
 #include "rq_internal.h"
@@ -31,6 +33,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float float2v __attribute__((ext_vector_type(2)));
 
 // The 16 weights of lane group g in chunk t of `row` as bf16 pairs:
 // o[0..3] = chunk elements 8g .. 8g+7, o[4..7] = 32 + 8g .. 32 + 8g + 7.
@@ -38,6 +41,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // Q4_K (dequant_k.rs:19-44): elements j and 32 + j of chunk c are the low
 // and high nibbles of qs[32c + j].
 struct SmQ4K {
+  static constexpr int CE = 64;  // elements of a row per chunk
   struct Chunk {
     uint4 hd;
     uint2 q;
@@ -77,6 +81,7 @@ struct SmQ4K {
 // y[l + 64ch + 32], nibble ch of ql[l + 32] | bits 4ch + 2.. of qh[l];
 // scales sc[l / 16 + 4ch] and sc[l / 16 + 4ch + 2].
 struct SmQ6K {
+  static constexpr int CE = 64;  // elements of a row per chunk
   struct Chunk {
     uint2 a, b, h;
     uint32_t sc, d;
@@ -123,6 +128,7 @@ struct SmQ6K {
 // Q8_0 (dequant.rs:40-47) on the split layout (int8 quants in element
 // order, f16 d per 32): the chunk's two blocks are its two runs.
 struct SmQ8 {
+  static constexpr int CE = 64;  // elements of a row per chunk
   struct Chunk {
     uint2 a, b;
     uint32_t d;
@@ -151,6 +157,7 @@ struct SmQ8 {
 
 // Q5_K (dequant_k.rs:51-80): as Q4_K, plus bit 2c / 2c + 1 of qh[j] -> 16.
 struct SmQ5K {
+  static constexpr int CE = 64;  // elements of a row per chunk
   struct Chunk {
     uint4 hd;
     uint2 q, h;
@@ -193,6 +200,7 @@ struct SmQ5K {
 // 8g .. 8g + 7 of qh.
 template <bool Q5>
 struct SmQx0 {
+  static constexpr int CE = 64;  // elements of a row per chunk
   struct Chunk {
     uint2 a, b;
     uint32_t ha, hb, da, db;
@@ -274,6 +282,67 @@ __device__ __forceinline__ void load_x(XFrag<MT> &f, const uint16_t *const (&xr)
   }
 }
 
+// Q4_K with half super-blocks as chunks (rows of k % 128 == 0): lane group
+// g takes GEMV piece 4h + g of half h -- 16 contiguous qs bytes, the low and
+// high nibbles of chunk 2h + g / 2 at positions 16 (g % 2) .. + 16 -- so
+// the four lanes of a row read 64 contiguous bytes per load (against 32 in
+// 8-byte pieces for the 64-element chunk), and the scales decoded once serve
+// 32 weights.  Four MFMAs per column tile: low nibbles 0..7, 8..15, high
+// nibbles 0..7, 8..15 of the lane's bytes, with the activations at the same
+// positions (element 64 (g / 2) + 16 (g % 2) + 32 r + 8 j of the chunk).
+struct SmQ4KH {
+  static constexpr int CE = 128;
+  typedef FmtQ4K::Piece Chunk;
+  __device__ static Chunk load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int64_t t, int g) {
+    // pieces are counted from the half's first element: piece g is chunk
+    // 2h + g / 2, bytes 16 (g % 2) .. + 16 of its qs
+    return FmtQ4K::load_e(w, aux, (uint64_t)row * (uint64_t)k + 128u * (uint64_t)t, g);
+  }
+  __device__ static int xoff(int g) { return 64 * (g >> 1) + 16 * (g & 1); }
+};
+
+template <int MT>
+struct XFragH {
+  u32x4 v[MT][4];  // [ct][low 0..7, low 8..15, high 0..7, high 8..15]
+};
+
+template <int MT>
+__device__ __forceinline__ void load_xh(XFragH<MT> &f, const uint16_t *const (&xr)[MT], int64_t t) {
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) {
+    const uint16_t *p = xr[ct] + 128 * t;
+    f.v[ct][0] = *reinterpret_cast<const u32x4 *>(p);
+    f.v[ct][1] = *reinterpret_cast<const u32x4 *>(p + 8);
+    f.v[ct][2] = *reinterpret_cast<const u32x4 *>(p + 32);
+    f.v[ct][3] = *reinterpret_cast<const u32x4 *>(p + 40);
+  }
+}
+
+template <int MT>
+__device__ __forceinline__ void mma_chunk_h(const FmtQ4K::Piece &pc, const XFragH<MT> &xf, f32x4 (&acc)[MT],
+                                            uint32_t vm) {
+  float a0, b0, a1, b1;
+  FmtQ4K::scales(pc, a0, b0, a1, b1);
+  const uint32_t q[4] = {pc.qv.x, pc.qv.y, pc.qv.z, pc.qv.w};
+  uint32_t lo[8], hi[8];  // bf16 pairs: positions 2i, 2i + 1
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t l = q[j] & 0x0F0F0F0Fu, h = (q[j] >> 4) & 0x0F0F0F0Fu;
+    lo[2 * j] = pk_bf16(fmaf(ub(l, 0), a0, -b0), fmaf(ub(l, 1), a0, -b0)) & vm;
+    lo[2 * j + 1] = pk_bf16(fmaf(ub(l, 2), a0, -b0), fmaf(ub(l, 3), a0, -b0)) & vm;
+    hi[2 * j] = pk_bf16(fmaf(ub(h, 0), a1, -b1), fmaf(ub(h, 1), a1, -b1)) & vm;
+    hi[2 * j + 1] = pk_bf16(fmaf(ub(h, 2), a1, -b1), fmaf(ub(h, 3), a1, -b1)) & vm;
+  }
+  const bf16x8 f[4] = {pick(lo[0], lo[1], lo[2], lo[3]), pick(lo[4], lo[5], lo[6], lo[7]),
+                       pick(hi[0], hi[1], hi[2], hi[3]), pick(hi[4], hi[5], hi[6], hi[7])};
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int ct = 0; ct < MT; ++ct)
+      acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f[j], __builtin_bit_cast(bf16x8, xf.v[ct][j]), acc[ct], 0, 0,
+                                                        0);
+}
+
 // Decode chunk c into A fragments and multiply with the activation
 // fragments; vm (all ones or zero) masks the decoded weights, so a masked
 // chunk adds exact zeros.
@@ -297,48 +366,125 @@ __device__ __forceinline__ void mma_chunk(const typename C::Chunk &c, const XFra
                                                       acc[ct], 0, 0, 0);
 }
 
-// The NW waves' partial 16 x (16 MT) tiles summed through LDS and stored.
-// 16 x 16 C layout: lane l holds column (activation row) l % 16 and weight
-// rows 4 (l / 16) + i.  Thread t sums one lane slot of one column tile.
-template <int MT, int NW>
-__device__ __forceinline__ void reduce_store(f32x4 (&part)[NW][MT][64], const f32x4 (&acc)[MT], int wave, int lane,
-                                             int64_t m, int64_t n, int64_t n0, const Out &o) {
+// Lane slot l of the (row tile rt, column tile ct) output tile: activation
+// row 16 ct + l % 16, weight rows n0 + 16 rt + 4 (l / 16) + i.
+template <int MT>
+__device__ __forceinline__ void store_slot(const f32x4 &v, int rt, int ct, int l, int64_t m, int64_t n, int64_t n0,
+                                           const Out &o) {
+  const int64_t mr = 16 * ct + (l & 15);
+  if (mr < m) {
 #pragma unroll
-  for (int ct = 0; ct < MT; ++ct) part[wave][ct][lane] = acc[ct];
-  __syncthreads();
-  for (int slot = threadIdx.x; slot < MT * 64; slot += 64 * NW) {
-    const int ct = slot >> 6, l = slot & 63;
-    f32x4 v = part[0][ct][l];
-#pragma unroll
-    for (int q = 1; q < NW; ++q) v += part[q][ct][l];
-    const int64_t mr = 16 * ct + (l & 15);
-    if (mr < m) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t nr = n0 + 4 * (l >> 4) + i;
-        if (nr < n) store_one(o.y, o.ytype, mr * n + nr, o.bias ? with_bias(v[i], bias_at(o, nr), o.ytype) : v[i]);
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int64_t nr = n0 + 16 * rt + 4 * (l >> 4) + i;
+      if (nr < n) store_one(o.y, o.ytype, mr * n + nr, o.bias ? with_bias(v[i], bias_at(o, nr), o.ytype) : v[i]);
     }
   }
 }
 
-// MT column tiles of 16 activation rows (M <= 16 MT); NW waves split K,
-// wave w taking chunks w, w + NW, ...  A wave issues the loads of B chunks
-// (weights and activations) at once, then decodes and multiplies them.
-// The loop body has no conditional work: a load whose result is used under
-// a branch is sunk into the branch and waited for there, and a prefetch
-// carried from one iteration to the next is merged back into a load at the
-// loop top.  Chunks past the end load a valid chunk again and are masked.
-template <class C, int MT, int NW, int B>
-__global__ __launch_bounds__(64 * NW) void k_smallm(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
-                                                    const uint16_t *__restrict__ x, int64_t m, const Out o,
-                                                    int64_t n, int64_t k) {
-  __shared__ f32x4 part[NW][MT][64];
+// The NW waves' partial (16 RT) x (16 MT) tiles summed through LDS and
+// stored.  16 x 16 C layout: lane l holds column (activation row) l % 16 and
+// weight rows 4 (l / 16) + i of its row tile.  Thread t sums one lane slot
+// of one (row tile, column tile) pair.
+template <int MT, int NW, int RT = 1>
+__device__ __forceinline__ void reduce_store(f32x4 (&part)[NW][RT][MT][64], const f32x4 (&acc)[RT][MT], int wave,
+                                             int lane, int64_t m, int64_t n, int64_t n0, const Out &o) {
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < MT; ++ct) part[wave][rt][ct][lane] = acc[rt][ct];
+  __syncthreads();
+  for (int slot = threadIdx.x; slot < RT * MT * 64; slot += 64 * NW) {
+    const int rt = slot / (MT * 64), ct = (slot >> 6) % MT, l = slot & 63;
+    f32x4 v = part[0][rt][ct][l];
+#pragma unroll
+    for (int q = 1; q < NW; ++q) v += part[q][rt][ct][l];
+    store_slot<MT>(v, rt, ct, l, m, n, n0, o);
+  }
+}
+
+// Split K: the workgroup's summed partial tile (one f32x4 per lane slot) to
+// wsp[slot]; the last of the S workgroups of the tile to count itself in
+// cnt (left at zero for the next call) adds the S partials in order
+// s = 0 .. S - 1 -- the same order whichever arrives last -- and stores.
+// Partials, counter and reads are agent-scope relaxed atomics, which the
+// XCDs' separate L2 caches keep coherent at the device's memory; the
+// workgroup barrier waits for every wave's partial stores to complete
+// before the count.  (Agent-scope fences instead would write back and
+// invalidate whole L2 caches per workgroup: measured slower than no split.)
+__device__ __forceinline__ void store_agent(f32x4 *p, const f32x4 &v) {
+  uint64_t *q = reinterpret_cast<uint64_t *>(p);
+  __hip_atomic_store(q, __builtin_bit_cast(uint64_t, (float2v){v[0], v[1]}), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(q + 1, __builtin_bit_cast(uint64_t, (float2v){v[2], v[3]}), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f32x4 load_agent(const f32x4 *p) {
+  const uint64_t *q = reinterpret_cast<const uint64_t *>(p);
+  const float2v a = __builtin_bit_cast(float2v, __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  const float2v b =
+      __builtin_bit_cast(float2v, __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  return (f32x4){a[0], a[1], b[0], b[1]};
+}
+
+template <int MT, int NW>
+__device__ __forceinline__ void reduce_split(f32x4 (&part)[NW][1][MT][64], const f32x4 (&acc)[1][MT], int wave,
+                                             int lane, int64_t m, int64_t n, int64_t n0, const Out &o, int S, int s,
+                                             f32x4 *__restrict__ wsp, uint32_t *__restrict__ cnt) {
+  __shared__ int last;
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) part[wave][0][ct][lane] = acc[0][ct];
+  __syncthreads();
+  for (int slot = threadIdx.x; slot < MT * 64; slot += 64 * NW) {
+    const int ct = slot >> 6, l = slot & 63;
+    f32x4 v = part[0][0][ct][l];
+#pragma unroll
+    for (int q = 1; q < NW; ++q) v += part[q][0][ct][l];
+    store_agent(wsp + (int64_t)s * MT * 64 + slot, v);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t before = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = before == (uint32_t)(S - 1);
+    if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last) return;
+  for (int slot = threadIdx.x; slot < MT * 64; slot += 64 * NW) {
+    const int ct = slot >> 6, l = slot & 63;
+    f32x4 v = load_agent(wsp + slot);
+    for (int q = 1; q < S; ++q) v += load_agent(wsp + (int64_t)q * MT * 64 + slot);
+    store_slot<MT>(v, 0, ct, l, m, n, n0, o);
+  }
+}
+
+// MT column tiles of 16 activation rows (M <= 16 MT) and RT row tiles of 16
+// weight rows per workgroup; NW waves split the workgroup's chunks
+// [lo, hi) of K, wave w taking chunks lo + w, lo + w + NW, ...  A wave issues
+// the loads of B chunks (the weights of every row tile and the activations,
+// once for all RT row tiles) at once, then decodes and multiplies them: an
+// activation fragment serves RT row tiles, so a workgroup reads its slice
+// of x once per 16 RT weight rows.  The loop body has no conditional work:
+// a load whose result is used under a branch is sunk into the branch and
+// waited for there, and a prefetch carried from one iteration to the next is
+// merged back into a load at the loop top.  Chunks past the end load a valid
+// chunk again and are masked.
+template <class C, int MT, int NW, int B, int RT>
+__device__ __forceinline__ void smallm_tiles(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
+                                             const uint16_t *__restrict__ x, int64_t m, const Out &o, int64_t n,
+                                             int64_t k, int64_t tile, int S, int s, f32x4 *__restrict__ wsp,
+                                             uint32_t *__restrict__ cnt, f32x4 (&part)[NW][RT][MT][64]) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t n0 = (int64_t)blockIdx.x * 16;
-  const int64_t row = n0 + (lane & 15) < n ? n0 + (lane & 15) : n - 1;
-  const int64_t nk = k / 64;
+  const int64_t n0 = tile * 16 * RT;
+  int64_t row[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int64_t r = n0 + 16 * rt + (lane & 15);
+    row[rt] = r < n ? r : n - 1;
+  }
+  constexpr bool HALF = C::CE == 128;
+  const int64_t nk = k / C::CE, cps = (nk + S - 1) / S;
+  const int64_t lo = s * cps, hi = lo + cps < nk ? lo + cps : nk;
 
   // Activation rows of this lane in each column tile (rows past m read row
   // m - 1; their results are not stored).
@@ -346,33 +492,90 @@ __global__ __launch_bounds__(64 * NW) void k_smallm(const uint8_t *__restrict__ 
 #pragma unroll
   for (int ct = 0; ct < MT; ++ct) {
     const int64_t mr = 16 * ct + (lane & 15);
-    xr[ct] = x + (mr < m ? mr : m - 1) * k + 8 * g;
+    xr[ct] = x + (mr < m ? mr : m - 1) * k + (HALF ? 64 * (g >> 1) + 16 * (g & 1) : 8 * g);
   }
 
-  f32x4 acc[MT];
+  f32x4 acc[RT][MT];
 #pragma unroll
-  for (int ct = 0; ct < MT; ++ct) acc[ct] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < MT; ++ct) acc[rt][ct] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
-  for (int64_t t = wave; t < nk; t += B * NW) {
-    typename C::Chunk c[B];
-    XFrag<MT> xf[B];
+  // (a workgroup whose slice is empty, lo >= hi, still joins the count)
+  for (int64_t t = lo + wave; t < hi; t += B * NW) {
+    typename C::Chunk c[B][RT];
+    typename std::conditional<HALF, XFragH<MT>, XFrag<MT>>::type xf[B];
 #pragma unroll
     for (int i = 0; i < B; ++i) {
-      const int64_t ti = t + i * NW < nk ? t + i * NW : t;
-      c[i] = C::load(w, aux, row, k, ti, g);
-      load_x<MT>(xf[i], xr, ti);
+      const int64_t ti = t + i * NW < hi ? t + i * NW : t;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) c[i][rt] = C::load(w, aux, row[rt], k, ti, g);
+      if constexpr (HALF) load_xh<MT>(xf[i], xr, ti);
+      else load_x<MT>(xf[i], xr, ti);
     }
     // Keep every load of the batch ahead of the first use (the scheduler
     // would otherwise trade loads in flight for registers).
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < B; ++i) {
-      const uint32_t vm = i == 0 ? 0xFFFFFFFFu : opaque(t + i * NW < nk ? 0xFFFFFFFFu : 0u);
-      mma_chunk<C, MT>(c[i], xf[i], acc, g, vm);
+      const uint32_t vm = i == 0 ? 0xFFFFFFFFu : opaque(t + i * NW < hi ? 0xFFFFFFFFu : 0u);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        if constexpr (HALF) mma_chunk_h<MT>(c[i][rt], xf[i], acc[rt], vm);
+        else mma_chunk<C, MT>(c[i][rt], xf[i], acc[rt], g, vm);
+      }
     }
   }
 
-  reduce_store<MT, NW>(part, acc, wave, lane, m, n, n0, o);
+  if constexpr (RT == 1) {
+    if (S > 1) {
+      reduce_split<MT, NW>(part, acc, wave, lane, m, n, n0, o, S, s, wsp, cnt);
+      return;
+    }
+  }
+  reduce_store<MT, NW, RT>(part, acc, wave, lane, m, n, n0, o);
+}
+
+// Order of the workgroups of a split launch: workgroup b runs on XCD b % 8
+// (workgroups are dealt to the eight XCDs in turn, each with its own L2), so
+// the S workgroups of a row tile, numbered consecutively, would read the
+// 32-byte pieces of the same 128-byte lines from eight different L2s, each
+// fetching the line: measured 2x the weight bytes from memory on the
+// 896 x 4864 down projection.  XCD x takes the x-th eighth of the
+// workgroups instead, so the slices of a tile meet in one L2.  Grids that
+// are not a multiple of 8 (and unsplit launches) keep b.
+__device__ __forceinline__ int split_order(int b, int grid, int S) {
+  if (S == 1 || (grid & 7)) return b;
+  return (b & 7) * (grid >> 3) + (b >> 3);
+}
+
+// One weight: workgroup b takes row tiles [(b / S) RT, + RT), K slice b % S
+// (split partials at wsp + (b / S) S MT 64, counters cnt[b / S]).
+template <class C, int MT, int NW, int B, int RT>
+__global__ __launch_bounds__(64 * NW) void k_smallm(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
+                                                    const uint16_t *__restrict__ x, int64_t m, const Out o,
+                                                    int64_t n, int64_t k, int S, f32x4 *__restrict__ wsp,
+                                                    uint32_t *__restrict__ cnt) {
+  __shared__ f32x4 part[NW][RT][MT][64];
+  const int bid = split_order((int)blockIdx.x, (int)gridDim.x, S);
+  const int64_t tile = bid / S;
+  smallm_tiles<C, MT, NW, B, RT>(w, aux, x, m, o, n, k, tile, S, bid % S, wsp + tile * S * MT * 64, cnt + tile,
+                                 part);
+}
+
+// A set of weights sharing x (pick_entry chooses this workgroup's weight;
+// every entry's workgroups are a multiple of S, so b / S numbers the tiles
+// of the whole set).
+template <class C, int MT, int NW, int B, int RT>
+__global__ __launch_bounds__(64 * NW) void k_smallm_set(const WeightSet set, const uint16_t *__restrict__ x,
+                                                        int64_t m, int64_t k, int S, f32x4 *__restrict__ wsp,
+                                                        uint32_t *__restrict__ cnt) {
+  __shared__ f32x4 part[NW][RT][MT][64];
+  const int bid = split_order((int)blockIdx.x, (int)gridDim.x, S);
+  const SetEntry e = pick_entry(set, bid);
+  const int gt = bid / S;
+  smallm_tiles<C, MT, NW, B, RT>(e.w, e.aux, x, m, e.o, e.n, k, (bid - e.g0) / S, S, bid % S,
+                                 wsp + (int64_t)gt * S * MT * 64, cnt + gt, part);
 }
 
 // ---- f32 / f16 activations ------------------------------------------------
@@ -431,7 +634,7 @@ template <class C, int MT, int NW, int B, int XT>
 __global__ __launch_bounds__(64 * NW) void k_smallm_f32(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
                                                         const uint8_t *__restrict__ x, int64_t m, const Out o,
                                                         int64_t n, int64_t k) {
-  __shared__ f32x4 part[NW][MT][64];
+  __shared__ f32x4 part[NW][1][MT][64];
   const int lane = threadIdx.x & 63, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t n0 = (int64_t)blockIdx.x * 16;
@@ -446,9 +649,9 @@ __global__ __launch_bounds__(64 * NW) void k_smallm_f32(const uint8_t *__restric
     xr[ct] = x + ((mr < m ? mr : m - 1) * k + 8 * g) * XB;
   }
 
-  f32x4 acc[MT];
+  f32x4 acc[1][MT];
 #pragma unroll
-  for (int ct = 0; ct < MT; ++ct) acc[ct] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  for (int ct = 0; ct < MT; ++ct) acc[0][ct] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
   for (int64_t t = wave; t < nk; t += B * NW) {
     typename C::Chunk c[B];
@@ -463,7 +666,7 @@ __global__ __launch_bounds__(64 * NW) void k_smallm_f32(const uint8_t *__restric
 #pragma unroll
     for (int i = 0; i < B; ++i) {
       const uint32_t vm = i == 0 ? 0xFFFFFFFFu : opaque(t + i * NW < nk ? 0xFFFFFFFFu : 0u);
-      mma_chunk_f32<C, MT>(c[i], xf[i], acc, g, vm);
+      mma_chunk_f32<C, MT>(c[i], xf[i], acc[0], g, vm);
     }
   }
 
@@ -507,26 +710,134 @@ int dispatch_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hi
   }
 }
 
-// Four waves per workgroup.  Batch sizes as measured on the 0.5B-model
-// layer shapes: 4 chunks for one and two column tiles; one for four (their
-// registers leave no room for a batch, and the kernel is decode-bound).
-// More waves per workgroup or deeper batches were slower: the masked
-// chunks of a partly filled batch cost as much decode as real ones.
-template <class C, int MT>
-int run_mt(const rq_weight *wt, const uint16_t *x, int64_t m, const Out &o, hipStream_t s) {
-  constexpr int B = MT == 4 ? 1 : 4;
-  const dim3 grid((unsigned)((wt->n + 15) / 16));
-  const uint8_t *aux = wt->data + wt->aux_off;
-  hipLaunchKernelGGL((k_smallm<C, MT, 4, B>), grid, dim3(256), 0, s, wt->data, aux, x, m, o, wt->n, wt->k);
+// Launch plan: S workgroups per row tile splitting K, NW waves a workgroup,
+// batches of B chunks, RT row tiles a workgroup.
+//  * Split K when there are few row tiles (k / v / q / o / down of a small
+//    layer: 8 - 72 tiles on 256 CUs): S up to 8, at most 512 workgroups, at
+//    least two chunks a workgroup.
+//  * Waves and batch so that one batch of every wave covers the
+//    workgroup's chunks (each batch is a dependent round trip to memory),
+//    within the registers: a batch holds B chunks of every row tile and B
+//    activation fragments of 16 MT bytes a lane; 16 waves leave 128 VGPRs
+//    a lane.
+//  * Row tiles: with four waves and no split, as many as keep at least 256
+//    workgroups (each workgroup reads its slice of x once).
+struct SmPlan {
+  int s, nw, b, rt;
+};
+template <int MT>
+SmPlan smallm_plan(int64_t tiles, int64_t nk, bool can_split) {
+  int S = 1;
+  if (can_split && tiles < 128)
+    while (S < 8 && tiles * S * 2 <= 512 && nk >= 4 * S) S *= 2;
+  const int64_t c = (nk + S - 1) / S;
+  SmPlan p{S, 4, 1, 1};
+  if (MT == 4) {
+    if (c <= 4) p = {S, 4, 1, 1};
+    else if (c <= 8) p = {S, 8, 1, 1};
+    else p = {S, 16, 1, 1};
+  } else {
+    if (c <= 4) p = {S, 4, 1, 1};
+    else if (c <= 8) p = {S, 4, 2, 1};
+    else if (c <= 16) p = {S, 4, 4, 1};
+    else if (c <= 32) p = {S, 8, 4, 1};
+    else p = {S, 16, MT == 1 ? 5 : 2, 1};
+  }
+  const bool rt_ok = S == 1 && p.nw == 4 && p.b == (MT == 4 ? 1 : 4);
+  if (rt_ok) p.rt = tiles >= 4 * 256 ? 4 : (tiles >= 2 * 256 ? 2 : 1);
+  return p;
+}
+
+template <class C, int MT, int NW, int B, int RT>
+int launch_mt(const rq_weight *const *w, int count, bool set, const uint16_t *x, int64_t m, const Out *o, int S,
+              f32x4 *wsp, uint32_t *cnt, hipStream_t s) {
+  if (!set) {
+    const rq_weight *wt = w[0];
+    const int64_t tiles = ((wt->n + 15) / 16 + RT - 1) / RT;
+    hipLaunchKernelGGL((k_smallm<C, MT, NW, B, RT>), dim3((unsigned)(tiles * S)), dim3(64 * NW), 0, s, wt->data,
+                       wt->data + wt->aux_off, x, m, o[0], wt->n, wt->k, S, wsp, cnt);
+  } else {
+    WeightSet ws;
+    int64_t total = 0;
+    const int rc = fill_set(ws, w, count, o, [&](const rq_weight *wj) { return ((wj->n + 15) / 16 + RT - 1) / RT * S; },
+                            &total);
+    if (rc) return rc;
+    hipLaunchKernelGGL((k_smallm_set<C, MT, NW, B, RT>), dim3((unsigned)total), dim3(64 * NW), 0, s, ws, x, m,
+                       w[0]->k, S, wsp, cnt);
+  }
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "small-M launch failed");
 }
 
+template <class C, int MT, int NW, int B>
+constexpr int sm_batch() {
+  if constexpr (C::CE == 128) {
+    constexpr int cap = MT == 1 ? (NW == 16 ? 3 : 4) : (MT == 2 ? (NW == 16 ? 1 : 2) : 1);
+    return B < cap ? B : cap;
+  }
+  return B;
+}
+
+// Plans and launches one weight or a set (every weight of format C, one k).
+template <class C, int MT>
+int run_plan(const rq_weight *const *w, int count, bool set, const void *xv, int64_t m, const Out *o, hipStream_t s,
+             WsLease *ws) {
+  const uint16_t *x = static_cast<const uint16_t *>(xv);
+  int64_t tiles = 0;
+  for (int j = 0; j < count; ++j) tiles += (w[j]->n + 15) / 16;
+  SmPlan p = smallm_plan<MT>(tiles, w[0]->k / C::CE, ws != nullptr && tiles <= WsLease::kCounters);
+  f32x4 *wsp = nullptr;
+  uint32_t *cnt = nullptr;
+  if (p.s > 1) {
+    int rc = RQ_OK;
+    cnt = ws->counters();
+    wsp = cnt ? static_cast<f32x4 *>(ws->get((size_t)tiles * p.s * MT * 64 * sizeof(f32x4), &rc)) : nullptr;
+    if (!wsp) p = smallm_plan<MT>(tiles, w[0]->k / C::CE, false);  // no scratch: one workgroup per tile
+  }
+  // (a half-block chunk holds twice the weights and activations of a
+  // 64-element chunk: smaller batches where registers are short)
+#define RQ_SM(NW, B, RT) return launch_mt<C, MT, NW, sm_batch<C, MT, NW, B>(), RT>(w, count, set, x, m, o, p.s, wsp, cnt, s)
+  if constexpr (MT == 4) {
+    if (p.nw == 16) RQ_SM(16, 1, 1);
+    if (p.nw == 8) RQ_SM(8, 1, 1);
+    if (p.rt == 4) RQ_SM(4, 1, 4);
+    if (p.rt == 2) RQ_SM(4, 1, 2);
+    RQ_SM(4, 1, 1);
+  } else {
+    if (p.nw == 16) RQ_SM(16, (MT == 1 ? 5 : 2), 1);
+    if (p.nw == 8) RQ_SM(8, 4, 1);
+    if (p.b == 4) {
+      if (p.rt == 4) RQ_SM(4, 4, 4);
+      if (p.rt == 2) RQ_SM(4, 4, 2);
+      RQ_SM(4, 4, 1);
+    }
+    if (p.b == 2) RQ_SM(4, 2, 1);
+    RQ_SM(4, 1, 1);
+  }
+#undef RQ_SM
+}
+
 template <class C>
-int run(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s) {
-  const uint16_t *xb = static_cast<const uint16_t *>(x);
-  if (m <= 16) return run_mt<C, 1>(wt, xb, m, o, s);
-  if (m <= 32) return run_mt<C, 2>(wt, xb, m, o, s);
-  return run_mt<C, 4>(wt, xb, m, o, s);
+int run(const rq_weight *const *w, int count, bool set, const void *x, int64_t m, const Out *o, hipStream_t s,
+        WsLease *ws) {
+  if (m <= 16) return run_plan<C, 1>(w, count, set, x, m, o, s, ws);
+  if (m <= 32) return run_plan<C, 2>(w, count, set, x, m, o, s, ws);
+  return run_plan<C, 4>(w, count, set, x, m, o, s, ws);
+}
+
+int dispatch_bf16(const rq_weight *const *w, int count, bool set, const void *x, int64_t m, const Out *o,
+                  hipStream_t s, WsLease *ws) {
+  switch (w[0]->qtype) {
+    case RQ_Q4_K:
+      // half super-blocks as chunks where rows hold whole halves
+      if (w[0]->k % 128 == 0) return run<SmQ4KH>(w, count, set, x, m, o, s, ws);
+      return run<SmQ4K>(w, count, set, x, m, o, s, ws);
+    case RQ_Q6_K: return run<SmQ6K>(w, count, set, x, m, o, s, ws);
+    case RQ_Q8_0: return run<SmQ8>(w, count, set, x, m, o, s, ws);
+    case RQ_Q5_K: return run<SmQ5K>(w, count, set, x, m, o, s, ws);
+    case RQ_Q4_0: return run<SmQx0<false>>(w, count, set, x, m, o, s, ws);
+    case RQ_Q5_0: return run<SmQx0<true>>(w, count, set, x, m, o, s, ws);
+    default: return RQ_E_UNSUPPORTED;
+  }
 }
 
 }  // namespace
@@ -542,18 +853,21 @@ int launch_linear_smallm_f32(const rq_weight *wt, const void *x, int xtype, int6
   return RQ_E_UNSUPPORTED;
 }
 
+// bf16 activations, 2 <= m <= 64, k % 64 == 0, 16-byte aligned x, weights of
+// one format and k.
+int launch_linear_smallm_set(const rq_weight *const *w, int count, const void *x, int64_t m, const Out *o,
+                             hipStream_t s, WsLease *ws) {
+  const int64_t k = w[0]->k;
+  if (m < 2 || m > 64 || k % 64 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
+  for (int j = 1; j < count; ++j)
+    if (w[j]->qtype != w[0]->qtype || w[j]->k != k) return RQ_E_UNSUPPORTED;
+  return dispatch_bf16(w, count, true, x, m, o, s, ws);
+}
+
 // bf16 activations, 2 <= m <= 64, k % 64 == 0, 16-byte aligned x.
-int launch_linear_smallm(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s) {
+int launch_linear_smallm(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease *ws) {
   if (m < 2 || m > 64 || wt->k % 64 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
-  switch (wt->qtype) {
-    case RQ_Q4_K: return run<SmQ4K>(wt, x, m, o, s);
-    case RQ_Q6_K: return run<SmQ6K>(wt, x, m, o, s);
-    case RQ_Q8_0: return run<SmQ8>(wt, x, m, o, s);
-    case RQ_Q5_K: return run<SmQ5K>(wt, x, m, o, s);
-    case RQ_Q4_0: return run<SmQx0<false>>(wt, x, m, o, s);
-    case RQ_Q5_0: return run<SmQx0<true>>(wt, x, m, o, s);
-    default: return RQ_E_UNSUPPORTED;
-  }
+  return dispatch_bf16(&wt, 1, false, x, m, &o, s, ws);
 }
 
 }  // namespace rq

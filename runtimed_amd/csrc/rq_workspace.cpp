@@ -34,6 +34,7 @@ struct Slot {
   void *ptr = nullptr;
   size_t bytes = 0;
   bool graph_ref = false;  // a captured graph may refer to ptr: never free it
+  uint32_t *counters = nullptr;  // zero between calls; never freed
 };
 
 namespace {
@@ -146,6 +147,24 @@ void *WsLease::get(size_t bytes, int *rc) {
   void *p = static_cast<uint8_t *>(slot_->ptr) + used_;
   used_ += bytes;
   return p;
+}
+
+uint32_t *WsLease::counters() {
+  if (!slot_) acquire();
+  if (slot_->counters) return slot_->counters;
+  if (capturing_) return nullptr;
+  void *p = nullptr;
+  if (hipMallocAsync(&p, kCounters * sizeof(uint32_t), s_) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (hipMemsetAsync(p, 0, kCounters * sizeof(uint32_t), s_) != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipFreeAsync(p, s_);
+    return nullptr;
+  }
+  slot_->counters = static_cast<uint32_t *>(p);
+  return slot_->counters;
 }
 
 }  // namespace rq

@@ -180,10 +180,17 @@ class QWeight:
 def linear_multi(weights, x: torch.Tensor, biases=None, out_dtype: Optional[torch.dtype] = None):
     """Several linears on one input (q/k/v, gate/up: qwen2.rs:99-125) through
     rq_linear_multi; returns the outputs in order."""
-    k = x.shape[-1]
     x = x.contiguous()
-    rows = x.numel() // k if k else 0
     outs = [torch.empty((*x.shape[:-1], w.n), dtype=out_dtype or x.dtype, device=x.device) for w in weights]
+    if outs:
+        linear_multi_into(weights, x, outs, biases)
+    return outs
+
+
+def linear_multi_into(weights, x: torch.Tensor, outs, biases=None) -> None:
+    """linear_multi into preallocated outputs (x contiguous; outputs of one dtype)."""
+    k = x.shape[-1]
+    rows = x.numel() // k if k else 0
     count = len(weights)
     hs = (ctypes.c_void_p * count)(*[w.handle.value for w in weights])
     ys = (ctypes.c_void_p * count)(*[o.data_ptr() for o in outs])
@@ -193,9 +200,8 @@ def linear_multi(weights, x: torch.Tensor, biases=None, out_dtype: Optional[torc
         present = [b for b in biases if b is not None]
         btype = ftype(present[0].dtype) if present else F32
         bs = (ctypes.c_void_p * count)(*[(b.data_ptr() if b is not None else 0) for b in biases])
-    check(lib().rq_linear_multi(count, hs, _ptr(x), ftype(x.dtype), rows, k, bs, btype, ys,
-                                ftype(outs[0].dtype) if outs else F32, _stream(x.device)))
-    return outs
+    check(lib().rq_linear_multi(count, hs, _ptr(x), ftype(x.dtype), rows, k, bs, btype, ys, ftype(outs[0].dtype),
+                                _stream(x.device)))
 
 
 def bias_add(y: torch.Tensor, bias: torch.Tensor) -> torch.Tensor:
