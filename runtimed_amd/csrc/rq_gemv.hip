@@ -695,6 +695,13 @@ int run_seg(const rq_weight *wt, const void *x, int xtype, const Out &o, hipStre
 template <class F>
 int run_m1(const rq_weight *wt, const void *x, int xtype, const Out &o, hipStream_t s) {
   const int P = (int)(wt->k / F::PE);
+  // Q4_K long rows on many rows: the matrix-core GEMV where it applies.
+  if constexpr (std::is_same_v<F, FmtQ4K>) {
+    if (P > 64 && wt->n >= 4096) {
+      const int rc = launch_gemv_mx(wt, x, xtype, o, s);
+      if (rc != RQ_E_UNSUPPORTED) return rc;
+    }
+  }
   // Long rows on many rows: one wave per row walking the rows.
   if (P > 64 && wt->n >= 4096) {
     switch ((P + 63) / 64) {

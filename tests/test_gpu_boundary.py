@@ -33,15 +33,16 @@ def bias_vec(n, seed, dtype, dev):
     return torch.from_numpy(synth.activations(seed, 1, n)[0]).to(dtype).to(dev)
 
 
-# Every kernel family of the fused path: segment / team / long-row GEMVs
-# (M = 1, 2), the small-M matrix-core kernels (bf16 and f32), the tiled GEMM
+# Every kernel family of the fused path: segment / team / long-row /
+# matrix-core GEMVs (M = 1, 2), the small-M matrix-core kernels (bf16 and f32), the tiled GEMM
 # with and without split K, the pipelined 256 x 256 kernel, the f32 slices,
 # and the generic kernel (k % 64 != 0).
 ROUTES = [
     # (qtype, n, k, m, xdtype)
     (rq.Q4_K, 4864, 896, 1, torch.float32),     # segment GEMV
     (rq.Q4_K, 896, 4864, 1, torch.float32),     # team GEMV
-    (rq.Q4_K, 4100, 4096, 1, torch.float32),    # one wave per row
+    (rq.Q4_K, 4100, 4096, 1, torch.float32),    # matrix-core GEMV (Q4_K long rows)
+    (rq.Q8_0, 4100, 4096, 1, torch.float32),    # one wave per row
     (rq.Q6_K, 896, 896, 2, torch.float32),      # two rows, segment
     (rq.Q4_K, 896, 4864, 2, torch.bfloat16),    # two rows, team
     (rq.Q8_0, 128, 896, 16, torch.bfloat16),    # small-M bf16 MFMA

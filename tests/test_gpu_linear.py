@@ -47,6 +47,24 @@ def test_decode_gemv_f32(dev, qtype, n, k):
 
 
 @pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("n,k", [(4096, 512), (4133, 4096), (14336, 4096), (4096, 8192)])
+def test_gemv_matrix_cores_q4k(dev, xdt, n, k):
+    # M = 1 Q4_K with k % 512 == 0, k <= 8192 and n >= 4096 runs on the matrix
+    # cores: the codes as bf16 128 + q, x as two bf16 limbs (16 significant
+    # bits), f32 sums; x spans six decades (N(0,1) with every 7th element
+    # x300 and every 11th x1e-3), n = 4133 ends in a partial 32-row tile
+    print(f"gemv mx x={xdt} n={n} k={k}", flush=True)
+    w, wf = make(rq.Q4_K, n, k, 60 + n + k)
+    x = synth.activations(5, 1, k)
+    x[0, ::7] *= 300.0
+    x[0, 3::11] *= 1e-3
+    xt = torch.from_numpy(x).to(xdt)
+    y = w.forward(xt.to(dev), out_dtype=torch.float32).cpu().numpy()
+    assert y.shape == (1, n)
+    assert norm_err(y, ref(xt.float().numpy(), wf)) <= TOL_F32
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("qtype,n,k", [
     (rq.Q4_K, 4864, 896),   # 16-byte chunks of x per thread: 1 (f32) / 1 (16-bit)
     (rq.Q4_K, 512, 2048),   # 2 / 1
