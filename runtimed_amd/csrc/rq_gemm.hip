@@ -36,30 +36,41 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int BK = 64, LDS_K = BK + 8;
 
-// A BM x BN tile of y per workgroup of WM x WN waves; each wave owns a
-// (BM / WM) x (BN / WN) sub-tile made of MI x NI MFMA tiles of 32 x 32.  Each
-// thread decodes exactly one 32-element weight piece per K-step
+// A BM x BN tile of y per workgroup of KG groups of WM x WN waves; each
+// wave owns a (BM / WM) x (BN / WN) sub-tile made of MI x NI MFMA tiles of
+// 32 x 32.  Each thread decodes exactly one 32-element weight piece per K-step
 // (BN * 2 == 64 * WM * WN).
 // Split K: workgroup z covers K-steps [z * steps, (z + 1) * steps) and, when
 // part is not null, writes its f32 partial tile to part + z * m * n instead
-// of y (k_splitk_sum adds the partials).
-template <class F, int BM, int BN, int WM, int WN, int D>
-__global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restrict__ w,
-                                                       const uint8_t *__restrict__ aux,
-                                                       const uint16_t *__restrict__ x, int64_t m,
-                                                       int64_t n, int64_t k, const Out o, int64_t steps,
-                                                       float *__restrict__ part) {
-  constexpr int NT = 64 * WM * WN;
+// of y (k_splitk_sum adds the partials).  Inside a workgroup, K-group g
+// (waves g * WM * WN ..) takes the g-th of KG equal parts of those steps with
+// LDS buffers of its own (the host makes steps a multiple of KG); the groups
+// meet in LDS at the end (added in group order) and group 0 stores.  More
+// waves per tile then keep more loads in flight where a tile's K loop is
+// latency-bound (the 2048-wide layers at M = 512: 256 tiles of 64 x 64).
+template <class F, int BM, int BN, int WM, int WN, int D, int KG = 1>
+__global__ __launch_bounds__(64 * WM * WN * KG) void k_qgemm(const uint8_t *__restrict__ w,
+                                                            const uint8_t *__restrict__ aux,
+                                                            const uint16_t *__restrict__ x, int64_t m,
+                                                            int64_t n, int64_t k, const Out o, int64_t steps,
+                                                            float *__restrict__ part) {
+  constexpr int NT = 64 * WM * WN;  // threads of a K-group
   static_assert(BN * 2 == NT, "one weight piece per thread");
   constexpr int MI = BM / WM / 32, NI = BN / WN / 32;
   constexpr int A_LOADS = BM * BK / 8 / NT;  // 16-byte loads per thread per step
   constexpr int A_ROWS = NT / 8;              // activation rows covered by one load round
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * LDS_K];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * LDS_K];
+  constexpr int A_BYTES = BM * LDS_K * 2, B_BYTES = BN * LDS_K * 2;
+  constexpr int G_BYTES = 2 * (A_BYTES + B_BYTES);  // a group's double-buffered tiles
+  static_assert(KG == 1 || BM * BN * 4 <= G_BYTES, "the partial tile of a group fits its buffers");
+  __shared__ __attribute__((aligned(16))) uint8_t SM[KG * G_BYTES];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int grp = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / NT));
+  const int tid = threadIdx.x % NT, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
+  uint8_t *const G = SM + grp * G_BYTES;
+  auto As = [&](int buf) { return reinterpret_cast<uint16_t *>(G + buf * A_BYTES); };
+  auto Bs = [&](int buf) { return reinterpret_cast<uint16_t *>(G + 2 * A_BYTES + buf * B_BYTES); };
 
   // Weight piece of this thread: row n0 + (tid >> 1), half h = tid & 1;
   // activation slots: row (tid >> 3) + A_ROWS * i, 8 bf16 at column
@@ -77,25 +88,27 @@ __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restric
 
   // Loads run D K-steps ahead in D register slots (LLVM vector types: a
   // HIP uint4 array would be copied through private memory).
-  const int64_t kt0 = (int64_t)blockIdx.z * steps;
-  const int64_t nk = (k / BK - kt0 < steps ? k / BK - kt0 : steps);
+  const int64_t gsteps = steps / KG;
+  const int64_t kt0 = (int64_t)blockIdx.z * steps + grp * gsteps;
+  const int64_t nk = (k / BK - kt0 < gsteps ? k / BK - kt0 : gsteps);
   u32x4 ra[D][A_LOADS];
   typename F::Piece pb[D];
-  auto gload = [&](int slot, int64_t s) {  // local step s, clamped to the split
+  auto gload = [&](int slot, int64_t s) {  // local step s, clamped to the group's steps
     const int64_t kt = kt0 + (s < nk ? s : nk - 1);
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) ra[slot][i] = *reinterpret_cast<const u32x4 *>(xa[i] + kt * BK);
     pb[slot] = F::load(w, aux, gn, k, (int)(2 * kt + bh));
   };
   auto sstore = [&](int slot, int buf) {
+    uint16_t *A = As(buf), *B = Bs(buf);
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i)
-      *reinterpret_cast<u32x4 *>(&As[buf][(arow + A_ROWS * i) * LDS_K + acol]) = ra[slot][i];
+      *reinterpret_cast<u32x4 *>(&A[(arow + A_ROWS * i) * LDS_K + acol]) = ra[slot][i];
     uint32_t ob[16];
     F::decode_bf16(pb[slot], ob);
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      u32x4 *dst = reinterpret_cast<u32x4 *>(&Bs[buf][brow * LDS_K + 16 * bh + 32 * r]);
+      u32x4 *dst = reinterpret_cast<u32x4 *>(&B[brow * LDS_K + 16 * bh + 32 * r]);
 #pragma unroll
       for (int q = 0; q < 2; ++q)
         dst[q] = (u32x4){ob[8 * r + 4 * q], ob[8 * r + 4 * q + 1], ob[8 * r + 4 * q + 2], ob[8 * r + 4 * q + 3]};
@@ -109,16 +122,17 @@ __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restric
     for (int j = 0; j < NI; ++j) acc[i][j] = (f32x16){0};
 
   auto mfma_step = [&](int buf) {
+    const uint16_t *A = As(buf), *B = Bs(buf);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       const int kc = ks * 16 + 8 * (lane >> 5);
       bf16x8 fa[MI], fb[NI];
 #pragma unroll
       for (int i = 0; i < MI; ++i)
-        fa[i] = *reinterpret_cast<const bf16x8 *>(&As[buf][(wm * (BM / WM) + i * 32 + (lane & 31)) * LDS_K + kc]);
+        fa[i] = *reinterpret_cast<const bf16x8 *>(&A[(wm * (BM / WM) + i * 32 + (lane & 31)) * LDS_K + kc]);
 #pragma unroll
       for (int j = 0; j < NI; ++j)
-        fb[j] = *reinterpret_cast<const bf16x8 *>(&Bs[buf][(wn * (BN / WN) + j * 32 + (lane & 31)) * LDS_K + kc]);
+        fb[j] = *reinterpret_cast<const bf16x8 *>(&B[(wn * (BN / WN) + j * 32 + (lane & 31)) * LDS_K + kc]);
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -132,7 +146,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restric
   // buffer and its slot refilled with step s + 1 + D; one barrier.  The
   // stores of steps past the end are made anyway (clamped data into a buffer
   // that is never read) and only their matrix work is skipped, so no load is
-  // made under a branch.
+  // made under a branch.  Every group runs the same number of steps.
 #pragma unroll
   for (int j = 0; j < D; ++j) gload(j, j);
   sstore(0, 0);
@@ -148,6 +162,32 @@ __global__ __launch_bounds__(64 * WM * WN) void k_qgemm(const uint8_t *__restric
       gload((j + 1) % D, s + 1 + D);
       __syncthreads();
     });
+  }
+
+  if constexpr (KG > 1) {
+    // Groups 1 .. KG - 1 leave their accumulators in their own buffers
+    // (free after the last barrier); group 0 adds them in group order.
+    float *red = reinterpret_cast<float *>(G);
+    auto idx = [&](int i, int j, int r) { return (((wave * MI + i) * NI + j) * 16 + r) * 64 + lane; };
+    if (grp > 0) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) red[idx(i, j, r)] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (grp > 0) return;
+    for (int g = 1; g < KG; ++g) {
+      const float *rg = reinterpret_cast<const float *>(SM + g * G_BYTES);
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] += rg[idx(i, j, r)];
+    }
   }
 
   // Split K: f32 partials without the bias (k_splitk_sum adds it).
@@ -403,12 +443,16 @@ int splits_for(int64_t tiles, int64_t nk) {
   return sp;
 }
 
-template <class F, int BM, int BN, int WM, int WN, int D = 3>
+template <class F, int BM, int BN, int WM, int WN, int D = 3, int KG = 1>
 int launch(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease &ws,
            int sp_force = 0) {
   const int64_t nk = wt->k / BK;
   const int64_t gx = (wt->n + BN - 1) / BN, gy = (m + BM - 1) / BM;
   const int sp = sp_force > 0 ? sp_force : splits_for(gx * gy, nk);
+  // K-groups need equal shares of every split's steps.
+  if constexpr (KG > 1) {
+    if (nk % ((int64_t)sp * KG) != 0) return launch<F, BM, BN, WM, WN, D, 1>(wt, x, m, o, s, ws, sp);
+  }
   const int64_t steps = (nk + sp - 1) / sp;
   const int used = (int)((nk + steps - 1) / steps);  // splits that own at least one step
   float *part = nullptr;
@@ -418,7 +462,7 @@ int launch(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStrea
     if (!part) return rc;
   }
   const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)used);
-  hipLaunchKernelGGL((k_qgemm<F, BM, BN, WM, WN, D>), grid, dim3(64 * WM * WN), 0, s, wt->data,
+  hipLaunchKernelGGL((k_qgemm<F, BM, BN, WM, WN, D, KG>), grid, dim3(64 * WM * WN * KG), 0, s, wt->data,
                      wt->data + wt->aux_off, static_cast<const uint16_t *>(x), m, wt->n, wt->k, o, steps, part);
   if (part) {
     const int64_t mn = m * wt->n;
@@ -445,17 +489,21 @@ int by_m(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_
   if (big_tiles >= 256 && wt->k % 128 == 0) return launch_pipe<F>(wt, x, m, o, s);
   if (big_tiles >= 256) return launch<F, 256, 256, 2, 4, 1>(wt, x, m, o, s, ws);
   // Fewer than 128 tiles of 128 x 128 (2048-wide layers at M = 512): short K
-  // takes 64 x 64 tiles of two waves (256 workgroups); long K keeps 128 x 128
-  // and splits K four ways (at most, 32 K-steps per split).  Measured on the
-  // 2048 / 8192 prefill shapes: q/k/o 36 -> 26 us (64 x 128) -> 25.3 us
-  // (64 x 64), v Q6_K 28.2 -> 27.2 us, down 67 -> 53 us.
+  // takes 64 x 64 tiles of two waves (256 workgroups) in four K-groups (eight
+  // waves a workgroup); long K keeps 128 x 128 and splits K four ways (at
+  // most, 32 K-steps per split).  Other shapes: 128 x 128 in two K-groups.
+  // Each K-step is latency-bound at these sizes (a 64-deep step is 8-16
+  // MFMAs a wave), so more waves per tile help.  Measured on the 2048 / 8192
+  // prefill shapes: q/k/o 36 -> 26 us (64 x 128) -> 25.3 us (64 x 64) ->
+  // 18.4 us (four K-groups), v Q6_K 28.2 -> 27.2 -> 21.9 us, gate/up 37.9 ->
+  // 34.4 us (two K-groups), down 67 -> 53 us (two K-groups: 56 us).
   const int64_t tiles128 = ((m + 127) / 128) * ((wt->n + 127) / 128), nk = wt->k / BK;
-  if (tiles128 < 128 && nk <= 32) return launch<F, 64, 64, 2, 1>(wt, x, m, o, s, ws);
+  if (tiles128 < 128 && nk <= 32) return launch<F, 64, 64, 2, 1, 3, 4>(wt, x, m, o, s, ws);
   if (tiles128 < 128 && nk >= 64) {
     const int sp = (int)(nk / 32 < 4 ? nk / 32 : 4);
     return launch<F, 128, 128, 2, 2>(wt, x, m, o, s, ws, sp);
   }
-  return launch<F, 128, 128, 2, 2>(wt, x, m, o, s, ws);
+  return launch<F, 128, 128, 2, 2, 3, 2>(wt, x, m, o, s, ws);
 }
 
 }  // namespace

@@ -260,10 +260,15 @@ def test_golden_gemv_on_device(dev):
 
 @pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0])
 @pytest.mark.parametrize("m,n,k", [(257, 130, 512), (33, 1000, 256), (65, 64, 1024), (300, 256, 2048),
-                                   (300, 256, 8192), (129, 200, 8384)])
+                                   (300, 256, 8192), (129, 200, 8384), (300, 128, 448), (300, 16384, 640),
+                                   (257, 8192, 2048), (300, 16384, 576)])
 def test_mfma_gemm_edge_tiles(dev, qtype, m, n, k):
     # K >= 4096 with few tiles splits K across workgroups (f32 partials, then
-    # a sum); 8384 = 131 K-steps leaves a shorter last split.
+    # a sum); 8384 = 131 K-steps leaves a shorter last split.  Inside a
+    # workgroup K is split over groups of waves: four on 64 x 64 tiles (k =
+    # 512, 1024, 2048: 2, 4 and 8 steps a group), two on 128 x 128 tiles
+    # (k = 640 and 2048: 5 and 16 steps a group); 448 (7 steps) and 576
+    # (9 steps) do not divide and run one group.
     # bf16 activations with m > 1 run on the matrix cores; tiles are 32..256 x 128
     w, wf = make(qtype, n, k, 81 + m + n)
     xb = torch.from_numpy(synth.activations(9 + m, m, k)).to(torch.bfloat16)
