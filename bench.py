@@ -364,13 +364,21 @@ def extra_fp8(torch, rq, synth, dev, steps, warmup):
     def gemm():
         rq.fp8_gemm_q(xq, xs, wq, ws, y)
 
+    def both():
+        rq.fp8_gemm(x, wq, ws, mode=rq.FP8_PER_TOKEN, out=y)
+
+    # four calls per graph, timed over replays (a one-node graph's replay
+    # adds several microseconds of its own)
+    reps = 4
     t = Timer(torch)
-    gq = capture(torch, quant)
-    ms_q = t.replay(gq, steps, warmup)
-    gg = capture(torch, gemm)
-    ms_g = t.replay(gg, steps, warmup)
-    gb = capture(torch, lambda: rq.fp8_gemm(x, wq, ws, mode=rq.FP8_PER_TOKEN, out=y))
-    ms_b = t.replay(gb, steps, warmup)
+
+    def timed(fn):
+        g = capture(torch, lambda: [fn() for _ in range(reps)])
+        ms = t.replay(g, steps, warmup) / reps
+        del g
+        return ms
+
+    ms_q, ms_g, ms_b = timed(quant), timed(gemm), timed(both)
     tf = 2.0 * m * n * k / (ms_b * 1e-3) / 1e12
     tf_g = 2.0 * m * n * k / (ms_g * 1e-3) / 1e12
     return {"workload": "FP8 e4m3 GEMM 2048x14336x4096, per-token activation quantize + GEMM, bf16 out",

@@ -55,6 +55,22 @@ __device__ __forceinline__ uint32_t enc_e4m3_rne(float f) {
   return sign | (((uint32_t)(e + 7) << 3) | r);
 }
 
+// enc_e4m3_rne without branches, for the vector quantizer: the normal range
+// rounds the f32 bits to three mantissa bits (adding 0x7FFFF plus the kept
+// lsb carries into bit 20 exactly when round-to-nearest-even rounds up; the
+// carry moves into the exponent when the mantissa overflows), the
+// subnormal range is rint(a * 512) as above.  Same code as enc_e4m3_rne for
+// every one of the 2^32 f32 inputs (compared exhaustively on the host).
+__device__ __forceinline__ uint32_t enc_e4m3_rne_bf(float f) {
+  const uint32_t sign = (__float_as_uint(f) >> 24) & 0x80u;
+  const float a = fminf(fabsf(f), 448.0f);
+  const uint32_t u = __float_as_uint(a);
+  const uint32_t nrm = ((u + 0x7FFFFu + ((u >> 20) & 1u)) >> 20) - (120u << 3);
+  const uint32_t sub = (uint32_t)__builtin_rintf(a * 512.0f);
+  const uint32_t c = a < 0.015625f ? sub : nrm;
+  return f != f ? 0x7Fu : (sign | c);
+}
+
 // e4m3 decode for the scalar path (LUT formula of load_safetensors.rs:14-29).
 __device__ __forceinline__ float dec_e4m3(uint32_t b) {
   const int e = (b >> 3) & 0xF, m = b & 7;

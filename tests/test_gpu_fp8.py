@@ -46,8 +46,10 @@ def test_linear_fp8_default_and_explicit_scale(dev):  # linear_layer.rs:187-210
 
 
 @pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("k", [4096, 520, 72, 16384])
+@pytest.mark.parametrize("k", [4096, 520, 72, 16384, 66])
 def test_per_token_quantize_bit_exact(dev, xdt, k):
+    # a wave per row from 16-byte loads where rows are 16-byte aligned (k = 66
+    # is not: one workgroup per row, element loads)
     x = torch.from_numpy(synth.activations(11, 33, k) * 3.0).to(xdt)
     x[5] = 0.0
     xq, xs = rq.fp8_quantize(x.to(dev), rq.FP8_PER_TOKEN)
