@@ -112,17 +112,11 @@ def decode_workload(torch, rq, synth, layers, steps, warmup, dev):
             for name, n, k in LAYER:
                 lw[name].forward(x4864 if k == 4864 else x896, out=ys[name])
 
-    def gates():
-        for lw in W:
-            lw["gate"].forward(x896, out=ys["gate"])
-
     timer = Timer(torch)
     g = capture(torch, token)
     ms = timer.replay(g, steps, warmup)
-    gg = capture(torch, gates)
-    gate_ms = timer.replay(gg, max(steps, 20), warmup) / layers
-    del g, gg
-    return W, ms, gate_ms
+    del g
+    return W, ms
 
 
 def extra_decode_fused(torch, rq, synth, layers, steps, warmup, dev):
@@ -536,28 +530,60 @@ def extra_library(torch, dev, steps):
     return {"workload": "vendor BLAS on dense weights (reference point)", "shapes": out}
 
 
-def mode_gate(torch, rq, synth, dev, steps, warmup, eager=False):
-    """Only the dominant kernel: R distinct 4864x896 Q4_K gate weights
-    (R * 2.45 MB >= 1 GB), one GEMV each, in one HIP graph (or launched
-    eagerly, for counter collection)."""
+GATE_COPIES = 512  # 512 x 2.45 MB = 1.25 GB: more than the 256 MB Infinity Cache
+
+
+def gate_weights(rq, synth):
     n, k = 4864, 896
-    copies = 512
     blocks = synth.q4_k_blocks(104, n * k // 256)
-    W = [rq.QWeight(rq.Q4_K, blocks, n, k) for _ in range(copies)]
+    return [rq.QWeight(rq.Q4_K, blocks, n, k) for _ in range(GATE_COPIES)], n, k
+
+
+def gate_timing(torch, rq, synth, dev, steps, warmup):
+    """The dominant kernel alone: GATE_COPIES distinct 4864x896 Q4_K gate
+    weights, one GEMV each, captured in one HIP graph; microseconds per
+    launch (gaps included) from HIP events around the replays."""
+    W, n, k = gate_weights(rq, synth)
     x = torch.from_numpy(synth.activations(1, 1, k)).to(dev)
     y = torch.empty((1, n), device=dev)
-    b = n * k // 256 * Q4K_BLOCK + k * 4 + n * 4
+    g = capture(torch, lambda: [w.forward(x, out=y) for w in W])
+    ms = Timer(torch).replay(g, steps, warmup) / len(W)
+    del g, W
+    return ms * 1e3, n * k // 256 * Q4K_BLOCK + k * 4 + n * 4
+
+
+def mode_gate(torch, rq, synth, dev, steps, warmup, eager=False):
+    """Only the dominant kernel (gate_timing), or the same launches without a
+    HIP graph for counter collection."""
     if eager:
+        W, n, k = gate_weights(rq, synth)
+        x = torch.from_numpy(synth.activations(1, 1, k)).to(dev)
+        y = torch.empty((1, n), device=dev)
         for _ in range(steps):
             for w in W:
                 w.forward(x, out=y)
         torch.cuda.synchronize()
-        print(json.dumps({"mode": "gate-eager", "launches": copies * steps, "bytes_per_launch": b}), flush=True)
+        b = n * k // 256 * Q4K_BLOCK + k * 4 + n * 4
+        print(json.dumps({"mode": "gate-eager", "launches": len(W) * steps, "bytes_per_launch": b}), flush=True)
         return
-    g = capture(torch, lambda: [w.forward(x, out=y) for w in W])
-    ms = Timer(torch).replay(g, steps, warmup) / copies
-    print(json.dumps({"mode": "gate", "launches": copies * (steps + warmup + 2), "us_per_launch": round(ms * 1e3, 3),
-                      "GB/s": round(b / (ms * 1e-3) / 1e9, 1)}), flush=True)
+    us, b = gate_timing(torch, rq, synth, dev, steps, warmup)
+    print(json.dumps({"mode": "gate", "launches": GATE_COPIES * (steps + warmup + 2), "us_per_launch": round(us, 3),
+                      "GB/s": round(b / (us * 1e-6) / 1e9, 1)}), flush=True)
+
+
+def mode_prefill(torch, rq, synth, dev, steps):
+    """The four M=512 layer GEMMs of the prefill workload (q/k/o, v,
+    gate/up, down), eager launches (for traces and counters)."""
+    m = 512
+    for qt, n, k in ((rq.Q4_K, 2048, 2048), (rq.Q6_K, 2048, 2048), (rq.Q4_K, 8192, 2048), (rq.Q6_K, 2048, 8192)):
+        w = rq.QWeight(qt, synth.weight_blocks(qt, 7, n, k), n, k)
+        x = torch.randn((m, k), device=dev).to(torch.bfloat16)
+        y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        for _ in range(steps):
+            w.forward(x, out=y)
+        torch.cuda.synchronize()
+        del w
+    print(json.dumps({"mode": "prefill", "launches": 4 * steps}), flush=True)
 
 
 def mode_gemv_large(torch, rq, synth, dev, steps):
@@ -650,7 +676,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--m", type=int, default=16, help="activation rows of --mode verify")
     ap.add_argument("--multi", action="store_true", help="--mode verify through rq_linear_multi")
-    ap.add_argument("--mode", choices=["full", "gate", "copy", "fp8", "prefill-head", "gemv-large", "verify"],
+    ap.add_argument("--mode", choices=["full", "gate", "copy", "fp8", "prefill", "prefill-head", "gemv-large",
+                                       "verify"],
                     default="full",
                     help="gate: only the dominant GEMV; copy: counter calibration copy")
     ap.add_argument("--eager", action="store_true", help="gate mode without a HIP graph")
@@ -673,6 +700,8 @@ def main():
         return mode_copy(torch, dev, args.steps)
     if args.mode == "fp8":
         return mode_fp8(torch, rq, synth, dev, args.steps)
+    if args.mode == "prefill":
+        return mode_prefill(torch, rq, synth, dev, args.steps)
     if args.mode == "prefill-head":
         return mode_prefill_head(torch, rq, synth, dev, args.steps)
     if args.mode == "gemv-large":
@@ -680,12 +709,12 @@ def main():
     if args.mode == "verify":
         return mode_verify(torch, rq, synth, dev, args.steps, args.m, multi=args.multi)
     log(f"decode workload: {args.layers} layer copies, steps={args.steps} warmup={args.warmup}")
-    W, ms, gate_ms = decode_workload(torch, rq, synth, args.layers, args.steps, args.warmup, dev)
+    W, ms = decode_workload(torch, rq, synth, args.layers, args.steps, args.warmup, dev)
     step_bytes = layer_bytes() * args.layers
     value = step_bytes / (ms * 1e-3) / 1e9
-    gate_bytes = 4864 * 896 // 256 * Q4K_BLOCK + 896 * 4 + 4864 * 4
-    gate_gbs = gate_bytes / (gate_ms * 1e-3) / 1e9
-    log(f"decode: {ms:.4f} ms/step, {value:.1f} GB/s; gate GEMV {gate_ms * 1e3:.3f} us, {gate_gbs:.1f} GB/s")
+    gate_us, gate_bytes = gate_timing(torch, rq, synth, dev, max(args.steps, 20), args.warmup)
+    gate_gbs = gate_bytes / (gate_us * 1e-6) / 1e9
+    log(f"decode: {ms:.4f} ms/step, {value:.1f} GB/s; gate GEMV {gate_us:.3f} us, {gate_gbs:.1f} GB/s")
 
     extra = {}
     if not args.no_extras:
@@ -748,9 +777,11 @@ def main():
                      "traffic_source": "stored: profiles/traffic_q4k_gate_gemv.json (rocprofv3 --pmc FETCH_SIZE "
                                        "and WRITE_SIZE runs of bench.py --mode gate --eager, scaled by the same "
                                        "counters on a 512 MiB copy)",
-                     "timing": "HIP events around graph replays of 128 launches on the replay stream",
+                     "timing": f"HIP events around graph replays of {GATE_COPIES} launches on {GATE_COPIES} "
+                               "distinct weights (1.25 GB) on the replay stream, gaps included: the figure "
+                               "bench.py --mode gate prints (profiles/gemv_q4k_gate_4864x896.md)",
                      "kernel": "k_gemv_m1<FmtQ4K,1> (gate/up 4864x896)",
-                     "bytes_per_launch": gate_bytes, "us_per_launch": round(gate_ms * 1e3, 3)},
+                     "bytes_per_launch": gate_bytes, "us_per_launch": round(gate_us, 3)},
         "cpu_baseline": cpu,
         "extra": extra,
     }
