@@ -86,14 +86,16 @@ class Timer:
 
 
 def capture(torch, fn):
+    """fn's launches in a HIP graph, captured on the stream that ran fn once
+    eagerly just before (its library workspace already has the size fn
+    needs, so the graph holds no allocations)."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         fn()
-    torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):
         fn()
     torch.cuda.synchronize()
     return g

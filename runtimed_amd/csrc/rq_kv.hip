@@ -27,6 +27,32 @@ constexpr int KV_THREADS = 256;
 constexpr int KV_MAX_PARTS = 256;
 constexpr int64_t KV_MAX_SLABS_Y = 65535;
 
+// Four elements at i (i % 4 == 0, 16-byte aligned data) as f32: the type a
+// template parameter (TT < 0: the run-time ttype), so that a batch of loads
+// is not split across type branches.
+template <int TT>
+__device__ __forceinline__ float4 ld4t(const void *t, int ttype, int64_t i) {
+  if constexpr (TT < 0) {
+    return load_x4(t, ttype, i);
+  } else if constexpr (TT == RQ_F32) {
+    return *reinterpret_cast<const float4 *>(static_cast<const float *>(t) + i);
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(t) + i);
+    if constexpr (TT == RQ_BF16)
+      return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u), __uint_as_float(v.y << 16),
+                         __uint_as_float(v.y & 0xFFFF0000u));
+    else
+      return make_float4((float)__builtin_bit_cast(_Float16, (uint16_t)(v.x & 0xFFFFu)),
+                         (float)__builtin_bit_cast(_Float16, (uint16_t)(v.x >> 16)),
+                         (float)__builtin_bit_cast(_Float16, (uint16_t)(v.y & 0xFFFFu)),
+                         (float)__builtin_bit_cast(_Float16, (uint16_t)(v.y >> 16)));
+  }
+}
+
+// Loads a thread issues together in the vector loops (one load per loop
+// iteration waited for each load in turn).
+constexpr int KV_U = 4;
+
 __device__ __forceinline__ float block_max(float v, float *red) {
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
@@ -38,7 +64,7 @@ __device__ __forceinline__ float block_max(float v, float *red) {
 // elements (slab-major).  NaN elements are skipped, as the reference's
 // `a > max_abs` test skips them.  VEC: sd and chunk are multiples of 4 and t
 // is 16-byte aligned, so each lane loads 4 elements at once.
-template <bool VEC>
+template <bool VEC, int TT>
 __global__ __launch_bounds__(KV_THREADS) void k_kv_absmax(const void *__restrict__ t, int ttype, int64_t b,
                                                           int64_t h, int64_t sd, int64_t chunk,
                                                           float *__restrict__ part) {
@@ -53,13 +79,22 @@ __global__ __launch_bounds__(KV_THREADS) void k_kv_absmax(const void *__restrict
     const int64_t hi = (e1 < (bb + 1) * sd ? e1 : (bb + 1) * sd) - bb * sd;
     const int64_t base = (bb * h + hh) * sd;
     if (VEC) {
-      for (int64_t i = lo + 4 * threadIdx.x; i < hi; i += 4 * KV_THREADS) {
-        const float4 v = load_x4(t, ttype, base + i);
-        const float a0 = fabsf(v.x), a1 = fabsf(v.y), a2 = fabsf(v.z), a3 = fabsf(v.w);
-        if (a0 > mx) mx = a0;
-        if (a1 > mx) mx = a1;
-        if (a2 > mx) mx = a2;
-        if (a3 > mx) mx = a3;
+      for (int64_t i0 = lo + 4 * threadIdx.x; i0 < hi; i0 += 4 * KV_THREADS * KV_U) {
+        float4 v[KV_U];
+#pragma unroll
+        for (int u = 0; u < KV_U; ++u) {
+          const int64_t i = i0 + 4 * KV_THREADS * u;
+          v[u] = ld4t<TT>(t, ttype, base + (i < hi ? i : i0));  // past the range: a repeat, not counted
+        }
+#pragma unroll
+        for (int u = 0; u < KV_U; ++u) {
+          if (i0 + 4 * KV_THREADS * u >= hi) break;
+          const float a0 = fabsf(v[u].x), a1 = fabsf(v[u].y), a2 = fabsf(v[u].z), a3 = fabsf(v[u].w);
+          if (a0 > mx) mx = a0;
+          if (a1 > mx) mx = a1;
+          if (a2 > mx) mx = a2;
+          if (a3 > mx) mx = a3;
+        }
       }
     } else {
       for (int64_t i = lo + threadIdx.x; i < hi; i += KV_THREADS) {
@@ -85,7 +120,7 @@ __device__ __forceinline__ uint32_t encode_one(float v, float sc) {
 
 // Encode slab `slab` (= batch * h + head), elements [x0, x1) of it.  VEC:
 // sd and per_block are multiples of 4, t is 16-byte and q 8-byte aligned.
-template <int MODE, bool VEC>
+template <int MODE, bool VEC, int TT>
 __global__ __launch_bounds__(KV_THREADS) void k_kv_encode(const void *__restrict__ t, int ttype, int64_t b,
                                                           int64_t h, int64_t sd, const float *__restrict__ part,
                                                           int P, int64_t per_block, void *__restrict__ q,
@@ -101,7 +136,7 @@ __global__ __launch_bounds__(KV_THREADS) void k_kv_encode(const void *__restrict
       _Float16 *o = static_cast<_Float16 *>(q);
       if (VEC) {
         for (int64_t i = x0 + 4 * threadIdx.x; i < x1; i += 4 * KV_THREADS) {
-          const float4 v = load_x4(t, ttype, base + i);
+          const float4 v = ld4t<TT>(t, ttype, base + i);
           *reinterpret_cast<uint2 *>(o + base + i) = make_uint2(pack_f16x2(v.x, v.y), pack_f16x2(v.z, v.w));
         }
       } else {
@@ -116,11 +151,21 @@ __global__ __launch_bounds__(KV_THREADS) void k_kv_encode(const void *__restrict
     if (blockIdx.x == 0 && slab < h && threadIdx.x == 0) scales[hh] = sc;
     uint8_t *o = static_cast<uint8_t *>(q);
     if (VEC) {
-      for (int64_t i = x0 + 4 * threadIdx.x; i < x1; i += 4 * KV_THREADS) {
-        const float4 v = load_x4(t, ttype, base + i);
-        *reinterpret_cast<uint32_t *>(o + base + i) = encode_one<MODE>(v.x, sc) | (encode_one<MODE>(v.y, sc) << 8) |
-                                                      (encode_one<MODE>(v.z, sc) << 16) |
-                                                      (encode_one<MODE>(v.w, sc) << 24);
+      for (int64_t i0 = x0 + 4 * threadIdx.x; i0 < x1; i0 += 4 * KV_THREADS * KV_U) {
+        float4 v[KV_U];
+#pragma unroll
+        for (int u = 0; u < KV_U; ++u) {
+          const int64_t i = i0 + 4 * KV_THREADS * u;
+          v[u] = ld4t<TT>(t, ttype, base + (i < x1 ? i : i0));
+        }
+#pragma unroll
+        for (int u = 0; u < KV_U; ++u) {
+          const int64_t i = i0 + 4 * KV_THREADS * u;
+          if (i >= x1) break;
+          *reinterpret_cast<uint32_t *>(o + base + i) =
+              encode_one<MODE>(v[u].x, sc) | (encode_one<MODE>(v[u].y, sc) << 8) |
+              (encode_one<MODE>(v[u].z, sc) << 16) | (encode_one<MODE>(v[u].w, sc) << 24);
+        }
       }
     } else {
       for (int64_t i = x0 + threadIdx.x; i < x1; i += KV_THREADS)
@@ -189,12 +234,13 @@ bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 template <int MODE>
 void launch_encode(bool vec, dim3 grid, hipStream_t s, const void *t, int ttype, int64_t b, int64_t h, int64_t sd,
                    const float *part, int P, int64_t per, void *q, float *scales) {
-  if (vec)
-    hipLaunchKernelGGL((k_kv_encode<MODE, true>), grid, dim3(KV_THREADS), 0, s, t, ttype, b, h, sd, part, P, per, q,
-                       scales);
-  else
-    hipLaunchKernelGGL((k_kv_encode<MODE, false>), grid, dim3(KV_THREADS), 0, s, t, ttype, b, h, sd, part, P, per,
-                       q, scales);
+#define RQ_KVE(V, TT) \
+  hipLaunchKernelGGL((k_kv_encode<MODE, V, TT>), grid, dim3(KV_THREADS), 0, s, t, ttype, b, h, sd, part, P, per, q, scales)
+  if (!vec) RQ_KVE(false, -1);
+  else if (ttype == RQ_F32) RQ_KVE(true, RQ_F32);
+  else if (ttype == RQ_BF16) RQ_KVE(true, RQ_BF16);
+  else RQ_KVE(true, RQ_F16);
+#undef RQ_KVE
 }
 
 template <int MODE>
@@ -228,12 +274,13 @@ int launch_kv_quantize(const void *t, int ttype, int64_t b, int64_t h, int64_t s
   int rc = RQ_OK;
   float *part = static_cast<float *>(ws.get((size_t)(h * P) * sizeof(float), &rc));
   if (!part) return rc;
-  if (vec)
-    hipLaunchKernelGGL(k_kv_absmax<true>, dim3((unsigned)P, (unsigned)h), dim3(KV_THREADS), 0, s, t, ttype, b, h, sd,
-                       chunk, part);
-  else
-    hipLaunchKernelGGL(k_kv_absmax<false>, dim3((unsigned)P, (unsigned)h), dim3(KV_THREADS), 0, s, t, ttype, b, h,
-                       sd, chunk, part);
+  const dim3 pg((unsigned)P, (unsigned)h);
+#define RQ_KVM(V, TT) hipLaunchKernelGGL((k_kv_absmax<V, TT>), pg, dim3(KV_THREADS), 0, s, t, ttype, b, h, sd, chunk, part)
+  if (!vec) RQ_KVM(false, -1);
+  else if (ttype == RQ_F32) RQ_KVM(true, RQ_F32);
+  else if (ttype == RQ_BF16) RQ_KVM(true, RQ_BF16);
+  else RQ_KVM(true, RQ_F16);
+#undef RQ_KVM
   rc = last_launch("kv absmax");
   if (!rc) {
     if (mode == RQ_KV_FP8) launch_encode<RQ_KV_FP8>(vec, grid, s, t, ttype, b, h, sd, part, (int)P, per, q, scales);

@@ -713,8 +713,11 @@ int dispatch_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hi
 // Launch plan: S workgroups per row tile splitting K, NW waves a workgroup,
 // batches of B chunks, RT row tiles a workgroup.
 //  * Split K when there are few row tiles (k / v / q / o / down of a small
-//    layer: 8 - 72 tiles on 256 CUs): S up to 8, at most 512 workgroups, at
-//    least two chunks a workgroup.
+//    layer: 8 - 72 tiles on 256 CUs) and at least 16 activation rows: S up
+//    to 8, at most 512 workgroups, at least two chunks a workgroup.  Timed
+//    in HIP graphs on the 0.5B layer (7 launches / rq_linear_multi): M = 64
+//    160 -> 195 / 223 -> 287 GB/s, M = 16 238 -> 240 / 343 -> 354, but M = 4
+//    and 8 lose 6-10% (265 -> 242 at M = 4), so smaller M does not split.
 //  * Waves and batch so that one batch of every wave covers the
 //    workgroup's chunks (each batch is a dependent round trip to memory),
 //    within the registers: a batch holds B chunks of every row tile and B
@@ -784,7 +787,7 @@ int run_plan(const rq_weight *const *w, int count, bool set, const void *xv, int
   const uint16_t *x = static_cast<const uint16_t *>(xv);
   int64_t tiles = 0;
   for (int j = 0; j < count; ++j) tiles += (w[j]->n + 15) / 16;
-  SmPlan p = smallm_plan<MT>(tiles, w[0]->k / C::CE, ws != nullptr && tiles <= WsLease::kCounters);
+  SmPlan p = smallm_plan<MT>(tiles, w[0]->k / C::CE, ws != nullptr && tiles <= WsLease::kCounters && m >= 16);
   f32x4 *wsp = nullptr;
   uint32_t *cnt = nullptr;
   if (p.s > 1) {

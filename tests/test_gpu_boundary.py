@@ -291,10 +291,11 @@ def test_small_m_split_k_under_graph_capture(dev, m):
     _replay_check(lambda: w.forward(x, out_dtype=torch.float32), ref)
 
 
-def test_capture_without_warmup_uses_graph_allocations(dev):
+def test_capture_without_warmup(dev):
     # A fresh stream has no workspace yet: under capture the split-K
-    # partials and the aligned copy of x come from allocations recorded in
-    # the graph.
+    # partials and the aligned copy of x come from a buffer allocated outside
+    # the graph (the thread's capture mode relaxed for the allocation), which
+    # the graph then refers to.
     n, k, m = 2048, 8192, 300
     w, _ = make(rq.Q4_K, n, k, 840)
     x = torch.from_numpy(synth.activations(841, m, k)).to(torch.bfloat16).to(dev)
