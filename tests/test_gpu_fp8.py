@@ -52,6 +52,9 @@ def test_per_token_quantize_bit_exact(dev, xdt, k):
     # is not: one workgroup per row, element loads)
     x = torch.from_numpy(synth.activations(11, 33, k) * 3.0).to(xdt)
     x[5] = 0.0
+    x[7, 3] = float("nan")    # rows with NaN or infinity take the software encoder
+    x[9, 1] = float("inf")
+    x[11, 2] = -float("inf")
     xq, xs = rq.fp8_quantize(x.to(dev), rq.FP8_PER_TOKEN)
     want_q, want_s = oracle.fp8_quantize_rows(x.float().numpy())
     assert np.array_equal(xs.cpu().numpy().view(np.uint32), want_s.view(np.uint32))
