@@ -20,6 +20,8 @@
 //
 // Roofline: MFMA-bound for M >= ~300 (bf16 dense peak 2.5 PFLOP/s,
 // flops = 2*m*n*k); HBM-bound below (weight bytes dominate).
+#include <type_traits>
+
 #include "rq_epilogue.h"
 #include "rq_formats.h"
 #include "rq_pipe.h"
@@ -292,6 +294,32 @@ __device__ __forceinline__ void load_a(const uint8_t *const (&src)[4], int64_t s
 
 __device__ __forceinline__ void wait_lds_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// The 256 x 256 tile of a pipelined kernel to y: 16-bit outputs of whole
+// tiles through LDS (the four stages, free after the loop) as full rows,
+// other tiles straight from the accumulators.
+__device__ __forceinline__ void pipe_store(const f32x16 (&acc)[4][4], uint8_t *SM, const Out &o, int64_t m,
+                                           int64_t n, int64_t m0, int64_t n0, int wm, int wn, int lane, int tid) {
+  const bool vec = vec_stores_ok(o.y, n);
+  float bb[4][4];  // biases, loaded before the first store
+#pragma unroll
+  for (int j = 0; j < 4; ++j) tile_col_bias(o, n, n0 + 128 * wn + j * 32, lane, bb[j]);
+  if (o.ytype != RQ_F32 && vec && n % 8 == 0 && m0 + 256 <= m && n0 + 256 <= n) {
+    __syncthreads();  // every wave's stage reads are done
+    const float ones[4][4] = {};
+    stage_block_2b<false>(acc, SM, 128 * wm, 128 * wn, o.ytype, ones, ones, bb, lane);
+    __syncthreads();
+    store_staged_2b(SM, o.y, n, m0, n0, tid);
+    return;
+  }
+  const float one[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  static_for<4>([&](auto I) {
+    static_for<4>([&](auto J) {
+      store_tile32<false>(acc[I][J], o, m, n, m0 + 128 * wm + I * 32, n0 + 128 * wn + J * 32, one, one, bb[J],
+                          nullptr, nullptr, lane, vec);
+    });
+  });
+}
+
 template <class F>
 __global__ __launch_bounds__(256) void k_qgemm_pipe(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
                                                     const uint16_t *__restrict__ x, int64_t m, int64_t n,
@@ -401,25 +429,235 @@ __global__ __launch_bounds__(256) void k_qgemm_pipe(const uint8_t *__restrict__ 
     step(t + 3, std::integral_constant<int, 3>{});
   }
 
-  const bool vec = vec_stores_ok(o.y, n);
-  float bb[4][4];  // biases, loaded before the first store
+  pipe_store(acc, SM, o, m, n, m0, n0, wm, wn, lane, tid);
+}
+
+// ---- pipelined 256 x 256 kernel, Q6_K in chunk pairs ------------------
+//
+// The two 64-element chunks 2j and 2j + 1 of a row (a half super-block,
+// dequant_k.rs:87-111) share their quant bytes: ql byte l holds the low four
+// bits of element l of chunk 2j (nibble 0) and of chunk 2j + 1 (nibble 1),
+// qh byte l the high two bits of both (bits 0-1 / 2-3 for chunk 2j, 4-5 / 6-7
+// for 2j + 1).  k_qgemm_pipe loads a piece's 48 quant bytes once per chunk;
+// here a thread loads them once per pair (ql runs [16 hh, + 16) and
+// [32 + 16 hh, + 16), qh run [16 hh, + 16), the half's eight scales and d)
+// and decodes one 16-weight run of it per K-step: the pair of K-steps
+// 4j .. 4j + 3 is decoded during steps 4j - 2 .. 4j + 1 into the stage of
+// step s + 2, with the decoded values bit-identical to FmtQ6KG's.  Half the
+// load instructions and quant bytes of the per-chunk pieces, and a quarter
+// of the decode work per step instead of half of it on every other step.
+// Pairs alternate between two register slots, so the loop is unrolled by
+// eight steps (k % 256 == 0); everything else is k_qgemm_pipe's.
+struct Q6Pair {
+  u32x4 a, b, h;
+  uint32_t sc0, sc1;  // the half's int8 scales: bytes 0..3 (chunk 2j), 4..7 (chunk 2j + 1)
+  uint32_t d;
+};
+
+__device__ __forceinline__ Q6Pair load_q6_pair(const uint8_t *w, const uint8_t *aux, uint64_t rk, int64_t j,
+                                               int hh) {
+  const uint64_t e = rk + 128u * (uint64_t)j;
+  const uint64_t blk = e >> 8;
+  const int hf = (int)((e >> 7) & 1u);
+  const uint8_t *rec = w + blk * 208u;
+  Q6Pair p;
+  p.a = *reinterpret_cast<const u32x4 *>(rec + 64 * hf + 16 * hh);
+  p.b = *reinterpret_cast<const u32x4 *>(rec + 64 * hf + 32 + 16 * hh);
+  p.h = *reinterpret_cast<const u32x4 *>(rec + 128 + 32 * hf + 16 * hh);
+  const uint2 sc = *reinterpret_cast<const uint2 *>(rec + 192 + 8 * hf);
+  p.sc0 = sc.x;
+  p.sc1 = sc.y;
+  p.d = reinterpret_cast<const uint16_t *>(aux)[blk];
+  return p;
+}
+
+// Run RR of chunk 2j + CC of piece hh: positions 16 hh .. 16 hh + 15 of
+// K-step 4j + 2 CC + RR, as eight bf16 pairs (FmtQ6KG::decode_bf16's words
+// 8 RR .. 8 RR + 7 of that chunk's piece).
+template <int CC, int RR>
+__device__ __forceinline__ void q6_pair_run(const Q6Pair &p, int hh, uint32_t (&o)[8]) {
+  const float d = h2f(p.d);
+  const uint32_t scw = CC ? p.sc1 : p.sc0;
+  const float ds = d * (float)(int8_t)((scw >> (8 * (2 * RR + hh))) & 0xFFu);
+  const float z = -32.0f * ds;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) tile_col_bias(o, n, n0 + 128 * wn + j * 32, lane, bb[j]);
-  if (o.ytype != RQ_F32 && vec && n % 8 == 0 && m0 + 256 <= m && n0 + 256 <= n) {
-    __syncthreads();  // every wave's stage reads are done
-    const float ones[4][4] = {};
-    stage_block_2b<false>(acc, SM, 128 * wm, 128 * wn, o.ytype, ones, ones, bb, lane);
-    __syncthreads();
-    store_staged_2b(SM, o.y, n, m0, n0, tid);
-    return;
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t src = RR ? p.b[j] : p.a[j];
+    const uint32_t hb = p.h[j] >> (4 * CC);
+    const uint32_t q = opaque(((src >> (4 * CC)) & 0x0F0F0F0Fu) |
+                              (RR ? ((hb & 0x0C0C0C0Cu) << 2) : ((hb & 0x03030303u) << 4)));
+    o[2 * j] = pk_bf16(fmaf(ub(q, 0), ds, z), fmaf(ub(q, 1), ds, z));
+    o[2 * j + 1] = pk_bf16(fmaf(ub(q, 2), ds, z), fmaf(ub(q, 3), ds, z));
   }
-  const float one[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+}
+
+// LDS addresses as base registers plus compile-time offsets: stage st of a
+// base sits at (st % 2) * 32768 from it, and the bases of stages 2 and 3 are
+// 65536 above those of 0 and 1 (the offset field holds 16 bits).  Each base
+// folds the lane's row and its swizzled chunk, which do not change between
+// tiles 32 rows apart: (r >> 2) & 3 depends on r % 32 only.
+struct PipeBases {
+  uint32_t rd[2][2][2];  // [stages 2-3][pass H][A, B]: fragment reads
+  uint32_t wa[2];        // [stages 2-3]: activation writes
+  uint32_t wr[2][2];     // [stages 2-3][16-byte chunk q]: weight-run writes
+};
+
+// The 16 MFMAs of one pass on `cur`, reading pass H of stage ST into `nxt`
+// (as mfma_pass).
+template <int ST, int H>
+__device__ __forceinline__ void mfma_pass_o(const Pass &cur, Pass &nxt, const PipeBases &pb, f32x16 (&acc)[4][4]) {
   static_for<4>([&](auto I) {
     static_for<4>([&](auto J) {
-      store_tile32<false>(acc[I][J], o, m, n, m0 + 128 * wm + I * 32, n0 + 128 * wn + J * 32, one, one, bb[J],
-                          nullptr, nullptr, lane, vec);
+      acc[I][J] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16(cur.x[I]), as_bf16(cur.x[4 + J]), acc[I][J], 0, 0,
+                                                          0);
+      if constexpr (J == 0 || J == 2) {
+        constexpr int f = 2 * decltype(I)::value + J / 2;
+        __builtin_amdgcn_sched_barrier(0x6);  // VALU / SALU may cross
+        nxt.x[f] = ds_read16_off<(ST & 1) * P_STAGE + 2048 * (f & 3)>(pb.rd[ST >> 1][H][f >> 2]);
+        __builtin_amdgcn_sched_barrier(0x6);
+      }
     });
   });
+}
+
+template <int ST>
+__device__ __forceinline__ void write_a_o(const PipeBases &pb, const u32x4 (&a)[4]) {
+  static_for<4>([&](auto J) {
+    ds_write16_off<(ST & 1) * P_STAGE + 1024 * decltype(J)::value>(pb.wa[ST >> 1], a[J]);
+  });
+}
+
+// Run words of weight row br (R = 0) or br + 128 (R = 1) into stage ST.
+template <int ST, int R>
+__device__ __forceinline__ void write_run_o(const PipeBases &pb, const uint32_t (&o)[8]) {
+  ds_write16_off<(ST & 1) * P_STAGE + 8192 * R>(pb.wr[ST >> 1][0], (u32x4){o[0], o[1], o[2], o[3]});
+  ds_write16_off<(ST & 1) * P_STAGE + 8192 * R>(pb.wr[ST >> 1][1], (u32x4){o[4], o[5], o[6], o[7]});
+}
+
+__global__ __launch_bounds__(256) void k_q6_pipe(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
+                                                 const uint16_t *__restrict__ x, int64_t m, int64_t n, int64_t k,
+                                                 const Out o) {
+  __shared__ __attribute__((aligned(1024))) uint8_t SM[4 * P_STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  // tile order as in k_qgemm_pipe (XCD x takes the x-th eighth, M fastest)
+  const int64_t gm = gridDim.y, tiles = (int64_t)gridDim.x * gridDim.y;
+  const int64_t b = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+  const int64_t lin = tiles % 8 == 0 ? (b % 8) * (tiles / 8) + b / 8 : b;
+  const int64_t m0 = (lin % gm) * 256, n0 = (lin / gm) * 256;
+  const int64_t nk = k / 32, np = nk / 4;  // K-steps, chunk pairs
+  const int last = (int)nk - 1;
+
+  const uint8_t *asrc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t gr = m0 + 64 * wave + 16 * j + (lane >> 2);
+    asrc[j] = reinterpret_cast<const uint8_t *>(x + (gr < m ? gr : m - 1) * k) + 16 * (lane & 3);
+  }
+  const int hh = tid & 1, br = tid >> 1;
+  const uint64_t rk0 = (uint64_t)(n0 + br < n ? n0 + br : n - 1) * (uint64_t)k;
+  const uint64_t rk1 = (uint64_t)(n0 + br + 128 < n ? n0 + br + 128 : n - 1) * (uint64_t)k;
+
+  PipeBases pb;
+  {
+    const uint32_t s0 = lds_addr(SM);
+    const int l = lane & 31, g = lane >> 5, sw = (l >> 2) & 3;
+    const int ra_ = lane >> 2, swa = (lane >> 4) & 3;
+#pragma unroll
+    for (int hi = 0; hi < 2; ++hi) {
+      const uint32_t sb = s0 + 65536u * hi;
+#pragma unroll
+      for (int H = 0; H < 2; ++H) {
+        pb.rd[hi][H][0] = sb + 8192 * wm + 64 * l + 16 * ((2 * g + H) ^ sw);
+        pb.rd[hi][H][1] = sb + P_B + 8192 * wn + 64 * l + 16 * ((2 * g + H) ^ sw);
+      }
+      pb.wa[hi] = sb + 4096 * wave + 64 * ra_ + 16 * ((lane & 3) ^ swa);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) pb.wr[hi][q] = sb + P_B + 64 * br + 16 * ((2 * hh + q) ^ swz(br));
+    }
+  }
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = (f32x16){0};
+
+  // Prologue: stages 0 and 1 (chunk 0 of pair 0) written, pairs 0 and 1 in
+  // slots 0 and 1, activations of steps 2 and 3 in flight, pass 0 of step 0
+  // read.
+  u32x4 ra[2][4];
+  Q6Pair pp[2][2];  // [slot][row]
+  {
+    u32x4 a0[4], a1[4];
+    load_a(asrc, 0, a0);
+    load_a(asrc, 1, a1);
+    pp[0][0] = load_q6_pair(w, aux, rk0, 0, hh);
+    pp[0][1] = load_q6_pair(w, aux, rk1, 0, hh);
+    load_a(asrc, 2 < nk ? 2 : last, ra[0]);
+    load_a(asrc, 3 < nk ? 3 : last, ra[1]);
+    const int64_t p1 = np > 1 ? 1 : 0;
+    pp[1][0] = load_q6_pair(w, aux, rk0, p1, hh);
+    pp[1][1] = load_q6_pair(w, aux, rk1, p1, hh);
+    write_a_o<0>(pb, a0);
+    write_a_o<1>(pb, a1);
+    uint32_t o[8];
+    q6_pair_run<0, 0>(pp[0][0], hh, o);
+    write_run_o<0, 0>(pb, o);
+    q6_pair_run<0, 0>(pp[0][1], hh, o);
+    write_run_o<0, 1>(pb, o);
+    q6_pair_run<0, 1>(pp[0][0], hh, o);
+    write_run_o<1, 0>(pb, o);
+    q6_pair_run<0, 1>(pp[0][1], hh, o);
+    write_run_o<1, 1>(pb, o);
+  }
+  wait_lds_all();
+  __builtin_amdgcn_s_barrier();
+  Pass P0, P1;
+  static_for<8>([&](auto F) {
+    constexpr int f = decltype(F)::value;
+    P0.x[f] = ds_read16_off<2048 * (f & 3)>(pb.rd[0][0][f >> 2]);
+  });
+  wait_pass(P0);
+
+  // Step s = 8u + B: the run of step s + 2 (pair (s + 2) / 4, chunk
+  // ((s + 2) / 2) % 2, run (s + 2) % 2) from slot ((B + 2) / 4) % 2; slot 0
+  // is free after step 8u + 1 and takes pair 2u + 2, slot 1 after 8u + 5 and
+  // takes pair 2u + 3.
+  auto step = [&](int64_t s, auto Bc) {
+    constexpr int B = decltype(Bc)::value;
+    constexpr int T = (B + 2) & 7, CC = (T >> 1) & 1, RR = T & 1, SLOT = ((B + 2) >> 2) & 1;
+    constexpr int ST = B & 3, ST1 = (B + 1) & 3, ST2 = (B + 2) & 3;
+    __builtin_amdgcn_s_barrier();
+    uint32_t o0[8], o1[8];
+    q6_pair_run<CC, RR>(pp[SLOT][0], hh, o0);
+    q6_pair_run<CC, RR>(pp[SLOT][1], hh, o1);
+    mfma_pass_o<ST, 1>(P0, P1, pb, acc);
+    wait_pass(P1);
+    mfma_pass_o<ST1, 0>(P1, P0, pb, acc);
+    write_a_o<ST2>(pb, ra[B & 1]);
+    load_a(asrc, s + 4 < nk ? s + 4 : last, ra[B & 1]);
+    write_run_o<ST2, 0>(pb, o0);
+    write_run_o<ST2, 1>(pb, o1);
+    if constexpr (B == 1 || B == 5) {
+      const int64_t jn = (s + 7) >> 2 < np ? (s + 7) >> 2 : np - 1;
+      pp[B == 1 ? 0 : 1][0] = load_q6_pair(w, aux, rk0, jn, hh);
+      pp[B == 1 ? 0 : 1][1] = load_q6_pair(w, aux, rk1, jn, hh);
+    }
+    wait_pass(P0);
+    wait_lds_all();
+  };
+  for (int64_t t = 0; t < nk; t += 8) {
+    step(t, std::integral_constant<int, 0>{});
+    step(t + 1, std::integral_constant<int, 1>{});
+    step(t + 2, std::integral_constant<int, 2>{});
+    step(t + 3, std::integral_constant<int, 3>{});
+    step(t + 4, std::integral_constant<int, 4>{});
+    step(t + 5, std::integral_constant<int, 5>{});
+    step(t + 6, std::integral_constant<int, 6>{});
+    step(t + 7, std::integral_constant<int, 7>{});
+  }
+  pipe_store(acc, SM, o, m, n, m0, n0, wm, wn, lane, tid);
 }
 
 // y = sum over s < splits of part[s] (f32 partials of m * n outputs), with
@@ -475,8 +713,12 @@ int launch(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStrea
 template <class F>
 int launch_pipe(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s) {
   const dim3 grid((unsigned)((wt->n + 255) / 256), (unsigned)((m + 255) / 256));
-  hipLaunchKernelGGL((k_qgemm_pipe<F>), grid, dim3(256), 0, s, wt->data, wt->data + wt->aux_off,
-                     static_cast<const uint16_t *>(x), m, wt->n, wt->k, o);
+  if (std::is_same<F, FmtQ6KG>::value && wt->k % 256 == 0)
+    hipLaunchKernelGGL(k_q6_pipe, grid, dim3(256), 0, s, wt->data, wt->data + wt->aux_off,
+                       static_cast<const uint16_t *>(x), m, wt->n, wt->k, o);
+  else
+    hipLaunchKernelGGL((k_qgemm_pipe<F>), grid, dim3(256), 0, s, wt->data, wt->data + wt->aux_off,
+                       static_cast<const uint16_t *>(x), m, wt->n, wt->k, o);
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemm launch failed");
 }
 

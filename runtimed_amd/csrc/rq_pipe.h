@@ -46,6 +46,27 @@ __device__ __forceinline__ void ds_write16(uint8_t *p, u32x4 v) {
   asm volatile("ds_write_b128 %0, %1" : : "v"(off), "v"(v));
 }
 
+// The same at a byte offset known at compile time (the instruction's 16-bit
+// offset field): one base register serves every stage and tile at a fixed
+// distance from it.
+template <int OFF>
+__device__ __forceinline__ u32x4 ds_read16_off(uint32_t base) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(base), "i"(OFF));
+  return v;
+}
+
+template <int OFF>
+__device__ __forceinline__ void ds_write16_off(uint32_t base, u32x4 v) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  asm volatile("ds_write_b128 %0, %1 offset:%2" : : "v"(base), "v"(v), "i"(OFF));
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
 // Fragment registers of one K-step: 8 x 16 bytes of A rows, 8 of B rows.
 struct Frags {
   u32x4 x[16];

@@ -88,3 +88,9 @@ def test_fp8_pipe_lds_reads_complete_before_use(tmp_path):
 def test_qgemm_pipe_lds_reads_complete_before_use(tmp_path):
     # one kernel per GGUF format; 8 reads of the first pass plus 16 per step
     _check(tmp_path, "rq_gemm.hip", "k_qgemm_pipe", 24)
+
+
+@pytest.mark.skipif(not HAVE_HIPCC, reason="hipcc not present")
+def test_q6_pipe_lds_reads_complete_before_use(tmp_path):
+    # the Q6_K chunk-pair kernel: reads at base registers plus offsets
+    _check(tmp_path, "rq_gemm.hip", "k_q6_pipe", 24)
