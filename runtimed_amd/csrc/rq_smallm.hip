@@ -318,6 +318,88 @@ __device__ __forceinline__ void load_xh(XFragH<MT> &f, const uint16_t *const (&x
   }
 }
 
+// ---- activations staged in LDS ----
+//
+// The workgroup's slice of x -- rows 0 .. m - 1, elements [e0, e0 + ke) --
+// is copied into LDS once with coalesced 16-byte loads (consecutive threads
+// read consecutive 16 bytes of a row) at a row stride of xstr bytes (the
+// longest slice of the launch plus 16 bytes, so the 16 rows of one fragment
+// read start on different bank groups).  The MFMA B fragments are then LDS
+// reads at the positions the global fragment loads use.  Loaded per lane
+// from global memory, each fragment instruction gathers 16-byte pieces of
+// 16 rows from 32 cache lines, and that, not the decode, set the kernel's
+// time (the same kernel without decode and MFMAs ran within 5% of it).
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+__device__ __forceinline__ u32x4 ds_read16(const uint8_t *p) {
+  return *reinterpret_cast<const lds_u32x4 *>((const __attribute__((address_space(3))) uint8_t *)p);
+}
+__device__ __forceinline__ void ds_write16(uint8_t *p, u32x4 v) {
+  *reinterpret_cast<lds_u32x4 *>((__attribute__((address_space(3))) uint8_t *)p) = v;
+}
+
+struct XSlice {
+  const uint8_t *row[4];  // this lane's LDS row of each column tile, at its lane group's offset
+};
+
+template <int MT>
+__device__ __forceinline__ void lds_xh(XFragH<MT> &f, const XSlice &xs, int64_t tl) {
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) {
+    const uint8_t *p = xs.row[ct] + 256 * tl;
+    f.v[ct][0] = ds_read16(p);
+    f.v[ct][1] = ds_read16(p + 16);
+    f.v[ct][2] = ds_read16(p + 64);
+    f.v[ct][3] = ds_read16(p + 80);
+  }
+}
+
+template <int MT>
+__device__ __forceinline__ void lds_x(XFrag<MT> &f, const XSlice &xs, int64_t tl) {
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) {
+    const uint8_t *p = xs.row[ct] + 128 * tl;
+    f.a[ct] = ds_read16(p);
+    f.b[ct] = ds_read16(p + 64);
+  }
+}
+
+// Piece p (16 bytes) of the slice: row p / ppr, piece p % ppr of the row;
+// indices past the end repeat the last piece (the same bytes to the same
+// place).  The row comes from a float reciprocal: (p + 1/2) / ppr is at
+// least 1 / (2 ppr) away from an integer, far above the rounding error for
+// p < 2^20.
+struct XStage {
+  const uint16_t *x;
+  int64_t k, e0;
+  int ppr, total, xstr;
+  float inv;
+  __device__ __forceinline__ void at(int p, int &r, int &c) const {
+    p = p < total ? p : total - 1;
+    r = (int)(((float)p + 0.5f) * inv);
+    c = p - r * ppr;
+  }
+};
+
+template <int NT, int XR>
+__device__ __forceinline__ void xs_load(u32x4 (&v)[XR], const XStage &st, int base) {
+#pragma unroll
+  for (int i = 0; i < XR; ++i) {
+    int r, c;
+    st.at(base + i * NT + (int)threadIdx.x, r, c);
+    v[i] = *reinterpret_cast<const u32x4 *>(st.x + r * st.k + st.e0 + 8 * c);
+  }
+}
+
+template <int NT, int XR>
+__device__ __forceinline__ void xs_store(uint8_t *xs, const u32x4 (&v)[XR], const XStage &st, int base) {
+#pragma unroll
+  for (int i = 0; i < XR; ++i) {
+    int r, c;
+    st.at(base + i * NT + (int)threadIdx.x, r, c);
+    ds_write16(xs + r * st.xstr + 16 * c, v[i]);
+  }
+}
+
 template <int MT>
 __device__ __forceinline__ void mma_chunk_h(const FmtQ4K::Piece &pc, const XFragH<MT> &xf, f32x4 (&acc)[MT],
                                             uint32_t vm) {
@@ -373,10 +455,22 @@ __device__ __forceinline__ void store_slot(const f32x4 &v, int rt, int ct, int l
                                            const Out &o) {
   const int64_t mr = 16 * ct + (l & 15);
   if (mr < m) {
+    const int64_t nr0 = n0 + 16 * rt + 4 * (l >> 4);
+    float r[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t nr = n0 + 16 * rt + 4 * (l >> 4) + i;
-      if (nr < n) store_one(o.y, o.ytype, mr * n + nr, o.bias ? with_bias(v[i], bias_at(o, nr), o.ytype) : v[i]);
+      const int64_t nr = nr0 + i < n ? nr0 + i : n - 1;
+      r[i] = o.bias ? with_bias(v[i], bias_at(o, nr), o.ytype) : v[i];
+    }
+    // The lane's four outputs are consecutive columns of one row: one 16-byte
+    // (f32) or 8-byte store where the row holds all four and the addresses
+    // are aligned (2-byte stores one by one cost ~0.7 us of a 5 us launch).
+    if (nr0 + 3 < n && vec_stores_ok(o.y, n)) {
+      store_four(o.y, o.ytype, mr * n + nr0, r[0], r[1], r[2], r[3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (nr0 + i < n) store_one(o.y, o.ytype, mr * n + nr0 + i, r[i]);
     }
   }
 }
@@ -460,19 +554,25 @@ __device__ __forceinline__ void reduce_split(f32x4 (&part)[NW][1][MT][64], const
 // MT column tiles of 16 activation rows (M <= 16 MT) and RT row tiles of 16
 // weight rows per workgroup; NW waves split the workgroup's chunks
 // [lo, hi) of K, wave w taking chunks lo + w, lo + w + NW, ...  A wave issues
-// the loads of B chunks (the weights of every row tile and the activations,
-// once for all RT row tiles) at once, then decodes and multiplies them: an
-// activation fragment serves RT row tiles, so a workgroup reads its slice
-// of x once per 16 RT weight rows.  The loop body has no conditional work:
-// a load whose result is used under a branch is sunk into the branch and
-// waited for there, and a prefetch carried from one iteration to the next is
-// merged back into a load at the loop top.  Chunks past the end load a valid
-// chunk again and are masked.
-template <class C, int MT, int NW, int B, int RT>
+// the loads of B chunks (the weights of every row tile) at once, then
+// decodes and multiplies them.  With XL the workgroup's slice of x is first
+// copied into LDS (xs, row stride xstr; the loads of the first batch of
+// weights are issued right behind the copy's loads, so both are in flight
+// together) and the B fragments are LDS reads; without it each wave loads
+// its fragments from global memory with the weights (slices too long for
+// LDS).  An activation fragment serves RT row tiles.  The loop body has no
+// conditional work: a load whose result is used under a branch is sunk into
+// the branch and waited for there, and a prefetch carried from one
+// iteration to the next is merged back into a load at the loop top.  Chunks
+// past the end load a valid chunk again and are masked; so does a wave with
+// no chunk in the slice when x is in LDS (it still joins the copy and the
+// barrier); without LDS such a wave skips the work.
+template <class C, int MT, int NW, int B, int RT, bool XL>
 __device__ __forceinline__ void smallm_tiles(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
                                              const uint16_t *__restrict__ x, int64_t m, const Out &o, int64_t n,
                                              int64_t k, int64_t tile, int S, int s, f32x4 *__restrict__ wsp,
-                                             uint32_t *__restrict__ cnt, f32x4 (&part)[NW][RT][MT][64]) {
+                                             uint32_t *__restrict__ cnt, f32x4 (&part)[NW][RT][MT][64],
+                                             uint8_t *xs, int xstr) {
   const int lane = threadIdx.x & 63, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t n0 = tile * 16 * RT;
@@ -483,17 +583,9 @@ __device__ __forceinline__ void smallm_tiles(const uint8_t *__restrict__ w, cons
     row[rt] = r < n ? r : n - 1;
   }
   constexpr bool HALF = C::CE == 128;
+  typedef typename std::conditional<HALF, XFragH<MT>, XFrag<MT>>::type XF;
   const int64_t nk = k / C::CE, cps = (nk + S - 1) / S;
   const int64_t lo = s * cps, hi = lo + cps < nk ? lo + cps : nk;
-
-  // Activation rows of this lane in each column tile (rows past m read row
-  // m - 1; their results are not stored).
-  const uint16_t *xr[MT];
-#pragma unroll
-  for (int ct = 0; ct < MT; ++ct) {
-    const int64_t mr = 16 * ct + (lane & 15);
-    xr[ct] = x + (mr < m ? mr : m - 1) * k + (HALF ? 64 * (g >> 1) + 16 * (g & 1) : 8 * g);
-  }
 
   f32x4 acc[RT][MT];
 #pragma unroll
@@ -501,28 +593,91 @@ __device__ __forceinline__ void smallm_tiles(const uint8_t *__restrict__ w, cons
 #pragma unroll
     for (int ct = 0; ct < MT; ++ct) acc[rt][ct] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
-  // (a workgroup whose slice is empty, lo >= hi, still joins the count)
-  for (int64_t t = lo + wave; t < hi; t += B * NW) {
-    typename C::Chunk c[B][RT];
-    typename std::conditional<HALF, XFragH<MT>, XFrag<MT>>::type xf[B];
+  // Activation rows of this lane in each column tile (rows past m read row
+  // m - 1; their results are not stored), at its lane group's offset.
+  const int xo = HALF ? 64 * (g >> 1) + 16 * (g & 1) : 8 * g;  // elements
+  const uint16_t *xr[MT];
+  XSlice xsl;
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) {
+    const int64_t mr = 16 * ct + (lane & 15) < m ? 16 * ct + (lane & 15) : m - 1;
+    xr[ct] = x + mr * k + xo;
+    if constexpr (XL) xsl.row[ct] = xs + mr * xstr + 2 * xo;
+  }
+
+  auto load_batch = [&](int64_t t, typename C::Chunk (&c)[B][RT], XF (&xf)[B]) {
 #pragma unroll
     for (int i = 0; i < B; ++i) {
-      const int64_t ti = t + i * NW < hi ? t + i * NW : t;
+      const int64_t ti = t + i * NW < hi ? t + i * NW : (t < hi ? t : lo);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) c[i][rt] = C::load(w, aux, row[rt], k, ti, g);
-      if constexpr (HALF) load_xh<MT>(xf[i], xr, ti);
-      else load_x<MT>(xf[i], xr, ti);
+      if constexpr (!XL) {
+        if constexpr (HALF) load_xh<MT>(xf[i], xr, ti);
+        else load_x<MT>(xf[i], xr, ti);
+      }
     }
-    // Keep every load of the batch ahead of the first use (the scheduler
-    // would otherwise trade loads in flight for registers).
-    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto run_batch = [&](int64_t t, const typename C::Chunk (&c)[B][RT], XF (&xf)[B]) {
 #pragma unroll
     for (int i = 0; i < B; ++i) {
-      const uint32_t vm = i == 0 ? 0xFFFFFFFFu : opaque(t + i * NW < hi ? 0xFFFFFFFFu : 0u);
+      const int64_t ti = t + i * NW < hi ? t + i * NW : (t < hi ? t : lo);
+      if constexpr (XL) {
+        if constexpr (HALF) lds_xh<MT>(xf[i], xsl, ti - lo);
+        else lds_x<MT>(xf[i], xsl, ti - lo);
+      }
+      const uint32_t vm = (!XL && i == 0) ? 0xFFFFFFFFu : opaque(t + i * NW < hi ? 0xFFFFFFFFu : 0u);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         if constexpr (HALF) mma_chunk_h<MT>(c[i][rt], xf[i], acc[rt], vm);
         else mma_chunk<C, MT>(c[i][rt], xf[i], acc[rt], g, vm);
+      }
+    }
+  };
+
+  // (a workgroup whose slice is empty, lo >= hi, still joins the count)
+  if (lo < hi) {
+    const int64_t t0 = lo + wave;
+    if constexpr (XL) {
+      constexpr int NT = 64 * NW, XR = 8;
+      XStage st;
+      st.x = x;
+      st.k = k;
+      st.e0 = lo * C::CE;
+      st.ppr = (int)((hi - lo) * C::CE / 8);
+      st.total = (int)m * st.ppr;
+      st.xstr = xstr;
+      st.inv = 1.0f / (float)st.ppr;
+      u32x4 v[XR];
+      xs_load<NT, XR>(v, st, 0);
+      __builtin_amdgcn_sched_barrier(0);  // the copy's loads first: its wait then skips the weights
+      typename C::Chunk c0[B][RT];
+      XF xf0[B];
+      load_batch(t0, c0, xf0);
+      // the copy's loads and the first weight loads are all in flight here
+      __builtin_amdgcn_sched_barrier(0);
+      xs_store<NT, XR>(xs, v, st, 0);
+      for (int base = XR * NT; base < st.total; base += XR * NT) {
+        xs_load<NT, XR>(v, st, base);
+        xs_store<NT, XR>(xs, v, st, base);
+      }
+      __syncthreads();
+      run_batch(t0, c0, xf0);
+      for (int64_t t = t0 + B * NW; t < hi; t += B * NW) {
+        typename C::Chunk c[B][RT];
+        XF xf[B];
+        load_batch(t, c, xf);
+        __builtin_amdgcn_sched_barrier(0);
+        run_batch(t, c, xf);
+      }
+    } else {
+      for (int64_t t = t0; t < hi; t += B * NW) {
+        typename C::Chunk c[B][RT];
+        XF xf[B];
+        load_batch(t, c, xf);
+        // Keep every load of the batch ahead of the first use (the scheduler
+        // would otherwise trade loads in flight for registers).
+        __builtin_amdgcn_sched_barrier(0);
+        run_batch(t, c, xf);
       }
     }
   }
@@ -551,31 +706,33 @@ __device__ __forceinline__ int split_order(int b, int grid, int S) {
 
 // One weight: workgroup b takes row tiles [(b / S) RT, + RT), K slice b % S
 // (split partials at wsp + (b / S) S MT 64, counters cnt[b / S]).
-template <class C, int MT, int NW, int B, int RT>
+template <class C, int MT, int NW, int B, int RT, bool XL>
 __global__ __launch_bounds__(64 * NW) void k_smallm(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
                                                     const uint16_t *__restrict__ x, int64_t m, const Out o,
                                                     int64_t n, int64_t k, int S, f32x4 *__restrict__ wsp,
-                                                    uint32_t *__restrict__ cnt) {
+                                                    uint32_t *__restrict__ cnt, int xstr) {
   __shared__ f32x4 part[NW][RT][MT][64];
+  extern __shared__ __attribute__((aligned(16))) uint8_t xs_dyn[];
   const int bid = split_order((int)blockIdx.x, (int)gridDim.x, S);
   const int64_t tile = bid / S;
-  smallm_tiles<C, MT, NW, B, RT>(w, aux, x, m, o, n, k, tile, S, bid % S, wsp + tile * S * MT * 64, cnt + tile,
-                                 part);
+  smallm_tiles<C, MT, NW, B, RT, XL>(w, aux, x, m, o, n, k, tile, S, bid % S, wsp + tile * S * MT * 64, cnt + tile,
+                                     part, xs_dyn, xstr);
 }
 
 // A set of weights sharing x (pick_entry chooses this workgroup's weight;
 // every entry's workgroups are a multiple of S, so b / S numbers the tiles
 // of the whole set).
-template <class C, int MT, int NW, int B, int RT>
+template <class C, int MT, int NW, int B, int RT, bool XL>
 __global__ __launch_bounds__(64 * NW) void k_smallm_set(const WeightSet set, const uint16_t *__restrict__ x,
                                                         int64_t m, int64_t k, int S, f32x4 *__restrict__ wsp,
-                                                        uint32_t *__restrict__ cnt) {
+                                                        uint32_t *__restrict__ cnt, int xstr) {
   __shared__ f32x4 part[NW][RT][MT][64];
+  extern __shared__ __attribute__((aligned(16))) uint8_t xs_dyn[];
   const int bid = split_order((int)blockIdx.x, (int)gridDim.x, S);
   const SetEntry e = pick_entry(set, bid);
   const int gt = bid / S;
-  smallm_tiles<C, MT, NW, B, RT>(e.w, e.aux, x, m, e.o, e.n, k, (bid - e.g0) / S, S, bid % S,
-                                 wsp + (int64_t)gt * S * MT * 64, cnt + gt, part);
+  smallm_tiles<C, MT, NW, B, RT, XL>(e.w, e.aux, x, m, e.o, e.n, k, (bid - e.g0) / S, S, bid % S,
+                                     wsp + (int64_t)gt * S * MT * 64, cnt + gt, part, xs_dyn, xstr);
 }
 
 // ---- f32 / f16 activations ------------------------------------------------
@@ -725,6 +882,10 @@ int dispatch_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hi
 //    a lane.
 //  * Row tiles: with four waves and no split, as many as keep at least 256
 //    workgroups (each workgroup reads its slice of x once).
+// Largest LDS copy of the activation slice (beside the reduction buffer of
+// at most 32 KB, within the 160 KB of a CU).
+constexpr size_t kSmXsMax = 120 * 1024;
+
 struct SmPlan {
   int s, nw, b, rt;
 };
@@ -751,22 +912,40 @@ SmPlan smallm_plan(int64_t tiles, int64_t nk, bool can_split) {
   return p;
 }
 
-template <class C, int MT, int NW, int B, int RT>
+// Dynamic LDS of a kernel instantiation above 64 KB is asked for once.
+template <auto KERNEL>
+bool lds_allow(size_t bytes) {
+  if (bytes <= 65536) return true;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void *>(KERNEL), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)kSmXsMax);
+  if (attr != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return true;
+}
+
+template <class C, int MT, int NW, int B, int RT, bool XL>
 int launch_mt(const rq_weight *const *w, int count, bool set, const uint16_t *x, int64_t m, const Out *o, int S,
-              f32x4 *wsp, uint32_t *cnt, hipStream_t s) {
+              f32x4 *wsp, uint32_t *cnt, hipStream_t s, int xstr, size_t xbytes) {
+  // the reduction buffer and the activation slice share the CU's 160 KB
+  if (XL && (size_t)NW * RT * MT * 64 * sizeof(f32x4) + xbytes > 160 * 1024) return RQ_E_UNSUPPORTED;
   if (!set) {
     const rq_weight *wt = w[0];
     const int64_t tiles = ((wt->n + 15) / 16 + RT - 1) / RT;
-    hipLaunchKernelGGL((k_smallm<C, MT, NW, B, RT>), dim3((unsigned)(tiles * S)), dim3(64 * NW), 0, s, wt->data,
-                       wt->data + wt->aux_off, x, m, o[0], wt->n, wt->k, S, wsp, cnt);
+    if (!lds_allow<&k_smallm<C, MT, NW, B, RT, XL>>(xbytes)) return RQ_E_UNSUPPORTED;
+    hipLaunchKernelGGL((k_smallm<C, MT, NW, B, RT, XL>), dim3((unsigned)(tiles * S)), dim3(64 * NW), xbytes, s,
+                       wt->data, wt->data + wt->aux_off, x, m, o[0], wt->n, wt->k, S, wsp, cnt, xstr);
   } else {
     WeightSet ws;
     int64_t total = 0;
     const int rc = fill_set(ws, w, count, o, [&](const rq_weight *wj) { return ((wj->n + 15) / 16 + RT - 1) / RT * S; },
                             &total);
     if (rc) return rc;
-    hipLaunchKernelGGL((k_smallm_set<C, MT, NW, B, RT>), dim3((unsigned)total), dim3(64 * NW), 0, s, ws, x, m,
-                       w[0]->k, S, wsp, cnt);
+    if (!lds_allow<&k_smallm_set<C, MT, NW, B, RT, XL>>(xbytes)) return RQ_E_UNSUPPORTED;
+    hipLaunchKernelGGL((k_smallm_set<C, MT, NW, B, RT, XL>), dim3((unsigned)total), dim3(64 * NW), xbytes, s, ws, x,
+                       m, w[0]->k, S, wsp, cnt, xstr);
   }
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "small-M launch failed");
 }
@@ -798,7 +977,27 @@ int run_plan(const rq_weight *const *w, int count, bool set, const void *xv, int
   }
   // (a half-block chunk holds twice the weights and activations of a
   // 64-element chunk: smaller batches where registers are short)
-#define RQ_SM(NW, B, RT) return launch_mt<C, MT, NW, sm_batch<C, MT, NW, B>(), RT>(w, count, set, x, m, o, p.s, wsp, cnt, s)
+  // The activation slice in LDS (the longest slice of the launch, m rows)
+  // for 16 or more activation rows of up to 2048 elements, where it fits
+  // beside the reduction buffer.  Timed in HIP graphs (Q4_K, bf16, distinct
+  // weights): 4864 x 896 M = 16 5.41 -> 4.84 us, M = 64 10.86 -> 9.79,
+  // 896 x 896 M = 64 6.32 -> 5.61; slower at M = 4 / 8 (the fragments are
+  // few) and on 896 x 4864 at M = 64 (eight K slices of 83 KB each leave one
+  // workgroup per CU: 11.3 -> 14.8 us).
+  const int64_t cps = (w[0]->k / C::CE + p.s - 1) / p.s;
+  const int xstr = (int)(cps * C::CE * 2 + 16);
+  const size_t xbytes = (size_t)m * (size_t)xstr;
+  const bool xl = m >= 16 && w[0]->k <= 2048 && xbytes <= kSmXsMax;
+#define RQ_SM(NW, B, RT)                                                                                     \
+  {                                                                                                          \
+    if (xl) {                                                                                                \
+      const int rc_ = launch_mt<C, MT, NW, sm_batch<C, MT, NW, B>(), RT, true>(w, count, set, x, m, o, p.s, wsp, \
+                                                                              cnt, s, xstr, xbytes);        \
+      if (rc_ != RQ_E_UNSUPPORTED) return rc_;                                                               \
+    }                                                                                                        \
+    return launch_mt<C, MT, NW, sm_batch<C, MT, NW, B>(), RT, false>(w, count, set, x, m, o, p.s, wsp, cnt, s, 0, \
+                                                                     0);                                    \
+  }
   if constexpr (MT == 4) {
     if (p.nw == 16) RQ_SM(16, 1, 1);
     if (p.nw == 8) RQ_SM(8, 1, 1);

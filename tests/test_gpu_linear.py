@@ -133,9 +133,13 @@ def test_verify_small_m_bf16(dev, qtype, m):
 # (m = 3, 17, 33, 63), weight rows not a multiple of 16, fewer K-chunks than
 # waves (k = 64, 128), rows straddling super-blocks (k = 896), long K in
 # several batches a wave (k = 1088, 4864, 8192), and bf16 / f16 outputs.
+# From 16 rows with k <= 2048 the activation slice is copied to LDS: in
+# several rounds of the copy (64 x 2048), with K split over workgroups
+# (256 rows: 16 row tiles, eight slices) and unsplit (2048 rows).
 @pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0])
 @pytest.mark.parametrize("m,n,k", [(3, 37, 256), (17, 130, 128), (33, 100, 896), (63, 200, 64), (5, 4864, 896),
-                                   (3, 130, 4864), (33, 40, 8192), (17, 96, 1088)])
+                                   (3, 130, 4864), (33, 40, 8192), (17, 96, 1088), (64, 256, 2048),
+                                   (16, 2048, 2048), (40, 2048, 1024)])
 def test_small_m_edges(dev, qtype, m, n, k):
     w, wf = make(qtype, n, k, 31 + m + n)
     xb = torch.from_numpy(synth.activations(6 + m, m, k)).to(torch.bfloat16)
