@@ -369,8 +369,8 @@ __device__ __forceinline__ void lds_x(XFrag<MT> &f, const XSlice &xs, int64_t tl
 // least 1 / (2 ppr) away from an integer, far above the rounding error for
 // p < 2^20.
 struct XStage {
-  const uint16_t *x;
-  int64_t k, e0;
+  const uint8_t *x;  // the slice's first byte of row 0
+  int64_t rb;        // row stride of x in bytes
   int ppr, total, xstr;
   float inv;
   __device__ __forceinline__ void at(int p, int &r, int &c) const {
@@ -386,7 +386,7 @@ __device__ __forceinline__ void xs_load(u32x4 (&v)[XR], const XStage &st, int ba
   for (int i = 0; i < XR; ++i) {
     int r, c;
     st.at(base + i * NT + (int)threadIdx.x, r, c);
-    v[i] = *reinterpret_cast<const u32x4 *>(st.x + r * st.k + st.e0 + 8 * c);
+    v[i] = *reinterpret_cast<const u32x4 *>(st.x + r * st.rb + 16 * c);
   }
 }
 
@@ -398,6 +398,29 @@ __device__ __forceinline__ void xs_store(uint8_t *xs, const u32x4 (&v)[XR], cons
     st.at(base + i * NT + (int)threadIdx.x, r, c);
     ds_write16(xs + r * st.xstr + 16 * c, v[i]);
   }
+}
+
+// The rest of the copy after its first round (loaded by the caller ahead of
+// other loads), then the workgroup barrier.
+template <int NT, int XR>
+__device__ __forceinline__ void xs_finish(uint8_t *xs, u32x4 (&v)[XR], const XStage &st) {
+  xs_store<NT, XR>(xs, v, st, 0);
+  for (int base = XR * NT; base < st.total; base += XR * NT) {
+    xs_load<NT, XR>(v, st, base);
+    xs_store<NT, XR>(xs, v, st, base);
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ XStage make_stage(const uint8_t *x, int64_t rb, int64_t m, int64_t slice_bytes, int xstr) {
+  XStage st;
+  st.x = x;
+  st.rb = rb;
+  st.ppr = (int)(slice_bytes / 16);
+  st.total = (int)m * st.ppr;
+  st.xstr = xstr;
+  st.inv = 1.0f / (float)st.ppr;
+  return st;
 }
 
 template <int MT>
@@ -639,14 +662,8 @@ __device__ __forceinline__ void smallm_tiles(const uint8_t *__restrict__ w, cons
     const int64_t t0 = lo + wave;
     if constexpr (XL) {
       constexpr int NT = 64 * NW, XR = 8;
-      XStage st;
-      st.x = x;
-      st.k = k;
-      st.e0 = lo * C::CE;
-      st.ppr = (int)((hi - lo) * C::CE / 8);
-      st.total = (int)m * st.ppr;
-      st.xstr = xstr;
-      st.inv = 1.0f / (float)st.ppr;
+      const XStage st = make_stage(reinterpret_cast<const uint8_t *>(x + lo * C::CE), 2 * k, m,
+                                   2 * (hi - lo) * C::CE, xstr);
       u32x4 v[XR];
       xs_load<NT, XR>(v, st, 0);
       __builtin_amdgcn_sched_barrier(0);  // the copy's loads first: its wait then skips the weights
@@ -655,12 +672,7 @@ __device__ __forceinline__ void smallm_tiles(const uint8_t *__restrict__ w, cons
       load_batch(t0, c0, xf0);
       // the copy's loads and the first weight loads are all in flight here
       __builtin_amdgcn_sched_barrier(0);
-      xs_store<NT, XR>(xs, v, st, 0);
-      for (int base = XR * NT; base < st.total; base += XR * NT) {
-        xs_load<NT, XR>(v, st, base);
-        xs_store<NT, XR>(xs, v, st, base);
-      }
-      __syncthreads();
+      xs_finish<NT, XR>(xs, v, st);
       run_batch(t0, c0, xf0);
       for (int64_t t = t0 + B * NW; t < hi; t += B * NW) {
         typename C::Chunk c[B][RT];
@@ -733,6 +745,24 @@ __global__ __launch_bounds__(64 * NW) void k_smallm_set(const WeightSet set, con
   const int gt = bid / S;
   smallm_tiles<C, MT, NW, B, RT, XL>(e.w, e.aux, x, m, e.o, e.n, k, (bid - e.g0) / S, S, bid % S,
                                      wsp + (int64_t)gt * S * MT * 64, cnt + gt, part, xs_dyn, xstr);
+}
+
+// Largest LDS copy of the activation slice (beside the reduction buffer of
+// at most 32 KB, within the 160 KB of a CU).
+constexpr size_t kSmXsMax = 120 * 1024;
+
+// Dynamic LDS of a kernel instantiation above 64 KB is asked for once.
+template <auto KERNEL>
+bool lds_allow(size_t bytes) {
+  if (bytes <= 65536) return true;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void *>(KERNEL), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)kSmXsMax);
+  if (attr != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return true;
 }
 
 // ---- f32 / f16 activations ------------------------------------------------
@@ -882,10 +912,6 @@ int dispatch_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hi
 //    a lane.
 //  * Row tiles: with four waves and no split, as many as keep at least 256
 //    workgroups (each workgroup reads its slice of x once).
-// Largest LDS copy of the activation slice (beside the reduction buffer of
-// at most 32 KB, within the 160 KB of a CU).
-constexpr size_t kSmXsMax = 120 * 1024;
-
 struct SmPlan {
   int s, nw, b, rt;
 };
@@ -910,20 +936,6 @@ SmPlan smallm_plan(int64_t tiles, int64_t nk, bool can_split) {
   const bool rt_ok = S == 1 && p.nw == 4 && p.b == (MT == 4 ? 1 : 4);
   if (rt_ok) p.rt = tiles >= 4 * 256 ? 4 : (tiles >= 2 * 256 ? 2 : 1);
   return p;
-}
-
-// Dynamic LDS of a kernel instantiation above 64 KB is asked for once.
-template <auto KERNEL>
-bool lds_allow(size_t bytes) {
-  if (bytes <= 65536) return true;
-  static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void *>(KERNEL), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)kSmXsMax);
-  if (attr != hipSuccess) {
-    (void)hipGetLastError();
-    return false;
-  }
-  return true;
 }
 
 template <class C, int MT, int NW, int B, int RT, bool XL>

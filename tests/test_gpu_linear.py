@@ -161,12 +161,15 @@ def test_prefill_bf16_out(dev, qtype):
 # f32 and f16 activations with 4 <= M <= 64 run on the f32 matrix cores
 # (v_mfma_f32_16x16x4_f32) with the exact dequantized weights: the f32
 # tolerance holds; M < 4, M > 64 and K % 64 != 0 stay on the VALU kernel.
+# The 0.5B layer's gate / q shapes at 16 and 32 rows, and 16 x 1536 (more
+# than one batch a wave: sixteen waves).
 ALL_FORMATS = [rq.Q4_K, rq.Q6_K, rq.Q8_0, rq.Q5_K, rq.Q4_0, rq.Q5_0]
 
 
 @pytest.mark.parametrize("qtype", ALL_FORMATS)
 @pytest.mark.parametrize("m,n,k", [(2, 4864, 896), (4, 4864, 896), (5, 130, 256), (16, 896, 4864), (17, 300, 512),
-                                   (40, 64, 2048), (64, 258, 128), (65, 96, 256)])
+                                   (40, 64, 2048), (64, 258, 128), (65, 96, 256), (16, 4864, 896), (32, 896, 896),
+                                   (16, 300, 1536)])
 def test_small_m_f32_activations(dev, qtype, m, n, k):
     w, wf = make(qtype, n, k, 17 + m + n)
     x = torch.from_numpy(synth.activations(5 + m, m, k))
