@@ -53,6 +53,35 @@ __device__ __forceinline__ float4 ld4t(const void *t, int ttype, int64_t i) {
 // iteration waited for each load in turn).
 constexpr int KV_U = 4;
 
+// Elements of one 16-byte load: 4 f32 or 8 16-bit values.
+template <int TT>
+constexpr int kv_epl() {
+  return TT == RQ_F32 ? 4 : 8;
+}
+
+// kv_epl<TT>() elements at i (a multiple of that count, 16-byte aligned data)
+// as f32, from one 16-byte load.
+template <int TT>
+__device__ __forceinline__ void ld16(const void *t, int64_t i, float (&f)[8]) {
+  if constexpr (TT == RQ_F32) {
+    const float4 v = *reinterpret_cast<const float4 *>(static_cast<const float *>(t) + i);
+    f[0] = v.x, f[1] = v.y, f[2] = v.z, f[3] = v.w;
+  } else {
+    const uint4 v = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(t) + i);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (TT == RQ_BF16) {
+        f[2 * j] = __uint_as_float(w[j] << 16);
+        f[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
+      } else {
+        f[2 * j] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xFFFFu));
+        f[2 * j + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16));
+      }
+    }
+  }
+}
+
 __device__ __forceinline__ float block_max(float v, float *red) {
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
@@ -62,8 +91,9 @@ __device__ __forceinline__ float block_max(float v, float *red) {
 
 // Partial max|t| of elements [p * chunk, (p+1) * chunk) of head hh's b * sd
 // elements (slab-major).  NaN elements are skipped, as the reference's
-// `a > max_abs` test skips them.  VEC: sd and chunk are multiples of 4 and t
-// is 16-byte aligned, so each lane loads 4 elements at once.
+// `a > max_abs` test skips them.  VEC: sd and chunk are multiples of the
+// elements of a 16-byte load (4 f32, 8 16-bit) and t is 16-byte aligned, so
+// each lane loads 16 bytes at once.
 template <bool VEC, int TT>
 __global__ __launch_bounds__(KV_THREADS) void k_kv_absmax(const void *__restrict__ t, int ttype, int64_t b,
                                                           int64_t h, int64_t sd, int64_t chunk,
@@ -78,22 +108,23 @@ __global__ __launch_bounds__(KV_THREADS) void k_kv_absmax(const void *__restrict
     const int64_t lo = (e0 > bb * sd ? e0 : bb * sd) - bb * sd;
     const int64_t hi = (e1 < (bb + 1) * sd ? e1 : (bb + 1) * sd) - bb * sd;
     const int64_t base = (bb * h + hh) * sd;
-    if (VEC) {
-      for (int64_t i0 = lo + 4 * threadIdx.x; i0 < hi; i0 += 4 * KV_THREADS * KV_U) {
-        float4 v[KV_U];
+    if constexpr (VEC) {
+      constexpr int E = kv_epl<TT>();
+      for (int64_t i0 = lo + E * threadIdx.x; i0 < hi; i0 += E * KV_THREADS * KV_U) {
+        float v[KV_U][8];
 #pragma unroll
         for (int u = 0; u < KV_U; ++u) {
-          const int64_t i = i0 + 4 * KV_THREADS * u;
-          v[u] = ld4t<TT>(t, ttype, base + (i < hi ? i : i0));  // past the range: a repeat, not counted
+          const int64_t i = i0 + E * KV_THREADS * u;
+          ld16<TT>(t, base + (i < hi ? i : i0), v[u]);  // past the range: a repeat, not counted
         }
 #pragma unroll
         for (int u = 0; u < KV_U; ++u) {
-          if (i0 + 4 * KV_THREADS * u >= hi) break;
-          const float a0 = fabsf(v[u].x), a1 = fabsf(v[u].y), a2 = fabsf(v[u].z), a3 = fabsf(v[u].w);
-          if (a0 > mx) mx = a0;
-          if (a1 > mx) mx = a1;
-          if (a2 > mx) mx = a2;
-          if (a3 > mx) mx = a3;
+          if (i0 + E * KV_THREADS * u >= hi) break;
+#pragma unroll
+          for (int j = 0; j < E; ++j) {
+            const float a = fabsf(v[u][j]);
+            if (a > mx) mx = a;
+          }
         }
       }
     } else {
@@ -119,7 +150,8 @@ __device__ __forceinline__ uint32_t encode_one(float v, float sc) {
 }
 
 // Encode slab `slab` (= batch * h + head), elements [x0, x1) of it.  VEC:
-// sd and per_block are multiples of 4, t is 16-byte and q 8-byte aligned.
+// sd and per_block are multiples of the elements of a 16-byte load (4 f32,
+// 8 16-bit), t is 16-byte and q 8-byte aligned.
 template <int MODE, bool VEC, int TT>
 __global__ __launch_bounds__(KV_THREADS) void k_kv_encode(const void *__restrict__ t, int ttype, int64_t b,
                                                           int64_t h, int64_t sd, const float *__restrict__ part,
@@ -144,30 +176,57 @@ __global__ __launch_bounds__(KV_THREADS) void k_kv_encode(const void *__restrict
       }
       continue;
     }
+    uint8_t *o = static_cast<uint8_t *>(q);
+    if constexpr (VEC) {
+      // The first batch of elements is loaded before the head's partial
+      // maxima are read and folded (it does not depend on them), so the two
+      // reads overlap instead of following each other.
+      constexpr int E = kv_epl<TT>();
+      const int64_t i00 = x0 + E * threadIdx.x;
+      const int64_t ic = i00 < x1 ? i00 : x0;
+      float v[KV_U][8];
+#pragma unroll
+      for (int u = 0; u < KV_U; ++u) {
+        const int64_t i = i00 + E * KV_THREADS * u;
+        ld16<TT>(t, base + (i < x1 ? i : ic), v[u]);
+      }
+      float mx = threadIdx.x < P ? part[hh * P + threadIdx.x] : 0.0f;
+      mx = block_max(mx, red);
+      __syncthreads();  // red is reused by the next slab
+      const float sc = fmaxf(mx / (MODE == RQ_KV_FP8 ? 448.0f : 127.0f), 1e-8f);
+      if (blockIdx.x == 0 && slab < h && threadIdx.x == 0) scales[hh] = sc;
+      auto put = [&](int64_t i, const float (&f)[8]) {
+        uint32_t c[2] = {0u, 0u};
+#pragma unroll
+        for (int j = 0; j < E; ++j) c[j >> 2] |= encode_one<MODE>(f[j], sc) << (8 * (j & 3));
+        if constexpr (E == 8) *reinterpret_cast<uint2 *>(o + base + i) = make_uint2(c[0], c[1]);
+        else *reinterpret_cast<uint32_t *>(o + base + i) = c[0];
+      };
+#pragma unroll
+      for (int u = 0; u < KV_U; ++u) {
+        const int64_t i = i00 + E * KV_THREADS * u;
+        if (i < x1) put(i, v[u]);
+      }
+      for (int64_t i0 = i00 + E * KV_THREADS * KV_U; i0 < x1; i0 += E * KV_THREADS * KV_U) {
+#pragma unroll
+        for (int u = 0; u < KV_U; ++u) {
+          const int64_t i = i0 + E * KV_THREADS * u;
+          ld16<TT>(t, base + (i < x1 ? i : i0), v[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < KV_U; ++u) {
+          const int64_t i = i0 + E * KV_THREADS * u;
+          if (i < x1) put(i, v[u]);
+        }
+      }
+      continue;
+    }
     float mx = threadIdx.x < P ? part[hh * P + threadIdx.x] : 0.0f;
     mx = block_max(mx, red);
     __syncthreads();  // red is reused by the next slab
     const float sc = fmaxf(mx / (MODE == RQ_KV_FP8 ? 448.0f : 127.0f), 1e-8f);
     if (blockIdx.x == 0 && slab < h && threadIdx.x == 0) scales[hh] = sc;
-    uint8_t *o = static_cast<uint8_t *>(q);
-    if (VEC) {
-      for (int64_t i0 = x0 + 4 * threadIdx.x; i0 < x1; i0 += 4 * KV_THREADS * KV_U) {
-        float4 v[KV_U];
-#pragma unroll
-        for (int u = 0; u < KV_U; ++u) {
-          const int64_t i = i0 + 4 * KV_THREADS * u;
-          v[u] = ld4t<TT>(t, ttype, base + (i < x1 ? i : i0));
-        }
-#pragma unroll
-        for (int u = 0; u < KV_U; ++u) {
-          const int64_t i = i0 + 4 * KV_THREADS * u;
-          if (i >= x1) break;
-          *reinterpret_cast<uint32_t *>(o + base + i) =
-              encode_one<MODE>(v[u].x, sc) | (encode_one<MODE>(v[u].y, sc) << 8) |
-              (encode_one<MODE>(v[u].z, sc) << 16) | (encode_one<MODE>(v[u].w, sc) << 24);
-        }
-      }
-    } else {
+    {
       for (int64_t i = x0 + threadIdx.x; i < x1; i += KV_THREADS)
         o[base + i] = (uint8_t)encode_one<MODE>(load_x1(t, ttype, base + i), sc);
     }
@@ -220,11 +279,11 @@ int last_launch(const char *what) {
   return e == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "%s launch: %s", what, hipGetErrorString(e));
 }
 
-// Elements per workgroup along one slab: at least 4096 (a multiple of 4),
+// Elements per workgroup along one slab: at least 4096 (a multiple of 8),
 // and at most 1024 workgroups across a slab.
 int64_t slab_split(int64_t sd, int64_t *blocks) {
   int64_t per = 4096;
-  if ((sd + per - 1) / per > 1024) per = ((sd + 1023) / 1024 + 3) & ~(int64_t)3;
+  if ((sd + per - 1) / per > 1024) per = ((sd + 1023) / 1024 + 7) & ~(int64_t)7;
   *blocks = (sd + per - 1) / per;
   return per;
 }
@@ -260,17 +319,18 @@ int launch_kv_quantize(const void *t, int ttype, int64_t b, int64_t h, int64_t s
   int64_t xb = 0;
   const int64_t per = slab_split(sd, &xb);
   const dim3 grid((unsigned)xb, (unsigned)(b * h < KV_MAX_SLABS_Y ? b * h : KV_MAX_SLABS_Y));
-  const bool vec = sd % 4 == 0 && aligned(t, 16) && aligned(q, 8);
+  // vector loads: 16 bytes of input (4 f32 or 8 16-bit elements) a lane
+  const bool vec = sd % (ttype == RQ_F32 ? 4 : 8) == 0 && aligned(t, 16) && aligned(q, 8);
   if (mode == RQ_KV_F16) {
     launch_encode<RQ_KV_F16>(vec, grid, s, t, ttype, b, h, sd, nullptr, 0, per, q, scales);
     return last_launch("kv cast");
   }
   // Partial maxima: P ranges per head, each at least 4096 elements and a
-  // multiple of 4 long.
+  // multiple of 8 long.
   const int64_t per_head = b * sd;
   int64_t P = (per_head + 4095) / 4096;
   if (P > KV_MAX_PARTS) P = KV_MAX_PARTS;
-  const int64_t chunk = ((per_head + P - 1) / P + 3) & ~(int64_t)3;
+  const int64_t chunk = ((per_head + P - 1) / P + 7) & ~(int64_t)7;
   int rc = RQ_OK;
   float *part = static_cast<float *>(ws.get((size_t)(h * P) * sizeof(float), &rc));
   if (!part) return rc;
