@@ -635,6 +635,11 @@ int run_long(const rq_weight *wt, const void *x, int xtype, const Out &o, hipStr
 // Rows of more than 64 pieces, MR activation rows: a team of waves per row,
 // each workgroup walking up to kTeamRows rows; about 512 workgroups
 // (measured best of 128-2048 on 896 x 4864, 2048 x 8192 and 4096 x 14336).
+// Workgroups of four or more rows keep four rows' loads in flight at M = 1
+// for two-run pieces (Q4_K 2048 x 8192: 6.8 -> 5.9 us, 4096 x 14336 13.5 ->
+// 12.8 against two; Q6_K's four-run pieces lose, 2048 x 8192 7.1 -> 11.7;
+// on 896 x 4864, two rows a workgroup, four rows a workgroup were slower,
+// 4.09 -> 4.17 us).
 template <class F, int MR>
 int run_team(const rq_weight *wt, const void *x, int xtype, const Out &o, hipStream_t s) {
   const int P = (int)(wt->k / F::PE);
@@ -644,8 +649,12 @@ int run_team(const rq_weight *wt, const void *x, int xtype, const Out &o, hipStr
   if (per > kTeamRows) per = kTeamRows;
   const int64_t grid = (wt->n + per - 1) / per;
   if (grid > 0x7FFFFFFF) return RQ_E_UNSUPPORTED;
-  hipLaunchKernelGGL((k_gemv_team<F, 2, MR>), dim3((unsigned)grid), dim3(64 * team), 0, s, wt->data,
-                     wt->data + wt->aux_off, x, xtype, o, wt->n, wt->k);
+  if (MR == 1 && F::RUNS == 2 && per >= 4)
+    hipLaunchKernelGGL((k_gemv_team<F, 4, MR>), dim3((unsigned)grid), dim3(64 * team), 0, s, wt->data,
+                       wt->data + wt->aux_off, x, xtype, o, wt->n, wt->k);
+  else
+    hipLaunchKernelGGL((k_gemv_team<F, 2, MR>), dim3((unsigned)grid), dim3(64 * team), 0, s, wt->data,
+                       wt->data + wt->aux_off, x, xtype, o, wt->n, wt->k);
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }
 

@@ -35,9 +35,11 @@ DECODE_SHAPES = [(4864, 896), (896, 896), (128, 896), (896, 4864)]
 
 @pytest.mark.parametrize("qtype", [rq.Q8_0, rq.Q4_K, rq.Q6_K])
 @pytest.mark.parametrize("n,k", DECODE_SHAPES + [(2048, 2048), (512, 8192), (96, 1024), (4100, 4096),
-                                 (4096, 8192)])
+                                 (4096, 8192), (2048, 8192), (1601, 4864)])
 def test_decode_gemv_f32(dev, qtype, n, k):
-    # n >= 4096 with more than 64 pieces a row runs the one-wave-per-row kernel
+    # n >= 4096 with more than 64 pieces a row runs the one-wave-per-row kernel;
+    # n < 4096 the team kernel, with four rows in flight where a workgroup
+    # walks four or more (2048 x 8192; 1601 rows: workgroups of four and three)
     print(f"gemv qtype={qtype} n={n} k={k}", flush=True)
     w, wf = make(qtype, n, k, 10 + n + k)
     x = synth.activations(3, 1, k)
