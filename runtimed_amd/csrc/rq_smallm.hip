@@ -978,7 +978,13 @@ int run_plan(const rq_weight *const *w, int count, bool set, const void *xv, int
   const uint16_t *x = static_cast<const uint16_t *>(xv);
   int64_t tiles = 0;
   for (int j = 0; j < count; ++j) tiles += (w[j]->n + 15) / 16;
-  SmPlan p = smallm_plan<MT>(tiles, w[0]->k / C::CE, ws != nullptr && tiles <= WsLease::kCounters && m >= 16);
+  // No K split for rows of up to 1024 elements at m <= 32: the slice copy
+  // makes one unsplit batch cheap and the split's last-workgroup sum costs
+  // two round trips (896 x 896 at M = 16 4.72 -> 3.98 us, 128 x 896 3.85 ->
+  // 3.46, M = 32 4.91 -> 4.52; at M = 64 even, 5.55 vs 5.61).
+  const bool split_ok = !(w[0]->k <= 1024 && m <= 32);
+  SmPlan p = smallm_plan<MT>(tiles, w[0]->k / C::CE,
+                             split_ok && ws != nullptr && tiles <= WsLease::kCounters && m >= 16);
   f32x4 *wsp = nullptr;
   uint32_t *cnt = nullptr;
   if (p.s > 1) {
