@@ -901,10 +901,12 @@ int dispatch_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hi
 // batches of B chunks, RT row tiles a workgroup.
 //  * Split K when there are few row tiles (k / v / q / o / down of a small
 //    layer: 8 - 72 tiles on 256 CUs) and at least 16 activation rows: S up
-//    to 8, at most 512 workgroups, at least two chunks a workgroup.  Timed
+//    to 4, at most 512 workgroups, at least two chunks a workgroup.  Timed
 //    in HIP graphs on the 0.5B layer (7 launches / rq_linear_multi): M = 64
 //    160 -> 195 / 223 -> 287 GB/s, M = 16 238 -> 240 / 343 -> 354, but M = 4
 //    and 8 lose 6-10% (265 -> 242 at M = 4), so smaller M does not split.
+//    Four slices beat eight on 896 x 4864 (M = 16 8.71 -> 7.98 us, M = 64
+//    11.25 -> 10.12; two: 8.93 / 13.78).
 //  * Waves and batch so that one batch of every wave covers the
 //    workgroup's chunks (each batch is a dependent round trip to memory),
 //    within the registers: a batch holds B chunks of every row tile and B
@@ -919,7 +921,7 @@ template <int MT>
 SmPlan smallm_plan(int64_t tiles, int64_t nk, bool can_split) {
   int S = 1;
   if (can_split && tiles < 128)
-    while (S < 8 && tiles * S * 2 <= 512 && nk >= 4 * S) S *= 2;
+    while (S < 4 && tiles * S * 2 <= 512 && nk >= 4 * S) S *= 2;
   const int64_t c = (nk + S - 1) / S;
   SmPlan p{S, 4, 1, 1};
   if (MT == 4) {
@@ -1005,7 +1007,12 @@ int run_plan(const rq_weight *const *w, int count, bool set, const void *xv, int
   const int64_t cps = (w[0]->k / C::CE + p.s - 1) / p.s;
   const int xstr = (int)(cps * C::CE * 2 + 16);
   const size_t xbytes = (size_t)m * (size_t)xstr;
-  const bool xl = m >= 16 && w[0]->k <= 2048 && xbytes <= kSmXsMax;
+  // A copy above 80 KB leaves one workgroup per CU: only where the grid is
+  // about one round (the 4864 x 896 gate at M = 64, 304 workgroups, gains;
+  // gate and up in one launch, 608, lose: 14.0 -> 14.6 us).
+  const size_t part = (size_t)(MT == 4 ? 8 : 4) * MT * 64 * sizeof(f32x4);
+  const int64_t per_cu = (int64_t)((160 * 1024) / (part + xbytes));
+  const bool xl = m >= 16 && w[0]->k <= 2048 && xbytes <= kSmXsMax && tiles * p.s <= 320 * (per_cu > 0 ? per_cu : 1);
 #define RQ_SM(NW, B, RT)                                                                                     \
   {                                                                                                          \
     if (xl) {                                                                                                \
