@@ -739,13 +739,19 @@ int by_m(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_
   // prefill shapes: q/k/o 36 -> 26 us (64 x 128) -> 25.3 us (64 x 64) ->
   // 18.4 us (four K-groups), v Q6_K 28.2 -> 27.2 -> 21.9 us, gate/up 37.9 ->
   // 34.4 us (two K-groups), down 67 -> 53 us (two K-groups: 56 us).
+  // Register slots: the loop runs D steps an iteration, so a group's step
+  // count should be a multiple of D (three slots on the 8, 16 and 32 steps
+  // of these groups ran one dead step each); one slot on the 64 x 64 groups
+  // (q/k/o 18.4 -> 15.4 us, v 20.0 -> 16.7 us; two slots 16.0 / 17.5), two
+  // on 128 x 128 (gate/up 32.6 -> 29.0 us, down 45.1 -> 42.5 us; four slots
+  // 30.6 / 43.7).
   const int64_t tiles128 = ((m + 127) / 128) * ((wt->n + 127) / 128), nk = wt->k / BK;
-  if (tiles128 < 128 && nk <= 32) return launch<F, 64, 64, 2, 1, 3, 4>(wt, x, m, o, s, ws);
+  if (tiles128 < 128 && nk <= 32) return launch<F, 64, 64, 2, 1, 1, 4>(wt, x, m, o, s, ws);
   if (tiles128 < 128 && nk >= 64) {
     const int sp = (int)(nk / 32 < 4 ? nk / 32 : 4);
-    return launch<F, 128, 128, 2, 2>(wt, x, m, o, s, ws, sp);
+    return launch<F, 128, 128, 2, 2, 2>(wt, x, m, o, s, ws, sp);
   }
-  return launch<F, 128, 128, 2, 2, 3, 2>(wt, x, m, o, s, ws);
+  return launch<F, 128, 128, 2, 2, 2, 2>(wt, x, m, o, s, ws);
 }
 
 }  // namespace
