@@ -269,6 +269,28 @@ def extra_large_gemv(torch, rq, synth, dev, steps, warmup):
             "GB/s": round(b / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
+def extra_head_gemv(torch, rq, synth, dev, steps, warmup):
+    """The decode step's largest GEMV in the Q4_K_M model of the prefill
+    workload: the output projection 262144x2048 at M=1 (f32 activations), as
+    Q6_K (the Q4_K_M head) and as Q4_K, 3-4 distinct copies (> 1 GB) replayed
+    in a HIP graph."""
+    n, k = 262144, 2048
+    res = []
+    for name, qt, copies in (("Q6_K", rq.Q6_K, 3), ("Q4_K", rq.Q4_K, 4)):
+        blocks = synth.weight_blocks(qt, 11, n, k)
+        W = [rq.QWeight(qt, blocks, n, k) for _ in range(copies)]
+        x = torch.from_numpy(synth.activations(12, 1, k)).to(dev)
+        y = torch.empty((1, n), device=dev)
+        g = capture(torch, lambda: [w.forward(x, out=y) for w in W])
+        ms = Timer(torch).replay(g, max(2, steps // 4), 1) / copies
+        b = len(blocks) + k * 4 + n * 4
+        res.append({"format": name, "us_per_gemv": round(ms * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                    "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+        del g, W
+        torch.cuda.empty_cache()
+    return {"workload": "decode output projection 262144x2048 f32, M=1", "formats": res}
+
+
 def extra_verify(torch, rq, W, dev, steps, warmup, dtype=None, ms_list=(1, 2, 4, 8, 16, 64), multi=False):
     """The verify sweep over all layer copies: 7 rq_linear calls per layer,
     or (multi) q/k/v and gate/up each through one rq_linear_multi call."""
@@ -724,6 +746,7 @@ def main():
                                                                                args.warmup, dev)),
                          ("q8_0_gemv", lambda: extra_q8_gemv(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("q4_k_gemv_large", lambda: extra_large_gemv(torch, rq, synth, dev, args.steps, args.warmup)),
+                         ("head_gemv_m1", lambda: extra_head_gemv(torch, rq, synth, dev, args.steps, args.warmup)),
                          ("decode_multi", lambda: extra_decode_multi(torch, rq, W, args.steps, args.warmup, dev)),
                          ("verify", lambda: extra_verify(torch, rq, W, dev, args.steps, args.warmup)),
                          ("verify_multi", lambda: extra_verify(torch, rq, W, dev, args.steps, args.warmup,

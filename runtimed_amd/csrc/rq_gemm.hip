@@ -672,6 +672,37 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float *__restrict__ pa
   }
 }
 
+// The same with four consecutive outputs a thread (m * n and n multiples of
+// four, y 16-byte aligned): 16-byte partial loads, all S of a thread's loads
+// issued before the sums, which run in split order as above (same results).
+template <int S>
+__global__ __launch_bounds__(256) void k_splitk_sum4(const float *__restrict__ part, int64_t mn, int64_t n,
+                                                     const Out o) {
+  const float4 *p4 = reinterpret_cast<const float4 *>(part);
+  const int64_t mn4 = mn / 4;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < mn4; i += (int64_t)gridDim.x * 256) {
+    float4 t[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) t[s] = p4[s * mn4 + i];
+    float4 v = t[0];
+#pragma unroll
+    for (int s = 1; s < S; ++s) {
+      v.x += t[s].x;
+      v.y += t[s].y;
+      v.z += t[s].z;
+      v.w += t[s].w;
+    }
+    if (o.bias) {
+      const int64_t c = (4 * i) % n;
+      v.x = with_bias(v.x, load_as_f32(o.bias, o.btype, c), o.ytype);
+      v.y = with_bias(v.y, load_as_f32(o.bias, o.btype, c + 1), o.ytype);
+      v.z = with_bias(v.z, load_as_f32(o.bias, o.btype, c + 2), o.ytype);
+      v.w = with_bias(v.w, load_as_f32(o.bias, o.btype, c + 3), o.ytype);
+    }
+    store_four(o.y, o.ytype, 4 * i, v.x, v.y, v.z, v.w);
+  }
+}
+
 // Workgroups per tile along K: enough to give the 256 CUs a workgroup each,
 // but only for long K (at least 32 K-steps of 64 per split): the f32
 // partials and their sum cost about as much as a 2048-deep tile; at most 8.
@@ -704,8 +735,22 @@ int launch(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStrea
                      wt->data + wt->aux_off, static_cast<const uint16_t *>(x), m, wt->n, wt->k, o, steps, part);
   if (part) {
     const int64_t mn = m * wt->n;
-    const int64_t blocks = (mn + 255) / 256 < 4096 ? (mn + 255) / 256 : 4096;
-    hipLaunchKernelGGL(k_splitk_sum, dim3((unsigned)blocks), dim3(256), 0, s, part, used, mn, wt->n, o);
+    if (wt->n % 4 == 0 && (reinterpret_cast<uintptr_t>(o.y) & 15) == 0 && used <= 8) {
+      const int64_t blocks = (mn / 4 + 255) / 256 < 4096 ? (mn / 4 + 255) / 256 : 4096;
+      const dim3 g((unsigned)blocks), b(256);
+      switch (used) {
+        case 2: hipLaunchKernelGGL(k_splitk_sum4<2>, g, b, 0, s, part, mn, wt->n, o); break;
+        case 3: hipLaunchKernelGGL(k_splitk_sum4<3>, g, b, 0, s, part, mn, wt->n, o); break;
+        case 4: hipLaunchKernelGGL(k_splitk_sum4<4>, g, b, 0, s, part, mn, wt->n, o); break;
+        case 5: hipLaunchKernelGGL(k_splitk_sum4<5>, g, b, 0, s, part, mn, wt->n, o); break;
+        case 6: hipLaunchKernelGGL(k_splitk_sum4<6>, g, b, 0, s, part, mn, wt->n, o); break;
+        case 7: hipLaunchKernelGGL(k_splitk_sum4<7>, g, b, 0, s, part, mn, wt->n, o); break;
+        default: hipLaunchKernelGGL(k_splitk_sum4<8>, g, b, 0, s, part, mn, wt->n, o); break;
+      }
+    } else {
+      const int64_t blocks = (mn + 255) / 256 < 4096 ? (mn + 255) / 256 : 4096;
+      hipLaunchKernelGGL(k_splitk_sum, dim3((unsigned)blocks), dim3(256), 0, s, part, used, mn, wt->n, o);
+    }
   }
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemm launch failed");
 }

@@ -49,10 +49,12 @@ def test_decode_gemv_f32(dev, qtype, n, k):
 
 
 @pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("n,k", [(4096, 512), (4133, 4096), (14336, 4096), (4096, 8192)])
+@pytest.mark.parametrize("n,k", [(4096, 512), (4133, 1024), (8192, 2048), (4133, 4096), (14336, 4096),
+                                 (4096, 8192)])
 def test_gemv_matrix_cores_q4k(dev, xdt, n, k):
-    # M = 1 Q4_K with k % 512 == 0, k <= 8192 and n >= 4096 runs on the matrix
-    # cores: the codes as bf16 128 + q, x as two bf16 limbs (16 significant
+    # M = 1 Q4_K with k % 512 == 0, 1024 <= k <= 8192 and n >= 4096 runs on the
+    # matrix cores (k = 512 on the segment kernel): the codes as bf16 128 + q,
+    # x as two bf16 limbs (16 significant
     # bits), f32 sums; x spans six decades (N(0,1) with every 7th element
     # x300 and every 11th x1e-3), n = 4133 ends in a partial 32-row tile
     print(f"gemv mx x={xdt} n={n} k={k}", flush=True)
