@@ -656,6 +656,24 @@ def mode_prefill_head(torch, rq, synth, dev, steps):
     print(json.dumps({"mode": "prefill-head", "launches": steps}), flush=True)
 
 
+def mode_gemv_head(torch, rq, synth, dev, steps):
+    """Only the M=1 output projection 262144x2048 (Q6_K, then Q4_K), three
+    distinct copies each, eager launches (for traces and counters)."""
+    n, k = 262144, 2048
+    for qt in (rq.Q6_K, rq.Q4_K):
+        blocks = synth.weight_blocks(qt, 11, n, k)
+        W = [rq.QWeight(qt, blocks, n, k) for _ in range(3)]
+        x = torch.from_numpy(synth.activations(12, 1, k)).to(dev)
+        y = torch.empty((1, n), device=dev)
+        for _ in range(steps):
+            for w in W:
+                w.forward(x, out=y)
+        torch.cuda.synchronize()
+        del W
+        torch.cuda.empty_cache()
+    print(json.dumps({"mode": "gemv-head", "launches": 6 * steps}), flush=True)
+
+
 def mode_verify(torch, rq, synth, dev, steps, m, layers=128, xdt="bf16", multi=False):
     """Only the verify sweep at one M: the 7 GEMMs of `layers` layer copies
     (q/k/v and gate/up through rq_linear_multi with multi), eager launches
@@ -701,7 +719,7 @@ def main():
     ap.add_argument("--m", type=int, default=16, help="activation rows of --mode verify")
     ap.add_argument("--multi", action="store_true", help="--mode verify through rq_linear_multi")
     ap.add_argument("--mode", choices=["full", "gate", "copy", "fp8", "prefill", "prefill-head", "gemv-large",
-                                       "verify"],
+                                       "gemv-head", "verify"],
                     default="full",
                     help="gate: only the dominant GEMV; copy: counter calibration copy")
     ap.add_argument("--eager", action="store_true", help="gate mode without a HIP graph")
@@ -728,6 +746,8 @@ def main():
         return mode_prefill(torch, rq, synth, dev, args.steps)
     if args.mode == "prefill-head":
         return mode_prefill_head(torch, rq, synth, dev, args.steps)
+    if args.mode == "gemv-head":
+        return mode_gemv_head(torch, rq, synth, dev, args.steps)
     if args.mode == "gemv-large":
         return mode_gemv_large(torch, rq, synth, dev, args.steps)
     if args.mode == "verify":
