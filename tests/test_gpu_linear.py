@@ -120,6 +120,22 @@ def test_few_rows_exact_weights(dev, xdt, qtype, n, k, m):
         assert torch.equal(y[i:i + 1], y1)
 
 
+@pytest.mark.parametrize("n,k", [(896, 896), (128, 896), (896, 4864)])
+@pytest.mark.parametrize("m", [2, 4, 8, 16, 64])
+def test_verify_layer_shapes_bf16(dev, n, k, m):
+    # The speculative-verify sweep on the other Qwen2-0.5B layer matrices
+    # (q/o, k/v, down; gate/up is the case below): the small-M kernels run
+    # them on 56 or 8 row tiles, unsplit (k = 896) or with K in slices
+    # (down), with f32 and bf16 outputs
+    print(f"verify layer n={n} k={k} m={m}", flush=True)
+    w, wf = make(rq.Q4_K, n, k, 90 + n + m)
+    xb = torch.from_numpy(synth.activations(91 + m, m, k)).to(torch.bfloat16)
+    r = ref(xb.float().numpy(), wf)
+    for ydt in (torch.float32, torch.bfloat16):
+        y = w.forward(xb.to(dev), out_dtype=ydt).float().cpu().numpy()
+        assert norm_err(y, r) <= TOL_BF16, (ydt, norm_err(y, r))
+
+
 @pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0])
 @pytest.mark.parametrize("m", [2, 4, 8, 16, 64])
 def test_verify_small_m_bf16(dev, qtype, m):
