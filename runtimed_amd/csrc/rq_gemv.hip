@@ -704,13 +704,25 @@ int run_seg(const rq_weight *wt, const void *x, int xtype, const Out &o, hipStre
 template <class F>
 int run_m1(const rq_weight *wt, const void *x, int xtype, const Out &o, hipStream_t s) {
   const int P = (int)(wt->k / F::PE);
-  // Q4_K rows of 1024 or more elements on many rows: the matrix-core GEMV
-  // where it applies (against the segment kernel on 32- and 64-piece rows:
-  // 262144 x 2048 98.8 -> 58.2 us, 151936 x 1024 33.9 -> 20.9 us, 8192 x 2048
-  // 5.83 -> 5.15 us).
+  // Q4_K long rows on many rows: the matrix-core GEMV where it applies; rows
+  // of 32 and 64 pieces too where n k >= 2^24 (against the segment kernel:
+  // 262144 x 2048 98.8 -> 58.2 us, 151936 x 1024 33.9 -> 20.9, 16384 x 2048
+  // 9.46 -> 7.21, 8192 x 2048 5.87 -> 5.22; smaller grids lose: 4096 x 2048
+  // 3.71 -> 4.86, 4096 x 1024 2.97 -> 3.81).
   if constexpr (std::is_same_v<F, FmtQ4K>) {
-    if (P >= 32 && wt->n >= 4096) {
+    if ((P > 64 || (P >= 32 && wt->n * wt->k >= (int64_t)1 << 24)) && wt->n >= 4096) {
       const int rc = launch_gemv_mx(wt, x, xtype, o, s);
+      if (rc != RQ_E_UNSUPPORTED) return rc;
+    }
+  }
+  // Q6_K the same way (rows of 1024 or more elements, 64-element pieces)
+  // where n k >= 2^26: against the segment / long-row kernels 262144 x 2048
+  // 98.8 -> 82.3 us, 151936 x 1024 29.9 -> 28.3, 32768 x 2048 17.1 -> 16.0;
+  // smaller grids lose or tie (16384 x 2048 9.6 -> 10.3 us, 32768 x 1024 8.6
+  // -> 10.5, 8192 x 2048 5.4 -> 7.5, 14336 x 4096 16.2 -> 16.0).
+  if constexpr (std::is_same_v<F, FmtQ6K>) {
+    if (P >= 16 && wt->n >= 4096 && wt->n * wt->k >= (int64_t)1 << 26) {
+      const int rc = launch_gemv_mx6(wt, x, xtype, o, s);
       if (rc != RQ_E_UNSUPPORTED) return rc;
     }
   }

@@ -241,6 +241,180 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t *__restrict__ w,
   }
 }
 
+// ---- Q6_K (dequant_k.rs:94-125) ----
+//
+// The same layout with the device's Q6_K records (208 bytes a super-block:
+// ql 128 | qh 64 | int8 scales 16, d in the aux array): a 6-bit code q
+// becomes the bf16 pattern 0x4300 | q = 128 + q, and one
+// v_mfma_f32_32x32x16_bf16 covers one 16-element sub-block of 32 rows, so
+// w . x = d sum_t sc_t (S_t - 160 X_t) with S_t the MFMA's hi + lo sum of
+// x (128 + q) and X_t the sum of x over the sub-block.  Sub-block t = 8 hf +
+// 2 r + s (half hf, run r, 16-element group s) holds elements 128 hf + 32 r +
+// 16 s + j: its low four bits are nibble r / 2 of ql byte 64 hf + 32 (r & 1)
+// + 16 s + j, its high two bits bits 2r, 2r + 1 of qh byte 32 hf + 16 s + j.
+// Lane (row, half h) takes j = 8h .. 8h + 7.  Records are loaded coalesced
+// (13 pieces of 16 bytes a row, 416 a super-block of 32 rows, seven loads)
+// through a 6.5 KB LDS region of the wave.
+constexpr int kMx6Trans = 32 * 208;  // a wave's LDS region: one super-block of 32 rows
+constexpr int kMx6Loads = 7;         // 7 x 64 >= 416 pieces (the rest repeat piece 415)
+
+__host__ __device__ inline size_t mx6_lds_bytes(int64_t k) {
+  const int64_t waves = k / (256 * kMxSb);
+  return (size_t)k * 4 + kMxZero + (size_t)(k / 16) * 4 + (size_t)waves * (32 * 4 + kMx6Trans);
+}
+
+__global__ __launch_bounds__(1024) void k_gemv_mx6(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
+                                                   const void *__restrict__ x, int xtype, const Out o, int64_t n,
+                                                   int64_t k) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int waves = (int)(blockDim.x >> 6);
+  const int wr = lane & 31, h = lane >> 5;
+  const int nsb = (int)(k >> 8);
+  const uint32_t rstride = (uint32_t)nsb * 208u;  // bytes a row (the whole matrix is < 2 GB)
+  const int64_t row0 = (int64_t)blockIdx.x * 32;
+  const int rowcap = __builtin_amdgcn_readfirstlane((int)(n - row0 < 32 ? n - row0 - 1 : 31));
+
+  const bool f32x = xtype == RQ_F32;
+  const uint4 *xc = static_cast<const uint4 *>(x);
+  const uint4 xa = xc[f32x ? 2 * tid : tid];
+  const uint4 xb = xc[f32x ? 2 * tid + 1 : tid];
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Piece c = lane + 64 i of a super-block: 16-byte piece c % 13 of row
+  // c / 13 (c / 13 = (5042 c) >> 16 for c < 448); rows past the matrix
+  // clamped.
+  int prow[kMx6Loads], ppc[kMx6Loads];
+#pragma unroll
+  for (int i = 0; i < kMx6Loads; ++i) {
+    const int c = lane + 64 * i < 415 ? lane + 64 * i : 415;
+    prow[i] = (c * 5042) >> 16;
+    ppc[i] = c - 13 * prow[i];
+  }
+  const uint8_t *wt0 = w + (uint64_t)row0 * rstride + (uint64_t)(wv * kMxSb) * 208u;
+  mx_u32x4 t[kMxSb][kMx6Loads];
+#pragma unroll
+  for (int s = 0; s < kMxSb; ++s) {
+#pragma unroll
+    for (int i = 0; i < kMx6Loads; ++i) {
+      const int r = prow[i] < rowcap ? prow[i] : rowcap;
+      t[s][i] = __builtin_nontemporal_load(
+          reinterpret_cast<const mx_u32x4 *>(wt0 + (uint32_t)r * rstride + 208u * s + 16u * ppc[i]));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // d of this lane's row for the wave's two super-blocks (nsb and 2 wv are
+  // even, so the two halves are one aligned word).
+  const int drow = wr < rowcap ? wr : rowcap;
+  const uint32_t dd =
+      *reinterpret_cast<const uint32_t *>(aux + 2 * ((uint64_t)(row0 + drow) * nsb + (uint64_t)(wv * kMxSb)));
+
+  // x as hi / lo bf16 records (32 bytes per 8 elements), the zero
+  // fragments, and X_t per 16-element sub-block (the sum of hi + lo).
+  const bool bfx = xtype == RQ_BF16;
+  const int zero_off = (int)(4 * k);
+  float *xsum = reinterpret_cast<float *>(lds + zero_off + kMxZero);
+  {
+    const uint32_t va[4] = {xa.x, xa.y, xa.z, xa.w}, vb[4] = {xb.x, xb.y, xb.z, xb.w};
+    float xf[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float e0 = bfx ? __uint_as_float(va[j] << 16) : h2f(va[j]);
+      const float e1 = bfx ? __uint_as_float(va[j] & 0xFFFF0000u) : h2f(va[j] >> 16);
+      const uint32_t f0 = j < 2 ? va[2 * j] : vb[2 * j - 4], f1 = j < 2 ? va[2 * j + 1] : vb[2 * j - 3];
+      xf[2 * j] = f32x ? __uint_as_float(f0) : e0;
+      xf[2 * j + 1] = f32x ? __uint_as_float(f1) : e1;
+    }
+    uint32_t hi[4], lo[4];
+    float sx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      hi[j] = pk_bf16(xf[2 * j], xf[2 * j + 1]);
+      const float h0 = __uint_as_float(hi[j] << 16), h1 = __uint_as_float(hi[j] & 0xFFFF0000u);
+      lo[j] = pk_bf16(xf[2 * j] - h0, xf[2 * j + 1] - h1);
+      const float l0 = __uint_as_float(lo[j] << 16), l1 = __uint_as_float(lo[j] & 0xFFFF0000u);
+      sx += (h0 + l0) + (h1 + l1);
+    }
+    *reinterpret_cast<uint4 *>(lds + 32 * tid) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    *reinterpret_cast<uint4 *>(lds + 32 * tid + 16) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    sx += __shfl_xor(sx, 1);
+    if ((tid & 1) == 0) xsum[tid >> 1] = sx;
+  }
+  if (tid < kMxZero / 16) *reinterpret_cast<uint4 *>(lds + zero_off + 16 * tid) = make_uint4(0, 0, 0, 0);
+  __syncthreads();
+
+  // A fragment of sub-block (hf, r, s) for lane (A row a, half h): element
+  // e = 256 sb + 128 hf + 32 r + 16 s + 8 h, record byte 32 (e / 8) + 16 a =
+  // 1024 sb + 512 hf + 128 r + 64 s + 32 h + 16 a (rows 2..31 read zeros).
+  const int ar = lane & 31;
+  const uint32_t abase = ar < 2 ? (uint32_t)(16 * ar + 32 * h) : (uint32_t)zero_off;
+  const uint32_t astride = ar < 2 ? 1024u : 0u;
+  const mx_f32x16 zero = {};
+  float *red = xsum + k / 16;
+  uint8_t *trans = reinterpret_cast<uint8_t *>(red + 32 * waves) + kMx6Trans * wv;
+  // Row r of the region at byte 208 r (52 dwords apart: 16 consecutive rows
+  // start on distinct banks).
+  const uint8_t *trd = trans + 208 * wr;
+  float yacc = 0.0f;
+#pragma unroll
+  for (int s = 0; s < kMxSb; ++s) {
+    const int sb = wv * kMxSb + s;
+#pragma unroll
+    for (int i = 0; i < kMx6Loads; ++i)
+      *reinterpret_cast<mx_u32x4 *>(trans + 208 * prow[i] + 16 * ppc[i]) = t[s][i];
+    __builtin_amdgcn_wave_barrier();
+    // ql bytes 64 hf + 16 g + 8 h (g = s16 for r even, 2 + s16 for r odd)
+    // and qh bytes 32 hf + 16 s16 + 8 h, for hf, s16 in {0, 1}.
+    uint2 qa[2][2], qb[2][2], qq[2][2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int s16 = 0; s16 < 2; ++s16) {
+        qa[hf][s16] = *reinterpret_cast<const uint2 *>(trd + 64 * hf + 16 * s16 + 8 * h);
+        qb[hf][s16] = *reinterpret_cast<const uint2 *>(trd + 64 * hf + 32 + 16 * s16 + 8 * h);
+        qq[hf][s16] = *reinterpret_cast<const uint2 *>(trd + 128 + 32 * hf + 16 * s16 + 8 * h);
+      }
+    const uint4 scb = *reinterpret_cast<const uint4 *>(trd + 192);
+    __builtin_amdgcn_wave_barrier();
+    const uint8_t *ab = lds + abase + astride * (uint32_t)sb;
+    const float4 *xs4 = reinterpret_cast<const float4 *>(xsum) + 4 * sb;
+    const float4 xs[4] = {xs4[0], xs4[1], xs4[2], xs4[3]};
+    const uint32_t scw[4] = {scb.x, scb.y, scb.z, scb.w};
+    float acc_s = 0.0f, acc_x = 0.0f;  // sum sc S, sum sc X
+    static_for<2>([&](auto Hf) {
+      constexpr int hf = decltype(Hf)::value;
+      static_for<4>([&](auto Rr) {
+        constexpr int r = decltype(Rr)::value;
+        static_for<2>([&](auto Ss) {
+          constexpr int s16 = decltype(Ss)::value;
+          constexpr int sub = 8 * hf + 2 * r + s16;
+          const uint2 lq = (r & 1) ? qb[hf][s16] : qa[hf][s16];
+          const uint2 hq = qq[hf][s16];
+          const uint32_t c0 = ((lq.x >> (4 * (r >> 1))) & 0x0F0F0F0Fu) | (((hq.x >> (2 * r)) & 0x03030303u) << 4);
+          const uint32_t c1 = ((lq.y >> (4 * (r >> 1))) & 0x0F0F0F0Fu) | (((hq.y >> (2 * r)) & 0x03030303u) << 4);
+          const mx_bf16x8 a = *reinterpret_cast<const mx_bf16x8 *>(ab + 512 * hf + 128 * r + 64 * s16);
+          const mx_f32x16 c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b_frag(c0, c1), zero, 0, 0, 0);
+          const float sc = (float)(int8_t)((scw[sub >> 2] >> (8 * (sub & 3))) & 0xFFu);
+          const float xt = (&xs[sub >> 2].x)[sub & 3];
+          acc_s = fmaf(sc, c[0] + c[1], acc_s);
+          acc_x = fmaf(sc, xt, acc_x);
+        });
+      });
+    });
+    const float d = h2f(s ? dd >> 16 : dd);
+    yacc = fmaf(d, fmaf(-160.0f, acc_x, acc_s), yacc);
+  }
+
+  if (h == 0) red[32 * wv + wr] = yacc;
+  __syncthreads();
+  if (tid < 32 && row0 + tid < n) {
+    float v = 0.0f;
+    for (int i = 0; i < waves; ++i) v += red[32 * i + tid];
+    store_linear(o, 0, n, row0 + tid, v);
+  }
+}
+
 }  // namespace
 
 int launch_gemv_mx(const rq_weight *wt, const void *x, int xtype, const Out &o, hipStream_t s) {
@@ -263,6 +437,26 @@ int launch_gemv_mx(const rq_weight *wt, const void *x, int xtype, const Out &o, 
   }
   hipLaunchKernelGGL(k_gemv_mx, dim3((unsigned)grid), dim3((unsigned)(k / 8)), lds, s, wt->data, x, xtype, o, n,
                      k);
+  return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
+}
+
+int launch_gemv_mx6(const rq_weight *wt, const void *x, int xtype, const Out &o, hipStream_t s) {
+  const int64_t n = wt->n, k = wt->k;
+  if (wt->qtype != RQ_Q6_K || k % (256 * kMxSb) != 0 || k > kMxMaxK || n < 32) return RQ_E_UNSUPPORTED;
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
+  if ((uint64_t)n * (uint64_t)(k / 256) * 208u >= (1ull << 31)) return RQ_E_UNSUPPORTED;
+  const size_t lds = mx6_lds_bytes(k);
+  if (lds > 65536) {
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gemv_mx6),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       (int)mx6_lds_bytes(kMxMaxK));
+    if (attr != hipSuccess) {
+      (void)hipGetLastError();
+      return RQ_E_UNSUPPORTED;
+    }
+  }
+  hipLaunchKernelGGL(k_gemv_mx6, dim3((unsigned)((n + 31) / 32)), dim3((unsigned)(k / 8)), lds, s, wt->data,
+                     wt->data + wt->aux_off, x, xtype, o, n, k);
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
 }
 

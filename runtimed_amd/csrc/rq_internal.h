@@ -241,6 +241,8 @@ int launch_linear_fused(const rq_weight *w, const void *x, int xtype, int64_t m,
 // M = 1 Q4_K GEMV on the matrix cores (k % 512 == 0, k <= 8192, x 16-byte
 // aligned); RQ_E_UNSUPPORTED for other shapes.
 int launch_gemv_mx(const rq_weight *w, const void *x, int xtype, const Out &o, hipStream_t s);
+// The same for Q6_K (k % 512 == 0, k <= 8192).
+int launch_gemv_mx6(const rq_weight *w, const void *x, int xtype, const Out &o, hipStream_t s);
 // One launch for several weights of one format sharing x (count <= kMultiMax,
 // equal k, one output type): M = 1 and M = 2 on the segment layout, bf16
 // activations with 3 <= M <= 64 on the small-M matrix-core kernel.

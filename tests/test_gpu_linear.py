@@ -49,17 +49,38 @@ def test_decode_gemv_f32(dev, qtype, n, k):
 
 
 @pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("n,k", [(4096, 512), (4133, 1024), (8192, 2048), (4133, 4096), (14336, 4096),
-                                 (4096, 8192)])
+@pytest.mark.parametrize("n,k", [(4096, 512), (4096, 2048), (16394, 1024), (8192, 2048), (4133, 4096),
+                                 (14336, 4096), (4096, 8192)])
 def test_gemv_matrix_cores_q4k(dev, xdt, n, k):
-    # M = 1 Q4_K with k % 512 == 0, 1024 <= k <= 8192 and n >= 4096 runs on the
-    # matrix cores (k = 512 on the segment kernel): the codes as bf16 128 + q,
+    # M = 1 Q4_K with k % 512 == 0, k <= 8192 and n >= 4096 runs on the matrix
+    # cores for k > 2048, and for k = 1024, 2048 where n k >= 2^24 (4096 x 512
+    # and 4096 x 2048 stay on the segment kernel): the codes as bf16 128 + q,
     # x as two bf16 limbs (16 significant
     # bits), f32 sums; x spans six decades (N(0,1) with every 7th element
     # x300 and every 11th x1e-3), n = 4133 ends in a partial 32-row tile
     print(f"gemv mx x={xdt} n={n} k={k}", flush=True)
     w, wf = make(rq.Q4_K, n, k, 60 + n + k)
     x = synth.activations(5, 1, k)
+    x[0, ::7] *= 300.0
+    x[0, 3::11] *= 1e-3
+    xt = torch.from_numpy(x).to(xdt)
+    y = w.forward(xt.to(dev), out_dtype=torch.float32).cpu().numpy()
+    assert y.shape == (1, n)
+    assert norm_err(y, ref(xt.float().numpy(), wf)) <= TOL_F32
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("n,k", [(14336, 4096), (65546, 1024), (32768, 2048), (16384, 4096), (8200, 8192)])
+def test_gemv_matrix_cores_q6k(dev, xdt, n, k):
+    # M = 1 Q6_K with k % 512 == 0, 1024 <= k <= 8192, n >= 4096 and
+    # n k >= 2^26 runs on the matrix cores (14336 x 4096 just below the size
+    # bound on the long-row kernel): 6-bit codes as bf16
+    # 128 + q, one MFMA per 16-element sub-block with its int8 scale, x as two
+    # bf16 limbs; x spans six decades, n = 65546 and 8200 end in a partial
+    # 32-row tile
+    print(f"gemv mx6 x={xdt} n={n} k={k}", flush=True)
+    w, wf = make(rq.Q6_K, n, k, 61 + n + k)
+    x = synth.activations(6, 1, k)
     x[0, ::7] *= 300.0
     x[0, 3::11] *= 1e-3
     xt = torch.from_numpy(x).to(xdt)
