@@ -787,16 +787,17 @@ int by_m(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_
   // Register slots: the loop runs D steps an iteration, so a group's step
   // count should be a multiple of D (three slots on the 8, 16 and 32 steps
   // of these groups ran one dead step each); one slot on the 64 x 64 groups
-  // (q/k/o 18.4 -> 15.4 us, v 20.0 -> 16.7 us; two slots 16.0 / 17.5), two
-  // on 128 x 128 (gate/up 32.6 -> 29.0 us, down 45.1 -> 42.5 us; four slots
-  // 30.6 / 43.7).
+  // (q/k/o 18.4 -> 15.4 us, v 20.0 -> 16.7 us; two slots 16.0 / 17.5) and
+  // on 128 x 128 (gate/up 32.6 -> 29.0 us with two slots, 28.3 -> 27.8-28.2
+  // with one).  The split down projection also takes two K-groups (eight
+  // waves a workgroup): 42.7 -> 40.7 us, 44.5 -> 41.4 in alternating runs.
   const int64_t tiles128 = ((m + 127) / 128) * ((wt->n + 127) / 128), nk = wt->k / BK;
   if (tiles128 < 128 && nk <= 32) return launch<F, 64, 64, 2, 1, 1, 4>(wt, x, m, o, s, ws);
   if (tiles128 < 128 && nk >= 64) {
     const int sp = (int)(nk / 32 < 4 ? nk / 32 : 4);
-    return launch<F, 128, 128, 2, 2, 2>(wt, x, m, o, s, ws, sp);
+    return launch<F, 128, 128, 2, 2, 1, 2>(wt, x, m, o, s, ws, sp);
   }
-  return launch<F, 128, 128, 2, 2, 2, 2>(wt, x, m, o, s, ws);
+  return launch<F, 128, 128, 2, 2, 1, 2>(wt, x, m, o, s, ws);
 }
 
 }  // namespace
