@@ -42,6 +42,8 @@ ROUTES = [
     (rq.Q4_K, 4864, 896, 1, torch.float32),     # segment GEMV
     (rq.Q4_K, 896, 4864, 1, torch.float32),     # team GEMV
     (rq.Q4_K, 4100, 4096, 1, torch.float32),    # matrix-core GEMV (Q4_K long rows)
+    (rq.Q4_K, 8200, 2048, 1, torch.float16),    # matrix-core GEMV (Q4_K 64-piece rows, n k >= 2^24)
+    (rq.Q6_K, 32800, 2048, 1, torch.bfloat16),  # matrix-core GEMV (Q6_K, n k >= 2^26)
     (rq.Q8_0, 4100, 4096, 1, torch.float32),    # one wave per row
     (rq.Q6_K, 896, 896, 2, torch.float32),      # two rows, segment
     (rq.Q4_K, 896, 4864, 2, torch.bfloat16),    # two rows, team
