@@ -298,12 +298,148 @@ __global__ __launch_bounds__(512) void k_marlin_gemv_x(const mchunk *__restrict_
   }
 }
 
+// M = 1 on the matrix cores (k % 32 == 0, x 16-byte aligned): a workgroup
+// owns 32 rows, wave w takes chunks w, w + W, .. (CPW of them, chunks past kc
+// read chunk kc - 1 against zero activations).  Lane (row r = lane % 32, half
+// h = lane / 32) loads words 2h, 2h + 1 of row r's record (8 contiguous
+// bytes: the wave reads 32 consecutive records, 512 bytes, per chunk).  Word
+// j's codes (inputs 8j .. 8j + 7) become the bf16 patterns 0x4300 | q =
+// 128 + q in the order of the masked bytes (inputs 0, 2, 4, 6, 1, 3, 5, 7),
+// the B operand of one v_mfma_f32_32x32x16_bf16 (column = row, K group =
+// h); x is staged in the same order as two bf16 limbs (hi = bf16(x), lo =
+// bf16(x - hi)) in A rows 0 and 1 (rows 2..31 read zeros).  With one scale a
+// row no per-block scaling is needed: the accumulator runs over all of the
+// wave's chunks, and y = s_r (S - 136 X) with S the hi + lo sums of the
+// row's waves (added in wave order) and X the sum of hi + lo over k.
+template <int CPW>
+__global__ __launch_bounds__(1024) void k_marlin_mx(const mchunk *__restrict__ packed, const float *__restrict__ s,
+                                                    const void *__restrict__ x, int xtype, int64_t n, int64_t k,
+                                                    int64_t kc, void *__restrict__ y, int ytype) {
+  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];  // records, zero block, sums
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int W = (int)(blockDim.x >> 6);
+  const int wr = lane & 31, h = lane >> 5;
+  const int64_t row0 = (int64_t)blockIdx.x * 32;
+  const int64_t rowc = row0 + wr < n ? row0 + wr : n - 1;
+  const int nrec = W * CPW * 4;  // 8-input records of the staged x
+  const int zero_off = 32 * nrec;
+  float *red = reinterpret_cast<float *>(lds + zero_off + 1024);  // [W][32] row sums, then [W] x sums
+
+  // x first (the load counter retires in issue order, so the staging below
+  // then waits for x only): thread t stages record t (inputs 8t .. 8t + 7,
+  // zero past k; every launch has at most one record a thread), loading a
+  // valid record when it has none.
+  const bool f32x = xtype == RQ_F32, bfx = xtype == RQ_BF16;
+  const int e = tid < nrec ? tid : nrec - 1;
+  const bool live = tid < nrec && 8 * (int64_t)e < k;
+  const int64_t el = live ? e : 0;
+  const uint4 *xc = static_cast<const uint4 *>(x);
+  const uint4 xa = xc[f32x ? 2 * el : el];
+  const uint4 xb = xc[f32x ? 2 * el + 1 : el];
+  __builtin_amdgcn_sched_barrier(0);
+  // Weight words of this lane.
+  uint2 wq[CPW];
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    const int64_t c = (int64_t)wave + (int64_t)W * i;
+    const int64_t cc = c < kc ? c : kc - 1;
+    wq[i] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint8_t *>(packed + cc * n + rowc) + 8 * h);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Record e as hi then lo limbs of inputs 0, 2, 4, 6, 1, 3, 5, 7; the
+  // thread's sum of hi + lo.
+  float sx = 0.0f;
+  {
+    const uint32_t va[4] = {xa.x, xa.y, xa.z, xa.w}, vb[4] = {xb.x, xb.y, xb.z, xb.w};
+    float xf[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float e0 = bfx ? __uint_as_float(va[j] << 16) : h2f(va[j]);
+      const float e1 = bfx ? __uint_as_float(va[j] & 0xFFFF0000u) : h2f(va[j] >> 16);
+      const uint32_t f0 = j < 2 ? va[2 * j] : vb[2 * j - 4], f1 = j < 2 ? va[2 * j + 1] : vb[2 * j - 3];
+      xf[2 * j] = live ? (f32x ? __uint_as_float(f0) : e0) : 0.0f;
+      xf[2 * j + 1] = live ? (f32x ? __uint_as_float(f1) : e1) : 0.0f;
+    }
+    const float xo[8] = {xf[0], xf[2], xf[4], xf[6], xf[1], xf[3], xf[5], xf[7]};
+    uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      hi[j] = pk_bf16(xo[2 * j], xo[2 * j + 1]);
+      const float h0 = __uint_as_float(hi[j] << 16), h1 = __uint_as_float(hi[j] & 0xFFFF0000u);
+      lo[j] = pk_bf16(xo[2 * j] - h0, xo[2 * j + 1] - h1);
+      const float l0 = __uint_as_float(lo[j] << 16), l1 = __uint_as_float(lo[j] & 0xFFFF0000u);
+      sx += (h0 + l0) + (h1 + l1);
+    }
+    if (tid < nrec) {
+      *reinterpret_cast<uint4 *>(lds + 32 * e) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+      *reinterpret_cast<uint4 *>(lds + 32 * e + 16) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    }
+  }
+  if (tid < 64) *reinterpret_cast<uint4 *>(lds + zero_off + 16 * tid) = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) sx += __shfl_xor(sx, o);
+  if (lane == 0) red[32 * W + wave] = sx;
+  __syncthreads();
+
+  // A fragment of word j of chunk c for lane (A row a, half h): record
+  // 4c + j, limb a; the MFMA pair of a chunk takes words 2h and 2h + 1.
+  const int ar = lane & 31;
+  const uint32_t abase = ar < 2 ? (uint32_t)(16 * ar + 64 * h) : (uint32_t)zero_off;
+  const uint32_t astride = ar < 2 ? 128u * (uint32_t)W : 0u;  // bytes of records between a wave's chunks
+  const uint8_t *ab = lds + abase + (ar < 2 ? 128u * (uint32_t)wave : 0u);
+  f32x16 acc = {};
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    const uint32_t w0 = wq[i].x, w1 = wq[i].y;
+    const uint32_t sel01 = 0x04010400u, sel23 = 0x04030402u, magic = 0x43434343u;
+    const uint32_t l0 = w0 & 0x0F0F0F0Fu, h0 = (w0 >> 4) & 0x0F0F0F0Fu;
+    const uint32_t l1 = w1 & 0x0F0F0F0Fu, h1 = (w1 >> 4) & 0x0F0F0F0Fu;
+    const mchunk b0 = {__builtin_amdgcn_perm(magic, l0, sel01), __builtin_amdgcn_perm(magic, l0, sel23),
+                       __builtin_amdgcn_perm(magic, h0, sel01), __builtin_amdgcn_perm(magic, h0, sel23)};
+    const mchunk b1 = {__builtin_amdgcn_perm(magic, l1, sel01), __builtin_amdgcn_perm(magic, l1, sel23),
+                       __builtin_amdgcn_perm(magic, h1, sel01), __builtin_amdgcn_perm(magic, h1, sel23)};
+    const uint8_t *a = ab + astride * (uint32_t)i;
+    const bf16x8 a0 = *reinterpret_cast<const bf16x8 *>(a);
+    const bf16x8 a1 = *reinterpret_cast<const bf16x8 *>(a + 32);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, __builtin_bit_cast(bf16x8, b0), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, __builtin_bit_cast(bf16x8, b1), acc, 0, 0, 0);
+  }
+  // Lanes 0..31 hold row wr's hi and lo sums (C rows 0 and 1).
+  if (h == 0) red[32 * wave + wr] = acc[0] + acc[1];
+  __syncthreads();
+  if (tid < 32 && row0 + tid < n) {
+    float v = 0.0f, xt = 0.0f;
+    for (int i = 0; i < W; ++i) v += red[32 * i + tid];
+    for (int i = 0; i < W; ++i) xt += red[32 * W + i];
+    store_out(y, ytype, row0 + tid, fmaf(-136.0f, xt, v) * s[row0 + tid]);
+  }
+}
+
 template <int R, int MT>
 void launch_gemv(const uint4 *packed, const float *s, const void *x, int xtype, int64_t m, int64_t n, int64_t k,
                  int64_t kc, void *y, int ytype, bool vec, hipStream_t st) {
   const dim3 grid((unsigned)((n + R - 1) / R), (unsigned)((m + MT - 1) / MT));
   // MT rows of f32 activations in LDS when they fit in 64 KB.
   const size_t xb = (size_t)MT * k * sizeof(float) <= 65536 ? (size_t)MT * k * sizeof(float) : 0;
+  // Many weights: the matrix-core GEMV (k <= 8192: at most 16 chunks a wave
+  // and 16 waves; x records 4 bytes an input, at most 33 KB of LDS).
+  // (A workgroup a 32-row tile: from n >= 8192 the grid fills the chip;
+  // 4096 x 8192 ran 7.2 -> 10.2 us on 128 workgroups.)
+  if (MT == 1 && m == 1 && vec && k % 32 == 0 && k <= 8192 && n >= 8192 && n * k >= ((int64_t)1 << 24)) {
+    const int64_t cpw = kc <= 64 ? 4 : kc <= 128 ? 8 : 16;
+    const int64_t waves = (kc + cpw - 1) / cpw;
+    const size_t lds = (size_t)waves * cpw * 128 + 1024 + (size_t)(32 * waves + waves) * 4;
+    const mchunk *pk = reinterpret_cast<const mchunk *>(packed);
+    const dim3 g((unsigned)((n + 31) / 32)), b((unsigned)(64 * waves));
+    if (cpw == 4) hipLaunchKernelGGL(k_marlin_mx<4>, g, b, lds, st, pk, s, x, xtype, n, k, kc, y, ytype);
+    else if (cpw == 8) hipLaunchKernelGGL(k_marlin_mx<8>, g, b, lds, st, pk, s, x, xtype, n, k, kc, y, ytype);
+    else hipLaunchKernelGGL(k_marlin_mx<16>, g, b, lds, st, pk, s, x, xtype, n, k, kc, y, ytype);
+    return;
+  }
   // x and its chunk sums in at most 64 KB of LDS; x chunks a thread: k / (4 or 8) / 512 <= 8.
   if (MT == 1 && m == 1 && vec && k % 32 == 0 && (k + kc) * (int64_t)sizeof(float) <= 65536) {
     const int64_t per = (k / (xtype == RQ_F32 ? 4 : 8) + 511) / 512;

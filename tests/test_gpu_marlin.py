@@ -58,7 +58,10 @@ XTYPES = [(torch.float32, 1e-3), (torch.float16, 1e-3), (torch.bfloat16, 1e-2)]
 @pytest.mark.parametrize("xdtype,tol", XTYPES)
 @pytest.mark.parametrize("m,n,k", [(1, 4864, 896), (1, 896, 4864), (2, 32, 50), (3, 300, 100),
                                    (1, 128, 896), (5, 14336, 4096), (9, 40000, 64), (4, 33, 1000),
-                                   (1, 14336, 4096), (1, 40000, 64), (1, 100, 15360), (1, 70, 1000)])
+                                   (1, 14336, 4096), (1, 40000, 64), (1, 100, 15360), (1, 70, 1000),
+                                   # M = 1 with n >= 8192 and n k >= 2^24 on the matrix cores: 4, 8 and 16 chunks a
+                                   # wave, partial 32-row tiles, and (k = 2080) chunk slots past the end
+                                   (1, 16400, 1024), (1, 8210, 4096), (1, 8200, 8192), (1, 8200, 2080)])
 def test_gemv_parity(dev, xdtype, tol, m, n, k):
     rng = np.random.default_rng(m * 1000 + n + k)
     words = rng.integers(0, 2**32, ((k + 31) // 32, n, 4), dtype=np.uint64).astype(np.uint32)
