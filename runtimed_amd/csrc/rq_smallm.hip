@@ -998,7 +998,7 @@ int run_plan(const rq_weight *const *w, int count, bool set, const void *xv, int
   // (a half-block chunk holds twice the weights and activations of a
   // 64-element chunk: smaller batches where registers are short)
   // The activation slice in LDS (the longest slice of the launch, m rows)
-  // for 16 or more activation rows of up to 2048 elements, where it fits
+  // for 16 or more activation rows in slices of up to 2048 elements, where it fits
   // beside the reduction buffer.  Timed in HIP graphs (Q4_K, bf16, distinct
   // weights): 4864 x 896 M = 16 5.41 -> 4.84 us, M = 64 10.86 -> 9.79,
   // 896 x 896 M = 64 6.32 -> 5.61; slower at M = 4 / 8 (the fragments are
@@ -1012,7 +1012,10 @@ int run_plan(const rq_weight *const *w, int count, bool set, const void *xv, int
   // gate and up in one launch, 608, lose: 14.0 -> 14.6 us).
   const size_t part = (size_t)(MT == 4 ? 8 : 4) * MT * 64 * sizeof(f32x4);
   const int64_t per_cu = (int64_t)((160 * 1024) / (part + xbytes));
-  const bool xl = m >= 16 && w[0]->k <= 2048 && xbytes <= kSmXsMax && tiles * p.s <= 320 * (per_cu > 0 ? per_cu : 1);
+  // (The slice, not the row, decides: the down projection 896 x 4864 in four
+  // K slices of 1280 at M = 16 copies 41 KB, 7.80 -> 7.19 us; M = 32
+  // 8.25 -> 8.13; from M = 48 the copy no longer fits.)
+  const bool xl = m >= 16 && cps * C::CE <= 2048 && xbytes <= kSmXsMax && tiles * p.s <= 320 * (per_cu > 0 ? per_cu : 1);
 #define RQ_SM(NW, B, RT)                                                                                     \
   {                                                                                                          \
     if (xl) {                                                                                                \
