@@ -931,7 +931,9 @@ SmPlan smallm_plan(int64_t tiles, int64_t nk, bool can_split) {
   } else {
     if (c <= 4) p = {S, 4, 1, 1};
     else if (c <= 8) p = {S, 4, 2, 1};
-    else if (c <= 16) p = {S, 4, 4, 1};
+    // (split slices of 9-16 chunks at up to 16 rows: eight waves of single
+    // chunks, down 896 x 4864 at M = 16 7.07 -> 6.60 us)
+    else if (c <= 16) p = (MT == 1 && S > 1) ? SmPlan{S, 8, 1, 1} : SmPlan{S, 4, 4, 1};
     else if (c <= 32) p = {S, 8, 4, 1};
     else p = {S, 16, MT == 1 ? 5 : 2, 1};
   }
@@ -1034,6 +1036,9 @@ int run_plan(const rq_weight *const *w, int count, bool set, const void *xv, int
     RQ_SM(4, 1, 1);
   } else {
     if (p.nw == 16) RQ_SM(16, (MT == 1 ? 5 : 2), 1);
+    if constexpr (MT == 1) {
+      if (p.nw == 8 && p.b == 1) RQ_SM(8, 1, 1);
+    }
     if (p.nw == 8) RQ_SM(8, 4, 1);
     if (p.b == 4) {
       if (p.rt == 4) RQ_SM(4, 4, 4);
