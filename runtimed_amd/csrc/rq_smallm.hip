@@ -917,11 +917,18 @@ int dispatch_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hi
 struct SmPlan {
   int s, nw, b, rt;
 };
+// Measured on the Qwen2-0.5B layer (Q4_K, bf16, HIP graphs over distinct
+// weights): up to 8 rows, chunks of 8 or fewer in batches of one (o 896 x 896
+// at M = 8 3.30 -> 3.18 us, gate/up set 5.55 -> 5.04, M = 4 alike); at up to
+// 16 rows a K split of two, not four, with eight waves of single chunks
+// (down 896 x 4864: M = 16 7.27 -> 6.40 us, M = 8 7.51 -> 5.81, M = 4 7.03
+// -> 5.67).
 template <int MT>
-SmPlan smallm_plan(int64_t tiles, int64_t nk, bool can_split) {
+SmPlan smallm_plan(int64_t tiles, int64_t nk, bool can_split, int64_t m) {
   int S = 1;
+  const int smax = MT == 1 ? 2 : 4;
   if (can_split && tiles < 128)
-    while (S < 4 && tiles * S * 2 <= 512 && nk >= 4 * S) S *= 2;
+    while (S < smax && tiles * S * 2 <= 512 && nk >= 4 * S) S *= 2;
   const int64_t c = (nk + S - 1) / S;
   SmPlan p{S, 4, 1, 1};
   if (MT == 4) {
@@ -930,10 +937,9 @@ SmPlan smallm_plan(int64_t tiles, int64_t nk, bool can_split) {
     else p = {S, 16, 1, 1};
   } else {
     if (c <= 4) p = {S, 4, 1, 1};
-    else if (c <= 8) p = {S, 4, 2, 1};
-    // (split slices of 9-16 chunks at up to 16 rows: eight waves of single
-    // chunks, down 896 x 4864 at M = 16 7.07 -> 6.60 us)
-    else if (c <= 16) p = (MT == 1 && S > 1) ? SmPlan{S, 8, 1, 1} : SmPlan{S, 4, 4, 1};
+    else if (c <= 8) p = m <= 8 ? SmPlan{S, 4, 1, 1} : SmPlan{S, 4, 2, 1};
+    else if (MT == 1 && S > 1 && c <= 32) p = {S, 8, 1, 1};
+    else if (c <= 16) p = {S, 4, 4, 1};
     else if (c <= 32) p = {S, 8, 4, 1};
     else p = {S, 16, MT == 1 ? 5 : 2, 1};
   }
@@ -986,16 +992,20 @@ int run_plan(const rq_weight *const *w, int count, bool set, const void *xv, int
   // makes one unsplit batch cheap and the split's last-workgroup sum costs
   // two round trips (896 x 896 at M = 16 4.72 -> 3.98 us, 128 x 896 3.85 ->
   // 3.46, M = 32 4.91 -> 4.52; at M = 64 even, 5.55 vs 5.61).
-  const bool split_ok = !(w[0]->k <= 1024 && m <= 32);
-  SmPlan p = smallm_plan<MT>(tiles, w[0]->k / C::CE,
-                             split_ok && ws != nullptr && tiles <= WsLease::kCounters && m >= 16);
+  // Nor at m <= 64 (o 896 x 896 at M = 64 5.39 -> 5.15 us, q/k/v set 5.66 ->
+  // 5.30, one eight-wave workgroup a tile); below 16 rows only long rows
+  // (more than 32 chunks) split.
+  const bool split_ok = !(w[0]->k <= 1024 && m <= 64);
+  const int64_t nkc = w[0]->k / C::CE;
+  SmPlan p = smallm_plan<MT>(
+      tiles, nkc, split_ok && ws != nullptr && tiles <= WsLease::kCounters && (m >= 16 || nkc > 32), m);
   f32x4 *wsp = nullptr;
   uint32_t *cnt = nullptr;
   if (p.s > 1) {
     int rc = RQ_OK;
     cnt = ws->counters();
     wsp = cnt ? static_cast<f32x4 *>(ws->get((size_t)tiles * p.s * MT * 64 * sizeof(f32x4), &rc)) : nullptr;
-    if (!wsp) p = smallm_plan<MT>(tiles, w[0]->k / C::CE, false);  // no scratch: one workgroup per tile
+    if (!wsp) p = smallm_plan<MT>(tiles, nkc, false, m);  // no scratch: one workgroup per tile
   }
   // (a half-block chunk holds twice the weights and activations of a
   // 64-element chunk: smaller batches where registers are short)
