@@ -832,7 +832,7 @@ int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m
   // layer at m = 2, 150 vs 54 us at m = 16).
   const bool f32x = xtype == RQ_F32 || xtype == RQ_F16;
   if (m >= 4 && m <= 64 && f32x) {
-    const int rc = launch_linear_smallm_f32(wt, x, xtype, m, o, s);
+    const int rc = launch_linear_smallm_f32(wt, x, xtype, m, o, s, &ws);
     if (rc != RQ_E_UNSUPPORTED) return rc;
   }
   // More rows (prefill with f32 activations, the reference's compute type):
@@ -846,7 +846,7 @@ int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m
       const void *xs = static_cast<const uint8_t *>(x) + (size_t)r0 * (size_t)wt->k * xb;
       Out os = o;
       os.y = static_cast<uint8_t *>(o.y) + (size_t)r0 * (size_t)wt->n * yb;
-      const int rc = mm >= 4 ? launch_linear_smallm_f32(wt, xs, xtype, mm, os, s)
+      const int rc = mm >= 4 ? launch_linear_smallm_f32(wt, xs, xtype, mm, os, s, &ws)
                              : launch_linear_fused(wt, xs, xtype, mm, os, s, ws);
       if (rc) return rc;
     }
@@ -878,7 +878,7 @@ int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m
   }
   // Two or three f32 / f16 rows on rows too long for the VALU layouts: the
   // f32 matrix-core kernel takes every format and length (k % 64 == 0).
-  if (rc == RQ_E_UNSUPPORTED && f32x && m >= 2 && m <= 3) rc = launch_linear_smallm_f32(wt, x, xtype, m, o, s);
+  if (rc == RQ_E_UNSUPPORTED && f32x && m >= 2 && m <= 3) rc = launch_linear_smallm_f32(wt, x, xtype, m, o, s, &ws);
   return rc;
 }
 

@@ -264,7 +264,7 @@ int launch_linear_smallm_set(const rq_weight *const *w, int count, const void *x
 // The same for f32 / f16 activations on the f32 matrix cores with exact f32
 // weights (f32 accumulation).
 int launch_linear_smallm_f32(const rq_weight *wt, const void *x, int xtype, int64_t m, const Out &o,
-                             hipStream_t s);
+                             hipStream_t s, WsLease *ws);
 // Every shape and alignment: exact f32 weights decoded element by element
 // from the handle, f32 accumulation (the shapes the fused kernels do not
 // take: rows cut inside a 64-element chunk, rows longer than the GEMV

@@ -817,16 +817,23 @@ __device__ __forceinline__ void mma_chunk_f32(const typename C::Chunk &c, const 
   }
 }
 
+// Split K (S > 1): workgroup b takes row tile b / S and the (b % S)-th of
+// S equal runs of chunks, its partial tile summed as in reduce_split.
 template <class C, int MT, int NW, int B, int XT>
 __global__ __launch_bounds__(64 * NW) void k_smallm_f32(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
                                                         const uint8_t *__restrict__ x, int64_t m, const Out o,
-                                                        int64_t n, int64_t k) {
+                                                        int64_t n, int64_t k, int S, f32x4 *__restrict__ wsp,
+                                                        uint32_t *__restrict__ cnt) {
   __shared__ f32x4 part[NW][1][MT][64];
   const int lane = threadIdx.x & 63, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const int bid = split_order((int)blockIdx.x, (int)gridDim.x, S);
+  const int64_t tile = bid / S;
+  const int sl = bid % S;
+  const int64_t n0 = tile * 16;
   const int64_t row = n0 + (lane & 15) < n ? n0 + (lane & 15) : n - 1;
-  const int64_t nk = k / 64;
+  const int64_t nka = k / 64, cps = (nka + S - 1) / S;
+  const int64_t lo = sl * cps, nk = lo + cps < nka ? lo + cps : nka;
   constexpr int XB = XT == RQ_F32 ? 4 : 2;  // bytes per activation
 
   const uint8_t *xr[MT];
@@ -840,7 +847,7 @@ __global__ __launch_bounds__(64 * NW) void k_smallm_f32(const uint8_t *__restric
 #pragma unroll
   for (int ct = 0; ct < MT; ++ct) acc[0][ct] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
-  for (int64_t t = wave; t < nk; t += B * NW) {
+  for (int64_t t = lo + wave; t < nk; t += B * NW) {
     typename C::Chunk c[B];
     XFragF<MT> xf[B];
 #pragma unroll
@@ -857,42 +864,79 @@ __global__ __launch_bounds__(64 * NW) void k_smallm_f32(const uint8_t *__restric
     }
   }
 
+  if (S > 1) {
+    reduce_split<MT, NW>(part, acc, wave, lane, m, n, n0, o, S, sl, wsp + tile * S * MT * 64, cnt + tile);
+    return;
+  }
   reduce_store<MT, NW>(part, acc, wave, lane, m, n, n0, o);
 }
 
+// Workgroups along K for the f32 kernel, measured on the Qwen2-0.5B layer
+// (Q4_K, HIP graphs over distinct weights): long rows (32 or more 64-element
+// chunks) on few row tiles split four ways (down 896 x 4864: M = 4 12.6 ->
+// 9.0 us, M = 16 14.8 -> 9.9, M = 64 38.5 -> 15.5); above 32 activation rows
+// short rows split too, four ways on few tiles and two on up to 511 (M = 64:
+// o 896 x 896 10.8 -> 7.5, k / v 128 x 896 10.6 -> 6.6, gate 4864 x 896 18.1 ->
+// 15.3); at 32 rows or fewer they lose (o at M = 16 5.3 -> 6.5 in two).
+inline int f32_splits(int64_t tiles, int64_t nk, int64_t m) {
+  if (tiles > WsLease::kCounters) return 1;
+  int S = 1;
+  if (nk >= 32 && tiles < 128) {
+    while (S < 4 && tiles * S * 2 <= 512) S *= 2;
+  } else if (m > 32) {
+    S = tiles < 128 ? 4 : (tiles < 512 ? 2 : 1);
+  }
+  while (S > 1 && nk < S) S /= 2;
+  return S;
+}
+
 template <class C, int MT, int XT>
-int run_mt_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s) {
+int run_mt_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease *ws) {
   constexpr int B = MT == 1 ? 4 : (MT == 2 ? 2 : 1);
-  const dim3 grid((unsigned)((wt->n + 15) / 16));
+  const int64_t tiles = (wt->n + 15) / 16, nk = wt->k / 64;
+  // K split over S workgroups for few row tiles with long rows (the
+  // partials and counters in the workspace; without them, one workgroup a
+  // tile).
+  int S = f32_splits(tiles, nk, m);
+  f32x4 *wsp = nullptr;
+  uint32_t *cnt = nullptr;
+  if (S > 1) {
+    int rc = RQ_OK;
+    cnt = ws ? ws->counters() : nullptr;
+    wsp = cnt ? static_cast<f32x4 *>(ws->get((size_t)tiles * S * MT * 64 * sizeof(f32x4), &rc)) : nullptr;
+    if (!wsp) S = 1;
+  }
+  const dim3 grid((unsigned)(tiles * S));
+  const int64_t ck = (nk + S - 1) / S;  // chunks a workgroup
   const uint8_t *aux = wt->data + wt->aux_off;
   // One and two column tiles with more than one batch a wave: sixteen waves
   // (measured on the 0.5B layer: 896 x 4864 at M = 16 16.9 -> 14.5 us, at
   // M = 32 24.6 -> 20.8; four column tiles and the bf16 kernel were slower).
-  if (MT <= 2 && wt->k / 64 > 4 * B)
+  if (MT <= 2 && ck > 4 * B)
     hipLaunchKernelGGL((k_smallm_f32<C, MT, 16, (MT == 1 ? 2 : 1), XT>), grid, dim3(1024), 0, s, wt->data, aux,
-                       static_cast<const uint8_t *>(x), m, o, wt->n, wt->k);
+                       static_cast<const uint8_t *>(x), m, o, wt->n, wt->k, S, wsp, cnt);
   else
     hipLaunchKernelGGL((k_smallm_f32<C, MT, 4, B, XT>), grid, dim3(256), 0, s, wt->data, aux,
-                       static_cast<const uint8_t *>(x), m, o, wt->n, wt->k);
+                       static_cast<const uint8_t *>(x), m, o, wt->n, wt->k, S, wsp, cnt);
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "small-M launch failed");
 }
 
 template <class C, int XT>
-int run_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s) {
-  if (m <= 16) return run_mt_f32<C, 1, XT>(wt, x, m, o, s);
-  if (m <= 32) return run_mt_f32<C, 2, XT>(wt, x, m, o, s);
-  return run_mt_f32<C, 4, XT>(wt, x, m, o, s);
+int run_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease *ws) {
+  if (m <= 16) return run_mt_f32<C, 1, XT>(wt, x, m, o, s, ws);
+  if (m <= 32) return run_mt_f32<C, 2, XT>(wt, x, m, o, s, ws);
+  return run_mt_f32<C, 4, XT>(wt, x, m, o, s, ws);
 }
 
 template <int XT>
-int dispatch_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s) {
+int dispatch_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease *ws) {
   switch (wt->qtype) {
-    case RQ_Q4_K: return run_f32<SmQ4K, XT>(wt, x, m, o, s);
-    case RQ_Q6_K: return run_f32<SmQ6K, XT>(wt, x, m, o, s);
-    case RQ_Q8_0: return run_f32<SmQ8, XT>(wt, x, m, o, s);
-    case RQ_Q5_K: return run_f32<SmQ5K, XT>(wt, x, m, o, s);
-    case RQ_Q4_0: return run_f32<SmQx0<false>, XT>(wt, x, m, o, s);
-    case RQ_Q5_0: return run_f32<SmQx0<true>, XT>(wt, x, m, o, s);
+    case RQ_Q4_K: return run_f32<SmQ4K, XT>(wt, x, m, o, s, ws);
+    case RQ_Q6_K: return run_f32<SmQ6K, XT>(wt, x, m, o, s, ws);
+    case RQ_Q8_0: return run_f32<SmQ8, XT>(wt, x, m, o, s, ws);
+    case RQ_Q5_K: return run_f32<SmQ5K, XT>(wt, x, m, o, s, ws);
+    case RQ_Q4_0: return run_f32<SmQx0<false>, XT>(wt, x, m, o, s, ws);
+    case RQ_Q5_0: return run_f32<SmQx0<true>, XT>(wt, x, m, o, s, ws);
     default: return RQ_E_UNSUPPORTED;
   }
 }
@@ -1091,10 +1135,10 @@ int dispatch_bf16(const rq_weight *const *w, int count, bool set, const void *x,
 // (dispatched from m = 4, and at m = 2..3 for rows the VALU layouts do not
 // take).
 int launch_linear_smallm_f32(const rq_weight *wt, const void *x, int xtype, int64_t m, const Out &o,
-                             hipStream_t s) {
+                             hipStream_t s, WsLease *ws) {
   if (m < 2 || m > 64 || wt->k % 64 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
-  if (xtype == RQ_F32) return dispatch_f32<RQ_F32>(wt, x, m, o, s);
-  if (xtype == RQ_F16) return dispatch_f32<RQ_F16>(wt, x, m, o, s);
+  if (xtype == RQ_F32) return dispatch_f32<RQ_F32>(wt, x, m, o, s, ws);
+  if (xtype == RQ_F16) return dispatch_f32<RQ_F16>(wt, x, m, o, s, ws);
   return RQ_E_UNSUPPORTED;
 }
 
