@@ -293,6 +293,23 @@ def test_small_m_split_k_under_graph_capture(dev, m):
     _replay_check(lambda: w.forward(x, out_dtype=torch.float32), ref)
 
 
+@pytest.mark.parametrize("m,n,k", [(4, 896, 4864), (16, 896, 4864), (64, 896, 896), (64, 4864, 896)])
+def test_f32_small_m_split_k_under_graph_capture(dev, m, n, k):
+    # f32 activations on the f32 matrix cores: long rows split K four ways,
+    # short rows above 32 activation rows two or four ways; the last
+    # workgroup of a tile adds the partials in a fixed order, so eager calls
+    # and every graph replay give the same bits, within 1e-3 of the oracle
+    print(f"f32 split m={m} n={n} k={k}", flush=True)
+    w, wf = make(rq.Q4_K, n, k, 870 + m + n)
+    x = torch.from_numpy(synth.activations(871 + m, m, k)).to(dev)
+    ref = w.forward(x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert norm_err(ref.cpu().numpy(), oracle.linear_f64(x.cpu().numpy(), wf)) <= TOL_F32
+    for _ in range(3):
+        assert torch.equal(w.forward(x, out_dtype=torch.float32), ref)
+    _replay_check(lambda: w.forward(x, out_dtype=torch.float32), ref)
+
+
 def test_capture_without_warmup(dev):
     # A fresh stream has no workspace yet: under capture the split-K
     # partials and the aligned copy of x come from a buffer allocated outside
