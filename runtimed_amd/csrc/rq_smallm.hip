@@ -912,8 +912,16 @@ int run_mt_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipS
   // One and two column tiles with more than one batch a wave: sixteen waves
   // (measured on the 0.5B layer: 896 x 4864 at M = 16 16.9 -> 14.5 us, at
   // M = 32 24.6 -> 20.8; four column tiles and the bf16 kernel were slower).
+  // One column tile and at most one batch a wave (the 896-long rows):
+  // sixteen waves of one chunk, so each wave's MFMA chain is a quarter as
+  // long (verify with f32 activations on the 0.5B layer, 7 launches: M = 4
+  // 206 -> 214, M = 8 209 -> 219, M = 16 204 -> 217 GB/s; the same for two
+  // column tiles changed nothing, eight waves for four lost 4%).
   if (MT <= 2 && ck > 4 * B)
     hipLaunchKernelGGL((k_smallm_f32<C, MT, 16, (MT == 1 ? 2 : 1), XT>), grid, dim3(1024), 0, s, wt->data, aux,
+                       static_cast<const uint8_t *>(x), m, o, wt->n, wt->k, S, wsp, cnt);
+  else if (MT == 1)
+    hipLaunchKernelGGL((k_smallm_f32<C, 1, 16, 1, XT>), grid, dim3(1024), 0, s, wt->data, aux,
                        static_cast<const uint8_t *>(x), m, o, wt->n, wt->k, S, wsp, cnt);
   else
     hipLaunchKernelGGL((k_smallm_f32<C, MT, 4, B, XT>), grid, dim3(256), 0, s, wt->data, aux,
