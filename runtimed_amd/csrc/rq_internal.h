@@ -265,6 +265,9 @@ int launch_linear_smallm_set(const rq_weight *const *w, int count, const void *x
 // weights (f32 accumulation).
 int launch_linear_smallm_f32(const rq_weight *wt, const void *x, int xtype, int64_t m, const Out &o,
                              hipStream_t s, WsLease *ws);
+// 64 * slices f32 / f16 activation rows as slices of 64 rows in one launch.
+int launch_linear_smallm_f32_slices(const rq_weight *wt, const void *x, int xtype, int64_t slices, const Out &o,
+                                    hipStream_t s, WsLease *ws);
 // Every shape and alignment: exact f32 weights decoded element by element
 // from the handle, f32 accumulation (the shapes the fused kernels do not
 // take: rows cut inside a 64-element chunk, rows longer than the GEMV

@@ -821,7 +821,7 @@ __device__ __forceinline__ void mma_chunk_f32(const typename C::Chunk &c, const 
 // S equal runs of chunks, its partial tile summed as in reduce_split.
 template <class C, int MT, int NW, int B, int XT>
 __global__ __launch_bounds__(64 * NW) void k_smallm_f32(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
-                                                        const uint8_t *__restrict__ x, int64_t m, const Out o,
+                                                        const uint8_t *__restrict__ x, int64_t m_all, const Out o_all,
                                                         int64_t n, int64_t k, int S, f32x4 *__restrict__ wsp,
                                                         uint32_t *__restrict__ cnt) {
   __shared__ f32x4 part[NW][1][MT][64];
@@ -830,6 +830,13 @@ __global__ __launch_bounds__(64 * NW) void k_smallm_f32(const uint8_t *__restric
   const int bid = split_order((int)blockIdx.x, (int)gridDim.x, S);
   const int64_t tile = bid / S;
   const int sl = bid % S;
+  // Slice blockIdx.y: activation rows [16 MT y, 16 MT (y + 1)) of m_all, its
+  // own outputs, partials and tile counters.
+  const int64_t r0 = (int64_t)blockIdx.y * 16 * MT;
+  const int64_t m = m_all - r0 < 16 * MT ? m_all - r0 : 16 * MT;
+  const int64_t stile = (int64_t)blockIdx.y * (gridDim.x / S) + tile;
+  Out o = o_all;
+  o.y = static_cast<uint8_t *>(o_all.y) + r0 * n * (o_all.ytype == RQ_F32 ? 4 : 2);
   const int64_t n0 = tile * 16;
   const int64_t row = n0 + (lane & 15) < n ? n0 + (lane & 15) : n - 1;
   const int64_t nka = k / 64, cps = (nka + S - 1) / S;
@@ -840,7 +847,7 @@ __global__ __launch_bounds__(64 * NW) void k_smallm_f32(const uint8_t *__restric
 #pragma unroll
   for (int ct = 0; ct < MT; ++ct) {
     const int64_t mr = 16 * ct + (lane & 15);
-    xr[ct] = x + ((mr < m ? mr : m - 1) * k + 8 * g) * XB;
+    xr[ct] = x + ((r0 + (mr < m ? mr : m - 1)) * k + 8 * g) * XB;
   }
 
   f32x4 acc[1][MT];
@@ -865,7 +872,7 @@ __global__ __launch_bounds__(64 * NW) void k_smallm_f32(const uint8_t *__restric
   }
 
   if (S > 1) {
-    reduce_split<MT, NW>(part, acc, wave, lane, m, n, n0, o, S, sl, wsp + tile * S * MT * 64, cnt + tile);
+    reduce_split<MT, NW>(part, acc, wave, lane, m, n, n0, o, S, sl, wsp + stile * S * MT * 64, cnt + stile);
     return;
   }
   reduce_store<MT, NW>(part, acc, wave, lane, m, n, n0, o);
@@ -891,22 +898,24 @@ inline int f32_splits(int64_t tiles, int64_t nk, int64_t m) {
 }
 
 template <class C, int MT, int XT>
-int run_mt_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease *ws) {
+int run_mt_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease *ws,
+               int64_t slices = 1) {
   constexpr int B = MT == 1 ? 4 : (MT == 2 ? 2 : 1);
   const int64_t tiles = (wt->n + 15) / 16, nk = wt->k / 64;
   // K split over S workgroups for few row tiles with long rows (the
   // partials and counters in the workspace; without them, one workgroup a
-  // tile).
-  int S = f32_splits(tiles, nk, m);
+  // tile).  Slices of 16 MT activation rows run side by side (grid y), each
+  // with its own row tiles, so the split is planned on all of them.
+  int S = f32_splits(tiles * slices, nk, m / slices);
   f32x4 *wsp = nullptr;
   uint32_t *cnt = nullptr;
   if (S > 1) {
     int rc = RQ_OK;
     cnt = ws ? ws->counters() : nullptr;
-    wsp = cnt ? static_cast<f32x4 *>(ws->get((size_t)tiles * S * MT * 64 * sizeof(f32x4), &rc)) : nullptr;
+    wsp = cnt ? static_cast<f32x4 *>(ws->get((size_t)slices * tiles * S * MT * 64 * sizeof(f32x4), &rc)) : nullptr;
     if (!wsp) S = 1;
   }
-  const dim3 grid((unsigned)(tiles * S));
+  const dim3 grid((unsigned)(tiles * S), (unsigned)slices);
   const int64_t ck = (nk + S - 1) / S;  // chunks a workgroup
   const uint8_t *aux = wt->data + wt->aux_off;
   // One and two column tiles with more than one batch a wave: sixteen waves
@@ -934,6 +943,22 @@ int run_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStre
   if (m <= 16) return run_mt_f32<C, 1, XT>(wt, x, m, o, s, ws);
   if (m <= 32) return run_mt_f32<C, 2, XT>(wt, x, m, o, s, ws);
   return run_mt_f32<C, 4, XT>(wt, x, m, o, s, ws);
+}
+
+// m = 64 * slices activation rows as slices of 64 in one launch.
+template <int XT>
+int dispatch_f32_slices(const rq_weight *wt, const void *x, int64_t slices, const Out &o, hipStream_t s,
+                        WsLease *ws) {
+  const int64_t m = 64 * slices;
+  switch (wt->qtype) {
+    case RQ_Q4_K: return run_mt_f32<SmQ4K, 4, XT>(wt, x, m, o, s, ws, slices);
+    case RQ_Q6_K: return run_mt_f32<SmQ6K, 4, XT>(wt, x, m, o, s, ws, slices);
+    case RQ_Q8_0: return run_mt_f32<SmQ8, 4, XT>(wt, x, m, o, s, ws, slices);
+    case RQ_Q5_K: return run_mt_f32<SmQ5K, 4, XT>(wt, x, m, o, s, ws, slices);
+    case RQ_Q4_0: return run_mt_f32<SmQx0<false>, 4, XT>(wt, x, m, o, s, ws, slices);
+    case RQ_Q5_0: return run_mt_f32<SmQx0<true>, 4, XT>(wt, x, m, o, s, ws, slices);
+    default: return RQ_E_UNSUPPORTED;
+  }
 }
 
 template <int XT>
@@ -1147,6 +1172,15 @@ int launch_linear_smallm_f32(const rq_weight *wt, const void *x, int xtype, int6
   if (m < 2 || m > 64 || wt->k % 64 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
   if (xtype == RQ_F32) return dispatch_f32<RQ_F32>(wt, x, m, o, s, ws);
   if (xtype == RQ_F16) return dispatch_f32<RQ_F16>(wt, x, m, o, s, ws);
+  return RQ_E_UNSUPPORTED;
+}
+
+int launch_linear_smallm_f32_slices(const rq_weight *wt, const void *x, int xtype, int64_t slices, const Out &o,
+                                    hipStream_t s, WsLease *ws) {
+  if (slices < 1 || slices > 65535 || wt->k % 64 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0)
+    return RQ_E_UNSUPPORTED;
+  if (xtype == RQ_F32) return dispatch_f32_slices<RQ_F32>(wt, x, slices, o, s, ws);
+  if (xtype == RQ_F16) return dispatch_f32_slices<RQ_F16>(wt, x, slices, o, s, ws);
   return RQ_E_UNSUPPORTED;
 }
 

@@ -219,10 +219,13 @@ def test_small_m_f32_activations(dev, qtype, m, n, k):
     assert norm_err(y, ref(x.numpy(), wf)) <= TOL_F32
 
 
-# More than 64 f32 rows run as slices of 64 on the same kernel, with a last
-# slice of 1..3 rows on the VALU kernel or the GEMV.
+# More than 64 f32 rows run as slices of 64 side by side in one launch, with
+# the rest (a last slice of 1..3 rows on the VALU kernel or the GEMV) after
+# it; (512, 1000, 1024) splits K two ways over eight slices (tile counters
+# and partials per slice), (300, 2048, 640) runs four slices unsplit.
 @pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0, rq.Q5_0])
-@pytest.mark.parametrize("m,n,k", [(200, 300, 512), (129, 130, 256), (66, 64, 2048), (131, 96, 896)])
+@pytest.mark.parametrize("m,n,k", [(200, 300, 512), (129, 130, 256), (66, 64, 2048), (131, 96, 896),
+                                   (512, 1000, 1024), (300, 2048, 640)])
 def test_f32_activations_sliced(dev, qtype, m, n, k):
     w, wf = make(qtype, n, k, 23 + m)
     x = torch.from_numpy(synth.activations(7 + m, m, k))
