@@ -718,6 +718,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--m", type=int, default=16, help="activation rows of --mode verify")
     ap.add_argument("--multi", action="store_true", help="--mode verify through rq_linear_multi")
+    ap.add_argument("--xdt", choices=["bf16", "f32"], default="bf16", help="activation type of --mode verify")
     ap.add_argument("--mode", choices=["full", "gate", "copy", "fp8", "prefill", "prefill-head", "gemv-large",
                                        "gemv-head", "verify"],
                     default="full",
@@ -751,7 +752,7 @@ def main():
     if args.mode == "gemv-large":
         return mode_gemv_large(torch, rq, synth, dev, args.steps)
     if args.mode == "verify":
-        return mode_verify(torch, rq, synth, dev, args.steps, args.m, multi=args.multi)
+        return mode_verify(torch, rq, synth, dev, args.steps, args.m, xdt=args.xdt, multi=args.multi)
     log(f"decode workload: {args.layers} layer copies, steps={args.steps} warmup={args.warmup}")
     W, ms = decode_workload(torch, rq, synth, args.layers, args.steps, args.warmup, dev)
     step_bytes = layer_bytes() * args.layers
