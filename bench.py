@@ -25,6 +25,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -386,17 +387,21 @@ def extra_fp8(torch, rq, synth, dev, steps, warmup):
         rq.fp8_gemm(x, wq, ws, mode=rq.FP8_PER_TOKEN, out=y)
 
     # four calls per graph, timed over replays (a one-node graph's replay
-    # adds several microseconds of its own)
+    # adds several microseconds of its own).  The three graphs are timed in
+    # turn over five rounds, each round starting with the next of them, and
+    # each figure is the median of its five: timed one after the other once,
+    # whichever ran later ran on a warmer, faster-clocked GPU.
     reps = 4
     t = Timer(torch)
-
-    def timed(fn):
-        g = capture(torch, lambda: [fn() for _ in range(reps)])
-        ms = t.replay(g, steps, warmup) / reps
-        del g
-        return ms
-
-    ms_q, ms_g, ms_b = timed(quant), timed(gemm), timed(both)
+    fns = {"quant": quant, "gemm": gemm, "both": both}
+    graphs = {nm: capture(torch, lambda fn=fn: [fn() for _ in range(reps)]) for nm, fn in fns.items()}
+    samples = {nm: [] for nm in fns}
+    order = list(fns)
+    for r in range(5):
+        for nm in order[r % 3:] + order[:r % 3]:
+            samples[nm].append(t.replay(graphs[nm], max(2, steps // 2), warmup if r == 0 else 1) / reps)
+    del graphs
+    ms_q, ms_g, ms_b = (statistics.median(samples[nm]) for nm in ("quant", "gemm", "both"))
     tf = 2.0 * m * n * k / (ms_b * 1e-3) / 1e12
     tf_g = 2.0 * m * n * k / (ms_g * 1e-3) / 1e12
     return {"workload": "FP8 e4m3 GEMM 2048x14336x4096, per-token activation quantize + GEMM, bf16 out",

@@ -200,11 +200,10 @@ int rq_linear(const rq_weight *w, const void *x, int xtype, int64_t m, int64_t k
 
 /* rq_linear plus a bias of n values (type btype in {F32, F16, BF16}, device
  * memory) added to every row, as linear_bias does (the bias cast to y's
- * type, then added).  The add happens in the kernels' epilogues: y =
- * acc + (bias as ytype), rounded once to ytype.  For F32 outputs that is the
- * reference's sum exactly; for BF16 / F16 outputs it may differ by one unit
- * in the last place from linear_bias's two roundings (rq_linear followed by
- * rq_bias_add reproduces those).  A null bias is rq_linear. */
+ * type, then added).  The add happens in the kernels' epilogues with the
+ * reference's two roundings: y = ((acc as ytype) + (bias as ytype)) as ytype,
+ * the same bits as rq_linear followed by rq_bias_add (for F32 outputs both
+ * roundings are the identity).  A null bias is rq_linear. */
 int rq_linear_bias(const rq_weight *w, const void *x, int xtype, int64_t m, int64_t k, const void *bias, int btype,
                    void *y, int ytype, void *stream);
 
@@ -294,7 +293,9 @@ int rq_marlin_linear(const uint32_t *packed, const float *scales, int64_t n, int
  * q (b*h*sd bytes) = f32_to_fp8_e4m3(t / s) or (i8)clamp(round(t / s),
  * -128, 127) (NaN -> 0).  RQ_KV_F16: q holds b*h*sd f16 (t cast, round to
  * nearest even) and every scale is 1.  The per-head partial maxima live in
- * the stream's workspace. */
+ * the stream's workspace.  With b = 0 or sd = 0 (no elements) every scale is
+ * the floor (1e-8, or 1 for RQ_KV_F16), written by a kernel; no call reads
+ * host memory at launch time, so every shape may be captured in a graph. */
 int rq_kv_quantize(const void *t, int ttype, int64_t b, int64_t h, int64_t sd, int mode, void *q,
                    float *scales, void *stream);
 

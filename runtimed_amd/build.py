@@ -9,6 +9,7 @@ import concurrent.futures
 import os
 import subprocess
 import sys
+import time
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -35,17 +36,34 @@ COMMON = [
 def _compile(src: str) -> Path:
     obj = OUT / (Path(src).stem + ".o")
     cmd = [HIPCC, *COMMON, "-x", "hip", "-c", str(PKG / src), "-o", str(obj)]
+    started = time.time()
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{res.stderr}")
+    # the object is as old as the sources it was compiled from: an edit made
+    # while it compiled leaves it stale for an incremental build
+    os.utime(obj, (started, started))
     return obj
 
 
-def build(verbose: bool = False) -> Path:
+def _stale(src: str) -> bool:
+    """An object older than its source or than any header it may include."""
+    obj = OUT / (Path(src).stem + ".o")
+    if not obj.exists():
+        return True
+    deps = [PKG / src, *CSRC.glob("*.h"), *(PKG / "host").glob("*.hpp"), *(ROOT / "include").glob("*.h")]
+    return any(d.stat().st_mtime > obj.stat().st_mtime for d in deps)
+
+
+def build(verbose: bool = False, incremental: bool = False) -> Path:
+    """Compile every source (or, with incremental, only sources whose object
+    is stale) and link librq.so."""
     OUT.mkdir(exist_ok=True)
     srcs = [s for s in SOURCES if (PKG / s).exists()]
-    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
+    todo = [s for s in srcs if _stale(s)] if incremental else srcs
+    with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, min(8, len(todo)))) as ex:
+        list(ex.map(_compile, todo))
+    objs = [OUT / (Path(s).stem + ".o") for s in srcs]
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -73,5 +91,5 @@ def build_host_tests(verbose: bool = False) -> Path:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, incremental="--incremental" in sys.argv)
     sys.exit(0)

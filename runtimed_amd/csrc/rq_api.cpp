@@ -456,11 +456,9 @@ int rq_kv_quantize(const void *t, int ttype, int64_t b, int64_t h, int64_t sd, i
   if (h == 0) return RQ_OK;
   if (!scales) return set_error(RQ_E_ARG, "null scales");
   if (b == 0 || sd == 0) {
-    // No elements: every head's maximum is 0, so its scale is the floor.
-    std::vector<float> fill((size_t)h, mode == RQ_KV_F16 ? 1.0f : 1e-8f);
-    const hipError_t e = hipMemcpyAsync(scales, fill.data(), (size_t)h * sizeof(float), hipMemcpyHostToDevice,
-                                        as_stream(stream));
-    return hip_check(e, "hipMemcpyAsync");
+    // No elements: every head's maximum is 0, so its scale is the floor,
+    // written by a kernel (nothing read from host memory at replay time).
+    return launch_kv_fill_scales(scales, h, mode == RQ_KV_F16 ? 1.0f : 1e-8f, as_stream(stream));
   }
   if (!t || !q) return set_error(RQ_E_ARG, "null argument");
   int dev = 0;

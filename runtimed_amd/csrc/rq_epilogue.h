@@ -139,6 +139,9 @@ __device__ __forceinline__ void store_tile32(const rq_f32x16 &acc, const Out &o,
                                              bool vec) {
   const int h = lane >> 5;
   const int ytype = o.ytype;
+  // with a bias and a 16-bit output, the product is rounded to y's type
+  // before the (rounded) bias is added, as with_bias does
+  const bool twice = o.bias && ytype != RQ_F32;
   if (vec && row0 + 32 <= m && col0 + 32 <= n) {
     const int t = lane & 3;
     const int64_t col = col0 + (lane & 28);
@@ -152,6 +155,12 @@ __device__ __forceinline__ void store_tile32(const rq_f32x16 &acc, const Out &o,
         v1 *= sx[g] * sw[1];
         v2 *= sx[g] * sw[2];
         v3 *= sx[g] * sw[3];
+      }
+      if (twice) {
+        v0 = round_as(ytype, v0);
+        v1 = round_as(ytype, v1);
+        v2 = round_as(ytype, v2);
+        v3 = round_as(ytype, v3);
       }
       v0 += bb[0];
       v1 += bb[1];
@@ -169,7 +178,7 @@ __device__ __forceinline__ void store_tile32(const rq_f32x16 &acc, const Out &o,
       if (row < m && col < n) {
         float v = acc[r];
         if (SCALED) v *= (xs ? xs[row] : 1.0f) * swe;
-        store_one(o.y, ytype, row * n + col, v + be);
+        store_one(o.y, ytype, row * n + col, (twice ? round_as(ytype, v) : v) + be);
       }
     });
   }
@@ -189,10 +198,12 @@ __device__ __forceinline__ void store_tile32(const rq_f32x16 &acc, const Out &o,
 // A wave's 128 x 128 block (4 x 4 MFMA tiles of 32 x 32, rows rb.., columns
 // cb.. of the staged tile) into T; values scaled by sx * sw when SCALED,
 // plus the biases bb (rounded as tile_col_bias leaves them; 0 without one).
+// twice: a bias is present, so each value is rounded to y's type before its
+// bias is added (with_bias).
 template <bool SCALED>
 __device__ __forceinline__ void stage_block_2b(const rq_f32x16 (&acc)[4][4], uint8_t *T, int rb, int cb, int ytype,
                                                const float (&sx)[4][4], const float (&sw)[4][4],
-                                               const float (&bb)[4][4], int lane) {
+                                               const float (&bb)[4][4], bool twice, int lane) {
   const int h = lane >> 5, t = lane & 3;
   static_for<4>([&](auto I) {
     static_for<4>([&](auto J) {
@@ -206,6 +217,12 @@ __device__ __forceinline__ void stage_block_2b(const rq_f32x16 (&acc)[4][4], uin
           v1 *= sx[I][g] * sw[J][1];
           v2 *= sx[I][g] * sw[J][2];
           v3 *= sx[I][g] * sw[J][3];
+        }
+        if (twice) {
+          v0 = round_as(ytype, v0);
+          v1 = round_as(ytype, v1);
+          v2 = round_as(ytype, v2);
+          v3 = round_as(ytype, v3);
         }
         v0 += bb[J][0];
         v1 += bb[J][1];

@@ -61,14 +61,6 @@ __global__ __launch_bounds__(256) void k_fp8_quant_rows(const void *__restrict__
   if (tid == 0) xs[row] = amax / 448.0f;
 }
 
-
-// The same per-token encode with one wave per activation row (four rows a
-// workgroup): the row's maximum from 16-byte loads and a wave reduction,
-// then the codes from a second pass over the row (an L2 hit), 4 (f32) or 8
-// (f16 / bf16) codes per store.  Same codes and scales as k_fp8_quant_rows
-// (the maximum is exact in any order).  One workgroup per row with scalar
-// 2-byte loads took 21 us on 2048 x 4096 bf16, and so did this kernel with
-// one load per loop iteration (each waiting for the last).
 // The same per-token encode with one wave per activation row (four rows a
 // workgroup): the row's maximum from 16-byte loads and a wave reduction,
 // then the codes from a second pass over the row (an L2 hit, or the
@@ -431,7 +423,7 @@ __global__ __launch_bounds__(256) void k_fp8_gemm_pipe(const uint8_t *__restrict
   if (ytype != RQ_F32 && vec && n % 8 == 0 && m0 + 256 <= m && n0 + 256 <= n) {
     __syncthreads();  // every wave's stage reads are done
     const float nob[4][4] = {};
-    stage_block_2b<true>(acc, SM, 128 * wm, 128 * wn, ytype, sx, sw, nob, lane);
+    stage_block_2b<true>(acc, SM, 128 * wm, 128 * wn, ytype, sx, sw, nob, false, lane);
     __syncthreads();
     store_staged_2b(SM, y, n, m0, n0, threadIdx.x);
     return;

@@ -306,7 +306,7 @@ __device__ __forceinline__ void pipe_store(const f32x16 (&acc)[4][4], uint8_t *S
   if (o.ytype != RQ_F32 && vec && n % 8 == 0 && m0 + 256 <= m && n0 + 256 <= n) {
     __syncthreads();  // every wave's stage reads are done
     const float ones[4][4] = {};
-    stage_block_2b<false>(acc, SM, 128 * wm, 128 * wn, o.ytype, ones, ones, bb, lane);
+    stage_block_2b<false>(acc, SM, 128 * wm, 128 * wn, o.ytype, ones, ones, bb, o.bias != nullptr, lane);
     __syncthreads();
     store_staged_2b(SM, o.y, n, m0, n0, tid);
     return;

@@ -22,6 +22,7 @@
 #include <stdint.h>
 
 #include <utility>
+#include <vector>
 
 #include "../../include/rq.h"
 
@@ -205,9 +206,11 @@ class WsLease {
   WsLease(const WsLease &) = delete;
   WsLease &operator=(const WsLease &) = delete;
   // `bytes` of device memory (256-byte aligned) for this call; null with
-  // *rc set (and the error message) on failure.  Earlier pointers of the same
-  // lease stay valid.
-  void *get(size_t bytes, int *rc);
+  // *rc set on failure, and the thread's error message too unless `quiet`
+  // (a caller with a path that needs no scratch passes quiet, so a call that
+  // succeeds leaves no stale message).  Earlier pointers of the same lease
+  // stay valid.
+  void *get(size_t bytes, int *rc, bool quiet = false);
   // kCounters u32 of the slot that are zero between calls: a kernel that
   // counts in them must leave them zero when it ends.  Made (and zeroed)
   // on the first request outside stream capture; null under capture before
@@ -222,8 +225,7 @@ class WsLease {
   hipStream_t s_;
   bool capturing_ = false;
   size_t used_ = 0;
-  void *async_[4] = {nullptr, nullptr, nullptr, nullptr};  // freed in stream order when the lease ends
-  int n_async_ = 0;
+  std::vector<void *> async_;  // freed in stream order when the lease ends
 };
 
 // ---- launchers (each returns RQ_OK or an error code and message) ----
@@ -293,6 +295,8 @@ int launch_kv_quantize(const void *t, int ttype, int64_t b, int64_t h, int64_t s
                        float *scales, hipStream_t s, WsLease &ws);
 int launch_kv_dequantize(const void *q, int mode, const float *scales, int64_t b, int64_t h, int64_t sd, void *out,
                          int otype, hipStream_t s);
+// scales[0 .. h) = v on the stream (a kernel: safe under graph capture).
+int launch_kv_fill_scales(float *scales, int64_t h, float v, hipStream_t s);
 
 // ---- exact scalar conversions shared by device code ----
 
@@ -368,12 +372,14 @@ __device__ __forceinline__ float bias_at(const Out &o, int64_t col) {
 }
 
 // linear_bias (linear_layer.rs:107-118) adds the bias cast to y's dtype to
-// linear's result cast to y's dtype.  Fused into an epilogue, the f32 sum
-// acc + (bias as ytype) is rounded once by the store: for f32 outputs that
-// is the reference's acc + b exactly; for bf16 / f16 outputs it can differ
-// from the reference's two roundings by one unit in the last place of y
-// (and is the nearer of the two to the exact sum).
-__device__ __forceinline__ float with_bias(float acc, float b, int ytype) { return acc + round_as(ytype, b); }
+// linear's result cast to y's dtype, and the broadcast add rounds the sum to
+// y's dtype again.  Fused into an epilogue the same two roundings happen:
+// acc rounded to ytype, plus the bias rounded to ytype, summed in f32 (exact
+// for two bf16 / f16 values of one output) and rounded by the store.  For
+// f32 outputs both roundings are the identity.
+__device__ __forceinline__ float with_bias(float acc, float b, int ytype) {
+  return round_as(ytype, acc) + round_as(ytype, b);
+}
 
 // Output (row, col) of a linear call, with its bias.
 __device__ __forceinline__ void store_linear(const Out &o, int64_t row, int64_t n, int64_t col, float acc) {

@@ -274,6 +274,14 @@ __global__ __launch_bounds__(KV_THREADS) void k_kv_decode(const void *__restrict
   }
 }
 
+// Every head's scale set to one value (the floor of a head with no
+// elements).  A kernel, not a copy from host memory, so that a caller may
+// capture it in a graph.
+__global__ __launch_bounds__(256) void k_kv_fill_scales(float *__restrict__ scales, int64_t h, float v) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < h) scales[i] = v;
+}
+
 int last_launch(const char *what) {
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "%s launch: %s", what, hipGetErrorString(e));
@@ -348,6 +356,11 @@ int launch_kv_quantize(const void *t, int ttype, int64_t b, int64_t h, int64_t s
     rc = last_launch("kv encode");
   }
   return rc;
+}
+
+int launch_kv_fill_scales(float *scales, int64_t h, float v, hipStream_t s) {
+  hipLaunchKernelGGL(k_kv_fill_scales, dim3((unsigned)((h + 255) / 256)), dim3(256), 0, s, scales, h, v);
+  return last_launch("kv scale fill");
 }
 
 int launch_kv_dequantize(const void *q, int mode, const float *scales, int64_t b, int64_t h, int64_t sd, void *out,

@@ -524,10 +524,13 @@ __device__ __forceinline__ void reduce_store(f32x4 (&part)[NW][RT][MT][64], cons
 // cnt (left at zero for the next call) adds the S partials in order
 // s = 0 .. S - 1 -- the same order whichever arrives last -- and stores.
 // Partials, counter and reads are agent-scope relaxed atomics, which the
-// XCDs' separate L2 caches keep coherent at the device's memory; the
-// workgroup barrier waits for every wave's partial stores to complete
-// before the count.  (Agent-scope fences instead would write back and
-// invalidate whole L2 caches per workgroup: measured slower than no split.)
+// XCDs' separate L2 caches keep coherent at the device's memory.  Every
+// thread waits for its own partial stores to be acknowledged
+// (s_waitcnt vmcnt(0)) before the workgroup barrier, so no store is still in
+// flight when thread 0 counts the workgroup in: a barrier alone orders only
+// issue, and a workgroup-scope release waits for LDS, not for global stores.
+// (Agent-scope fences instead would write back and invalidate whole L2
+// caches per workgroup: measured slower than no split.)
 __device__ __forceinline__ void store_agent(f32x4 *p, const f32x4 &v) {
   uint64_t *q = reinterpret_cast<uint64_t *>(p);
   __hip_atomic_store(q, __builtin_bit_cast(uint64_t, (float2v){v[0], v[1]}), __ATOMIC_RELAXED,
@@ -558,6 +561,7 @@ __device__ __forceinline__ void reduce_split(f32x4 (&part)[NW][1][MT][64], const
     for (int q = 1; q < NW; ++q) v += part[q][0][ct][l];
     store_agent(wsp + (int64_t)s * MT * 64 + slot, v);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t before = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -912,7 +916,8 @@ int run_mt_f32(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipS
   if (S > 1) {
     int rc = RQ_OK;
     cnt = ws ? ws->counters() : nullptr;
-    wsp = cnt ? static_cast<f32x4 *>(ws->get((size_t)slices * tiles * S * MT * 64 * sizeof(f32x4), &rc)) : nullptr;
+    wsp = cnt ? static_cast<f32x4 *>(ws->get((size_t)slices * tiles * S * MT * 64 * sizeof(f32x4), &rc, true))
+              : nullptr;
     if (!wsp) S = 1;
   }
   const dim3 grid((unsigned)(tiles * S), (unsigned)slices);
@@ -1084,7 +1089,7 @@ int run_plan(const rq_weight *const *w, int count, bool set, const void *xv, int
   if (p.s > 1) {
     int rc = RQ_OK;
     cnt = ws->counters();
-    wsp = cnt ? static_cast<f32x4 *>(ws->get((size_t)tiles * p.s * MT * 64 * sizeof(f32x4), &rc)) : nullptr;
+    wsp = cnt ? static_cast<f32x4 *>(ws->get((size_t)tiles * p.s * MT * 64 * sizeof(f32x4), &rc, true)) : nullptr;
     if (!wsp) p = smallm_plan<MT>(tiles, nkc, false, m);  // no scratch: one workgroup per tile
   }
   // (a half-block chunk holds twice the weights and activations of a

@@ -94,11 +94,16 @@ void WsLease::acquire() {
 }
 
 WsLease::~WsLease() {
-  for (int i = 0; i < n_async_; ++i) (void)hipFreeAsync(async_[i], s_);
+  for (void *p : async_) (void)hipFreeAsync(p, s_);
   if (slot_) slot_->mu.unlock();
 }
 
-void *WsLease::get(size_t bytes, int *rc) {
+void *WsLease::get(size_t bytes, int *rc, bool quiet) {
+  auto fail = [&](int code, const char *what, size_t want, hipError_t e) -> void * {
+    (void)hipGetLastError();
+    *rc = quiet ? code : set_error(code, "%s of %zu bytes: %s", what, want, hipGetErrorString(e));
+    return nullptr;
+  };
   if (!slot_) acquire();
   bytes = (bytes + 255) & ~(size_t)255;
   if (bytes == 0) bytes = 256;
@@ -134,18 +139,10 @@ void *WsLease::get(size_t bytes, int *rc) {
         return p;
       }
     }
-    if (n_async_ == 4) {
-      *rc = set_error(RQ_E_NOMEM, "more than four workspace requests in one call");
-      return nullptr;
-    }
     void *p = nullptr;
     const hipError_t e = hipMallocAsync(&p, bytes, s_);
-    if (e != hipSuccess) {
-      *rc = set_error(e == hipErrorOutOfMemory ? RQ_E_NOMEM : RQ_E_DEVICE, "workspace of %zu bytes: %s", bytes,
-                      hipGetErrorString(e));
-      return nullptr;
-    }
-    async_[n_async_++] = p;
+    if (e != hipSuccess) return fail(e == hipErrorOutOfMemory ? RQ_E_NOMEM : RQ_E_DEVICE, "workspace", bytes, e);
+    async_.push_back(p);
     return p;
   }
   if (!slot_->ptr || used_ + bytes > slot_->bytes) {
@@ -153,22 +150,11 @@ void *WsLease::get(size_t bytes, int *rc) {
     want = (want + kGrain - 1) / kGrain * kGrain;
     void *p = nullptr;
     const hipError_t e = hipMallocAsync(&p, want, s_);
-    if (e != hipSuccess) {
-      *rc = set_error(e == hipErrorOutOfMemory ? RQ_E_NOMEM : RQ_E_DEVICE, "workspace of %zu bytes: %s", want,
-                      hipGetErrorString(e));
-      return nullptr;
-    }
+    if (e != hipSuccess) return fail(e == hipErrorOutOfMemory ? RQ_E_NOMEM : RQ_E_DEVICE, "workspace", want, e);
     // The old buffer may still serve launches of this call (earlier
     // requests) and of earlier calls: freed in stream order at the end of
     // this lease, or kept if a graph may refer to it.
-    if (slot_->ptr && !slot_->graph_ref) {
-      if (n_async_ == 4) {
-        (void)hipFreeAsync(p, s_);
-        *rc = set_error(RQ_E_NOMEM, "more than four workspace requests in one call");
-        return nullptr;
-      }
-      async_[n_async_++] = slot_->ptr;
-    }
+    if (slot_->ptr && !slot_->graph_ref) async_.push_back(slot_->ptr);
     slot_->ptr = p;
     slot_->bytes = want;
     slot_->graph_ref = false;

@@ -73,6 +73,23 @@ bool block_geometry(uint32_t t, size_t *elems, size_t *bytes) {
 
 bool librq_decodes(uint32_t t) { return t == 2 || t == 6 || t == 8 || t == 12 || t == 13 || t == 14; }
 
+// to_candle_quantized_dtype (load_gguf.rs:11-26): the block formats whose
+// 2-D tensors the reference loads as candle QMatMul (Q4_1 and Q5_1 among
+// them, though tensor_bytes rejects those first for want of a geometry).
+bool candle_quantized(uint32_t t) { return (t >= 2 && t <= 3) || (t >= 6 && t <= 8) || (t >= 10 && t <= 14); }
+
+const char *format_name(uint32_t t) {
+  switch (t) {
+    case 3: return "Q4_1";
+    case 7: return "Q5_1";
+    case 9: return "Q8_1";
+    case 10: return "Q2_K";
+    case 11: return "Q3_K";
+    case 15: return "Q8_K";
+    default: return "block format";
+  }
+}
+
 // Cursor over the mapped bytes (header.rs:41-107).
 struct Cursor {
   const uint8_t *data;
@@ -506,18 +523,28 @@ Weights Weights::load(const GgufFile &file, int device) {
   for (const auto &info : file.tensors) {
     size_t len = 0;
     const uint8_t *raw = file.tensor_bytes(info, &len);
-    if (info.dims.size() == 2 && info.dtype != 0 && info.dtype != 1 && info.dtype != 30) {
+    if (info.dims.size() == 2 && candle_quantized(info.dtype)) {
       if (!librq_decodes(info.dtype))
-        throw ModelError(ModelError::Config, "tensor '" + info.name + "': block format " + std::to_string(info.dtype) + " has no device decoder");
+        throw ModelError(ModelError::Candle, "tensor '" + info.name + "': " + format_name(info.dtype) + " (dtype " +
+                                                 std::to_string(info.dtype) +
+                                                 ") is a candle-only block format: librq has no decoder for it");
       auto q = std::make_shared<QMatMul>((int)info.dtype, raw, len, (size_t)info.dims[1], (size_t)info.dims[0], device);
       if (info.name == "token_embd.weight" && !untied) w.q_map_["output.weight"] = q;  // load_gguf.rs:89-97
       w.q_map_[info.name] = q;
       continue;
     }
-    const DType t = info.dtype == 0 ? DType::F32 : info.dtype == 1 ? DType::F16 : info.dtype == 30 ? DType::BF16 : DType::U8;
     std::vector<size_t> dims(info.dims.rbegin(), info.dims.rend());
-    if (t == DType::U8) dims = {len};
-    Tensor dense = Tensor::from_host(raw, dims, t, device);
+    Tensor dense;
+    if (info.dtype == 0 || info.dtype == 1 || info.dtype == 30) {
+      const DType t = info.dtype == 0 ? DType::F32 : info.dtype == 1 ? DType::F16 : DType::BF16;
+      dense = Tensor::from_host(raw, dims, t, device);
+    } else {
+      // tensor_f32 (header.rs:207-211): dequant_tensor to f32, with its errors
+      if (!librq_decodes(info.dtype))
+        throw GgufError(GgufError::Unsupported, "tensor '" + info.name + "': " + format_name(info.dtype) +
+                                                    " (dtype " + std::to_string(info.dtype) + ") does not decode");
+      dense = QMatMul((int)info.dtype, raw, len, 1, info.n_elements, device).dequantize().reshaped(dims);
+    }
     if (info.name == "token_embd.weight" && !untied) w.map_["output.weight"] = dense;
     w.map_[info.name] = dense;
   }

@@ -44,9 +44,15 @@ struct GgufError : std::runtime_error {
   bool is_missing() const { return kind == Io; }
 };
 
-// ModelError (crates/runtimed-model/src/error.rs:5-27)
+// ModelError (crates/runtimed-model/src/error.rs:5-27).  Candle is the
+// reference's tensor-error variant ("tensor: ..."); this mirror raises it for
+// a 2-D Q2_K or Q3_K tensor, which the reference hands to candle's QMatMul
+// (load_gguf.rs:11-26) but librq has no decoder for: there is no candle here
+// to hold it (the Rust binding keeps such tensors on candle).  Q4_1 and Q5_1
+// never get that far: tensor_bytes has no geometry for them and fails with
+// GgufError::Unsupported, here as in the reference (header.rs:191-194).
 struct ModelError : std::runtime_error {
-  enum Kind { Arch, Config, MissingWeight, Shape, Gguf };
+  enum Kind { Arch, Config, MissingWeight, Shape, Gguf, Candle };
   Kind kind;
   std::string name;
   std::vector<size_t> expected, got;
@@ -203,9 +209,14 @@ class Weights {
   static Weights from_parts(int device, std::unordered_map<std::string, Tensor> map);
   static Weights from_quantized(int device, std::unordered_map<std::string, Tensor> map,
                                 std::unordered_map<std::string, std::shared_ptr<QMatMul>> q_map);
-  // load_gguf.rs:40-120: 2-D quantized tensors become QMatMul handles (raw
-  // block bytes uploaded as they are), dense tensors are uploaded as their
-  // dtype; a missing output.weight aliases token_embd.weight.
+  // load_gguf.rs:40-120: 2-D tensors in the block formats the reference maps
+  // to candle (load_gguf.rs:11-26) become QMatMul handles (raw block bytes
+  // uploaded as they are), or raise ModelError::Candle for Q2_K / Q3_K,
+  // which librq does not decode; every other tensor goes the reference's
+  // tensor_f32 way: F32 / F16 / BF16 uploaded as their dtype, block formats
+  // decoded to F32 (GgufError::Unsupported where dequant_tensor has no
+  // decoder, dequant.rs:143).  A missing output.weight aliases
+  // token_embd.weight.
   static Weights load(const GgufFile &file, int device);
 
   Tensor linear(const Tensor &x, const std::string &name) const;        // linear_layer.rs:45-66

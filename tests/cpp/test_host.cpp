@@ -181,6 +181,25 @@ static void cpu_tests() {
     CHECK(n && n->offset % 64 == 0 && n->offset - t->offset == 576);
     CHECK(g.tensor("missing") == nullptr);
   });
+  run("load_formats_without_a_librq_decoder", [] {  // load_gguf.rs:11-26, header.rs:191-211
+    // Q2_K / Q3_K: the reference loads them into candle's QMatMul; librq has
+    // no decoder, so the mirror raises its distinct ModelError::Candle
+    for (uint32_t t : {10u, 11u}) {
+      std::vector<uint8_t> data(2 * (t == 10 ? 84 : 110), 0x11);
+      auto g = GgufFile::parse(forge({{"blk.0.ffn_up.weight", {256, 2}, t, data}}));
+      auto e = expect_throw<ModelError>([&] { Weights::load(g, 0); });
+      CHECK(e.kind == ModelError::Candle);
+      CHECK(std::string(e.what()).find("candle-only") != std::string::npos);
+    }
+    // Q4_1 / Q5_1 (mapped to candle too) and Q8_1 (not mapped): tensor_bytes
+    // has no geometry for them, GgufError::Unsupported as in the reference
+    for (uint32_t t : {3u, 7u, 9u}) {
+      std::vector<uint8_t> data(8 * 40, 0);
+      auto g = GgufFile::parse(forge({{"blk.0.ffn_up.weight", {256, 1}, t, data}}));
+      auto e = expect_throw<GgufError>([&] { Weights::load(g, 0); });
+      CHECK(e.kind == GgufError::Unsupported);
+    }
+  });
   run("truncated_tensor_is_range_error", [] {
     auto bytes = forge({{"w", {256, 2}, 12, rand_blocks(12, 2)}});
     bytes.resize(bytes.size() - 10);
@@ -309,6 +328,20 @@ static void gpu_tests() {
         CHECK(norm_err(y.to_vec<float>(), r) <= 1e-3);
       }
     }
+  });
+  run("load_gguf_one_dim_block_tensor_as_f32", [] {  // load_gguf.rs:107-110: tensor_f32
+    // a block-format tensor that is not 2-D is decoded to dense f32, as the
+    // reference's tensor_f32 does, bit-exact against the oracle
+    auto b8 = rand_blocks(8, 16);
+    auto g = GgufFile::parse(forge({{"blk.0.attn_norm.weight", {512}, 8, b8}}));
+    auto w = Weights::load(g, 0);
+    CHECK(w.q_matmul("blk.0.attn_norm.weight") == nullptr);
+    auto got = w.get("blk.0.attn_norm.weight");
+    CHECK((got.dims() == std::vector<size_t>{512}) && got.dtype() == DType::F32);
+    std::vector<float> want(512);
+    CHECK(rqo_dequant_tensor(8, b8.data(), b8.size(), 512, want.data()) == 0);
+    auto v = got.to_vec<float>();
+    CHECK(std::memcmp(v.data(), want.data(), want.size() * 4) == 0);
   });
   run("cpu_fp8_gemm_matches_reference", [] {  // fp8_gemm.rs:198-208, on the device
     std::vector<float> xv{1, 2, 3, 4};

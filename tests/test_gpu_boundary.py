@@ -74,17 +74,12 @@ def test_linear_bias_every_route(dev, qtype, n, k, m, xdt, bdt):
         tol = TOL_F32 if exact and ydt == torch.float32 else TOL_BF16
         err = norm_err(y.float().cpu().numpy(), r)
         assert err <= tol, (ydt, err)
-        # against linear then the broadcast add: identical for f32 outputs; for
-        # bf16 the fused sum is rounded once instead of twice, so the two
-        # differ by at most about one unit in the last place
-        y_nb = w.forward(x, out_dtype=ydt)
-        y0 = y_nb.clone()
+        # against linear then the broadcast add (linear_layer.rs:107-118: y
+        # rounded to its dtype, the bias cast to it, the sum rounded again):
+        # the fused epilogue makes the same two roundings, bit for bit
+        y0 = w.forward(x, out_dtype=ydt)
         rq.bias_add(y0, b)
-        if ydt == torch.float32:
-            assert torch.equal(y, y0)
-        else:
-            bound = (torch.abs(y_nb.float()) + torch.abs(y.float()) + torch.abs(y0.float())) * 2.0 ** -7 + 1e-30
-            assert bool(torch.all(torch.abs(y.float() - y0.float()) <= bound))
+        assert torch.equal(y, y0), ydt
 
 
 def test_bias_add_semantics(dev):
@@ -159,8 +154,10 @@ def test_unaligned_activations_lm_head(dev):
 def test_linear_multi_matches_separate_calls(dev, xdt, m):
     # q/k/v (Q4_K 896 / 128 / 128 x 896) with biases, then gate/up: one
     # launch per set, each output identical to its own rq_linear_bias call
+    # and within the gate of the oracle (dequant + f64 matmul + bias)
     print(f"multi m={m} x={xdt}", flush=True)
     k = 896
+    tol = TOL_F32 if xdt == torch.float32 else TOL_BF16
     # bf16 activations beyond two rows: the set may split K over a different
     # number of workgroups than a single weight, so only the summation order
     # differs (within f32 rounding); otherwise the same kernels run
@@ -170,26 +167,49 @@ def test_linear_multi_matches_separate_calls(dev, xdt, m):
         if exact:
             return torch.equal(a, b)
         return norm_err(a.cpu().numpy(), b.cpu().numpy()) <= 1e-5
-    ws = [make(rq.Q4_K, n, k, 700 + i)[0] for i, n in enumerate((896, 128, 128))]
+
+    def oracle_ok(y, wf, xin, b=None):
+        r = oracle.linear_f64(xin.float().cpu().numpy(), wf)
+        if b is not None:
+            r = r + b.float().cpu().numpy().astype(np.float64)
+        return norm_err(y.cpu().numpy(), r) <= tol
+    made = [make(rq.Q4_K, n, k, 700 + i) for i, n in enumerate((896, 128, 128))]
+    ws = [w for w, _ in made]
     x = torch.from_numpy(synth.activations(710 + m, m, k)).to(xdt).to(dev)
     bs = [bias_vec(w.n, 720 + i, torch.float16, dev) for i, w in enumerate(ws)]
     outs = rq.linear_multi(ws, x, biases=bs, out_dtype=torch.float32)
-    for w, b, y in zip(ws, bs, outs):
+    for (w, wf), b, y in zip(made, bs, outs):
         assert same(y, w.forward(x, out_dtype=torch.float32, bias=b))
-    gu = [make(rq.Q4_K, 4864, k, 730 + i)[0] for i in range(2)]
+        assert oracle_ok(y, wf, x, b)
+    # bf16 outputs with biases: the set's epilogue rounds the product, adds
+    # the rounded bias and rounds again, as the set without biases followed
+    # by the broadcast add does (linear_layer.rs:107-118), bit for bit
+    outs16 = rq.linear_multi(ws, x, biases=bs, out_dtype=torch.bfloat16)
+    plain16 = rq.linear_multi(ws, x, out_dtype=torch.bfloat16)
+    for b, y, y0 in zip(bs, outs16, plain16):
+        rq.bias_add(y0, b)
+        assert torch.equal(y, y0)
+    gu_made = [make(rq.Q4_K, 4864, k, 730 + i) for i in range(2)]
+    gu = [w for w, _ in gu_made]
     outs = rq.linear_multi(gu, x, out_dtype=torch.float32)
-    for w, y in zip(gu, outs):
+    for (w, wf), y in zip(gu_made, outs):
         assert same(y, w.forward(x, out_dtype=torch.float32))
+        assert oracle_ok(y, wf, x)
     assert all(torch.equal(a, b) for a, b in zip(outs, rq.linear_multi(gu, x, out_dtype=torch.float32)))
     # a mixed set (Q4_K, Q4_K, Q6_K as Q4_K_M stores q / k / v) and a set
     # with long rows: grouped by format, each output as its own call
-    mixed = [make(rq.Q4_K, 896, k, 740)[0], make(rq.Q4_K, 128, k, 741)[0], make(rq.Q6_K, 128, k, 742)[0]]
-    for w, y in zip(mixed, rq.linear_multi(mixed, x, biases=[None, bs[1], None], out_dtype=torch.float32)):
-        assert same(y, w.forward(x, out_dtype=torch.float32, bias=bs[1] if w is mixed[1] else None))
-    longs = [make(rq.Q4_K, 896, 4864, 750)[0], make(rq.Q4_K, 300, 4864, 751)[0]]
+    mixed_made = [make(rq.Q4_K, 896, k, 740), make(rq.Q4_K, 128, k, 741), make(rq.Q6_K, 128, k, 742)]
+    mixed = [w for w, _ in mixed_made]
+    mixed_bias = [None, bs[1], None]
+    for (w, wf), b, y in zip(mixed_made, mixed_bias, rq.linear_multi(mixed, x, biases=mixed_bias,
+                                                                     out_dtype=torch.float32)):
+        assert same(y, w.forward(x, out_dtype=torch.float32, bias=b))
+        assert oracle_ok(y, wf, x, b)
+    longs_made = [make(rq.Q4_K, 896, 4864, 750), make(rq.Q4_K, 300, 4864, 751)]
     x2 = torch.from_numpy(synth.activations(752, m, 4864)).to(xdt).to(dev)
-    for w, y in zip(longs, rq.linear_multi(longs, x2, out_dtype=torch.float32)):
+    for (w, wf), y in zip(longs_made, rq.linear_multi([w for w, _ in longs_made], x2, out_dtype=torch.float32)):
         assert same(y, w.forward(x2, out_dtype=torch.float32))
+        assert oracle_ok(y, wf, x2)
 
 
 def test_linear_multi_against_oracle(dev):

@@ -2,9 +2,10 @@
 own weight handle, as the reference's serving loop issues them (requests run
 on a blocking pool, up to four at once: runtime1.rs:23, runtime1.rs:217).
 Every result must equal the same call made alone, bit for bit: the kernels
-are deterministic, the split-K partials are allocated stream-ordered per call,
-and the library keeps no mutable state shared between calls on different
-handles."""
+are deterministic, the split-K partials and tile counters live in the calling
+stream's own workspace (one buffer and counter block per device and stream,
+held by one call at a time while it enqueues), and the library keeps no
+mutable state shared between calls on different streams."""
 import threading
 
 import pytest

@@ -106,6 +106,21 @@ def test_reference_kats_on_device(dev):
     assert (out[0], out[32], out[64], out[96], out[16]) == (17.0, 48.0, 85.0, 112.0, -62.0)
 
 
+def test_hand_derived_kats_on_device(dev):
+    # the literal Q6_K bit-field and Q8_0 sign vectors, worked out by hand from
+    # dequant_k.rs:87-111 and dequant.rs:40-47, through the device layouts
+    # (208-byte Q6_K records + d array, Q8_0 codes + scale array); two rows
+    # of each so the second row's scale lookup is covered too
+    from tests.test_oracle import F16_HALF, Q6K_FIELDS_BLOCK, Q6K_FIELDS_OUT
+
+    q6 = np.frombuffer(Q6K_FIELDS_BLOCK + Q6K_FIELDS_BLOCK[:208] + F16_HALF, np.uint8)
+    out = rq.QWeight(rq.Q6_K, q6, 2, 256).dequantize().cpu().numpy()
+    assert np.array_equal(out[0], Q6K_FIELDS_OUT) and np.array_equal(out[1], Q6K_FIELDS_OUT * 0.5)
+    q8 = np.frombuffer((F16_HALF + bytes([0x80, 0xFF, 0x81, 0x7F] * 8)) * 2, np.uint8)
+    out = rq.QWeight(rq.Q8_0, q8, 2, 32).dequantize().cpu().numpy()
+    assert np.array_equal(out, np.tile(np.array([-64.0, -0.5, -63.5, 63.5] * 8, np.float32), (2, 1)))
+
+
 def test_weight_info(dev):
     data = synth.q4_k_blocks(1, 4864 * 896 // 256)
     w = rq.QWeight(rq.Q4_K, data, 4864, 896)

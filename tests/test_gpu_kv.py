@@ -103,6 +103,29 @@ def test_empty_and_errors(dev):
     with pytest.raises(rq.RqError) as e:
         rq.check(rq.lib().rq_kv_quantize(None, rq.F32, 1, 1, 1, 7, None, rq._ptr(s), None))
     assert e.value.code == -5
+
+
+def test_empty_shape_under_graph_capture(dev):
+    # the floor scales of an empty chunk come from a kernel, so the call can
+    # be captured; every replay rewrites them (the eager fill between
+    # replays puts other values there first)
+    s8 = torch.empty(5, device=dev)
+    s16 = torch.empty(5, device=dev)
+    stream = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            h = torch.cuda.current_stream().cuda_stream
+            rq.check(rq.lib().rq_kv_quantize(None, rq.F32, 1, 5, 0, rq.KV_INT8, None, rq._ptr(s8), h))
+            rq.check(rq.lib().rq_kv_quantize(None, rq.BF16, 0, 5, 64, rq.KV_F16, None, rq._ptr(s16), h))
+    for rep in range(3):
+        s8.fill_(3.0 + rep)
+        s16.fill_(-1.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert s8.cpu().tolist() == [np.float32(1e-8)] * 5, rep
+        assert s16.cpu().tolist() == [1.0] * 5, rep
     with pytest.raises(rq.RqError) as e:
         rq.check(rq.lib().rq_kv_dequantize(None, rq.KV_FP8, None, 1, 1, 4, None, rq.F32, None))
     assert e.value.code == -5

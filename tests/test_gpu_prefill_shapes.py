@@ -13,7 +13,11 @@ prefill chunks).  Each shape runs the tile route rq_linear picks for it:
 Reference: runtimed-gguf dequant + dense matmul (linear_layer.rs:88-104),
 evaluated by the oracle in f64 on the bit-exact dequantized rows of the
 sampled output columns.  Column samples cover every output tile of the
-route.  Gate: normalized error <= 2e-2 (bf16 operands)."""
+route.  Gate: normalized error <= 2e-2 (bf16 operands).
+
+The same shapes also run with f32 activations and f32 outputs, the
+reference's compute type (store.rs:3-4: "Compute always runs in F32"), which
+rq_linear takes on its f32 route; gate 1e-3 (f32 accumulation)."""
 import numpy as np
 import pytest
 import torch
@@ -25,6 +29,7 @@ from tests.conftest import norm_err
 pytestmark = pytest.mark.gpu
 
 TOL_BF16 = 2e-2
+TOL_F32 = 1e-3
 M = 512
 
 SHAPES = [
@@ -66,14 +71,16 @@ def test_prefill_m512_real_shape(dev, name, qtype, n, k):
     print(f"prefill m={M} {name} qtype={qtype} n={n} k={k}", flush=True)
     data = synth.weight_blocks(qtype, 900 + n + k, n, k)
     w = rq.QWeight(qtype, data, n, k)
-    xb = torch.from_numpy(synth.activations(910 + n, M, k)).to(torch.bfloat16)
+    x32 = torch.from_numpy(synth.activations(910 + n, M, k))
+    xb = x32.to(torch.bfloat16)
     if n <= 2048:
         cols = np.arange(n)
     elif n <= 8192:
         cols = sample_columns(n, 128, 16, n)
     else:
         cols = sample_columns(n, 256, 2, n)
-    r = oracle.linear_f64(xb.float().numpy(), rows_f32(qtype, data, k, cols))
+    wrows = rows_f32(qtype, data, k, cols)
+    r = oracle.linear_f64(xb.float().numpy(), wrows)
     xd = xb.to(dev)
     for ydt in (torch.bfloat16, torch.float32):
         y = w.forward(xd, out_dtype=ydt)
@@ -83,4 +90,12 @@ def test_prefill_m512_real_shape(dev, name, qtype, n, k):
         print(f"  {name} y={ydt} normalized error {err:.2e} on {len(cols)} columns", flush=True)
         assert err <= TOL_BF16, (name, ydt, err)
         del y
+    del xd
+    r32 = oracle.linear_f64(x32.numpy(), wrows)
+    y = w.forward(x32.to(dev), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    err = norm_err(y[:, torch.from_numpy(cols).to(dev)].cpu().numpy(), r32)
+    print(f"  {name} x=f32 y=f32 normalized error {err:.2e} on {len(cols)} columns", flush=True)
+    assert err <= TOL_F32, (name, "f32", err)
+    del y
     w.close()

@@ -202,6 +202,72 @@ def test_q5_0_single_high_bits_hand_derived():
     assert np.array_equal(out, np.array([15.0, 0.0] * 8 + [0.0, 15.0] * 8, np.float32))
 
 
+# The reference's Q6_K KAT (dequant_k.rs:155-177) sets only qh[0] = 0xFF and
+# ql[0] = 0x11 in half 0, so it cannot tell which 2-bit qh field feeds which
+# of a position's four outputs, which ql nibble feeds y[l] and which y[l+64],
+# or where the second half's ql / qh / scales start.  Here every field is
+# distinct.  Per half h and position l < 32 (dequant_k.rs:87-111):
+#   y[l]      = d sc[2 0 + l/16] ((ql[l] & F)      | (qh[l] & 3) << 4        - 32)
+#   y[l + 32] = d sc[2 1 + l/16] ((ql[l + 32] & F) | ((qh[l] >> 2) & 3) << 4 - 32)
+#   y[l + 64] = d sc[2 2 + l/16] ((ql[l] >> 4)     | ((qh[l] >> 4) & 3) << 4 - 32)
+#   y[l + 96] = d sc[2 3 + l/16] ((ql[l + 32] >> 4)| ((qh[l] >> 6) & 3) << 4 - 32)
+# with ql, qh, sc offset by 64, 32, 8 bytes in half 1.  Block: d = 1;
+# ql = 0x21 x32, 0x43 x32, 0x65 x32, 0x87 x32; qh = 0xE4 x32 (fields 0, 1, 2, 3
+# from the low bits up), 0x1B x32 (fields 3, 2, 1, 0); scales 1, -2, 3, -4, ...
+# Half 0 codes: 1 | 0 = 1 -> -31; 3 | 16 = 19 -> -13; 2 | 32 = 34 -> 2;
+# 4 | 48 = 52 -> 20.  Half 1: 5 | 48 = 53 -> 21; 7 | 32 = 39 -> 7;
+# 6 | 16 = 22 -> -10; 8 | 0 = 8 -> -24.  Each code times its two scales
+# (l < 16, l >= 16) gives the 16 runs of 16 equal elements below.
+Q6K_FIELDS_BLOCK = (bytes([0x21] * 32 + [0x43] * 32 + [0x65] * 32 + [0x87] * 32) + bytes([0xE4] * 32 + [0x1B] * 32)
+                    + bytes((s if s > 0 else 256 + s) for s in (1, -2, 3, -4, 5, -6, 7, -8, 9, -10, 11, -12, 13, -14,
+                                                                 15, -16)) + F16_ONE)
+Q6K_FIELDS_OUT = np.repeat(np.array([-31, 62, -39, 52, 10, -12, 140, -160,
+                                     189, -210, 77, -84, -130, 140, -360, 384], np.float32), 16)
+
+
+def test_q6_k_bit_fields_hand_derived():
+    assert len(Q6K_FIELDS_BLOCK) == 210
+    out = oracle.dequant_block("q6_k", Q6K_FIELDS_BLOCK)
+    assert np.array_equal(out, Q6K_FIELDS_OUT)
+    # d = 0.5 halves every element (exact: the products are small integers)
+    half = Q6K_FIELDS_BLOCK[:208] + F16_HALF
+    assert np.array_equal(oracle.dequant_block("q6_k", half), Q6K_FIELDS_OUT * 0.5)
+
+
+def test_q6_k_bit_fields_catch_plausible_mistakes():
+    # decoders with one plausible slip each, written here only to show that
+    # the vector above tells them apart from the reference layout
+    def decode(block, swap_qh=False, swap_nibbles=False, same_half=False):
+        ql, qh, sc = block[0:128], block[128:192], np.frombuffer(block[192:208], np.int8)
+        out = np.zeros(256, np.float32)
+        for h in range(2):
+            o = 0 if same_half else h
+            for l in range(32):
+                a, b, hb = ql[64 * o + l], ql[64 * o + l + 32], qh[32 * o + l]
+                lo_a, hi_a = (a >> 4, a & 15) if swap_nibbles else (a & 15, a >> 4)
+                lo_b, hi_b = (b >> 4, b & 15) if swap_nibbles else (b & 15, b >> 4)
+                f = [(hb >> s) & 3 for s in (0, 2, 4, 6)]
+                if swap_qh:
+                    f[1], f[2] = f[2], f[1]
+                q = [lo_a | f[0] << 4, lo_b | f[1] << 4, hi_a | f[2] << 4, hi_b | f[3] << 4]
+                for j in range(4):
+                    out[128 * h + l + 32 * j] = float(sc[8 * h + l // 16 + 2 * j]) * (q[j] - 32)
+        return out
+
+    assert np.array_equal(decode(Q6K_FIELDS_BLOCK), Q6K_FIELDS_OUT)
+    for slip in ({"swap_qh": True}, {"swap_nibbles": True}, {"same_half": True}):
+        assert not np.array_equal(decode(Q6K_FIELDS_BLOCK, **slip), Q6K_FIELDS_OUT), slip
+
+
+def test_q8_0_signed_codes_hand_derived():
+    # d = 0.5; codes 0x80, 0xFF, 0x81, 0x7F are -128, -1, -127, 127 as i8
+    # (dequant.rs:40-47): -64, -0.5, -63.5, 63.5.  Unsigned codes would give
+    # 64, 127.5, 64.5, 63.5.
+    block = F16_HALF + bytes([0x80, 0xFF, 0x81, 0x7F] * 8)
+    out = oracle.dequant_block("q8_0", block)
+    assert np.array_equal(out, np.array([-64.0, -0.5, -63.5, 63.5] * 8, np.float32))
+
+
 # ------------------------------------- independent restatements ----------
 
 @pytest.mark.parametrize("qtype", [8, 2, 6, 12, 13, 14])
