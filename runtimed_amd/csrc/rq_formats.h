@@ -38,6 +38,15 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((fmt_f32x2){lo, hi}, fmt_bf16x2));
 }
 
+// Two f32 values as two bf16 limbs each: hi = v rounded to bf16, lo =
+// (v - hi) rounded to bf16 (v - hi is exact in f32), packed in pairs as
+// pk_bf16 packs them.  hi + lo is v to within 2^-17 |v|, so products of
+// limbs carry 16 significant bits of each operand.
+__device__ __forceinline__ void limbs2(float a, float b, uint32_t &hi, uint32_t &lo) {
+  hi = pk_bf16(a, b);
+  lo = pk_bf16(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xFFFF0000u));
+}
+
 // Load `len` (multiple of 4) activations starting at x[idx] into f32 registers.
 template <int LEN>
 __device__ __forceinline__ void load_run(const void *x, int xtype, int64_t idx, float *dst) {

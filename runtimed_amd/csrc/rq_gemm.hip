@@ -50,19 +50,34 @@ constexpr int BK = 64, LDS_K = BK + 8;
 // meet in LDS at the end (added in group order) and group 0 stores.  More
 // waves per tile then keep more loads in flight where a tile's K loop is
 // latency-bound (the 2048-wide layers at M = 512: 256 tiles of 64 x 64).
-template <class F, int BM, int BN, int WM, int WN, int D, int KG = 1>
+//
+// XT is the activation type: RQ_BF16 as above, or RQ_F32 / RQ_F16 (the
+// reference computes in f32, store.rs:3-4), which run on the same bf16
+// matrix cores as two bf16 limbs per operand: the activations split as they
+// go to LDS, the weights decoded to their exact f32 values (the reference's
+// dequantized weights) and split the same way, and each product taken as
+// hi*hi + hi*lo + lo*hi (three MFMAs, f32 accumulation).  The dropped lo*lo
+// term and the limbs' own rounding leave about 2^-16 of each product, far
+// inside the 1e-3 gate of f32 paths; LDS holds a hi and a lo tile of each
+// operand.
+template <class F, int BM, int BN, int WM, int WN, int D, int KG = 1, int XT = RQ_BF16>
 __global__ __launch_bounds__(64 * WM * WN * KG) void k_qgemm(const uint8_t *__restrict__ w,
                                                             const uint8_t *__restrict__ aux,
-                                                            const uint16_t *__restrict__ x, int64_t m,
+                                                            const void *__restrict__ xv, int64_t m,
                                                             int64_t n, int64_t k, const Out o, int64_t steps,
                                                             float *__restrict__ part) {
+  constexpr bool LIMBS = XT != RQ_BF16;
+  constexpr int NL = LIMBS ? 2 : 1;           // LDS tiles of each operand (hi, lo)
+  constexpr int XB = XT == RQ_F32 ? 4 : 2;    // bytes of an activation in memory
+  constexpr int EPL = 16 / XB;                // activations per 16-byte load
+  constexpr int LPR = BK / EPL;               // loads per activation row and step
   constexpr int NT = 64 * WM * WN;  // threads of a K-group
   static_assert(BN * 2 == NT, "one weight piece per thread");
   constexpr int MI = BM / WM / 32, NI = BN / WN / 32;
-  constexpr int A_LOADS = BM * BK / 8 / NT;  // 16-byte loads per thread per step
-  constexpr int A_ROWS = NT / 8;              // activation rows covered by one load round
+  constexpr int A_LOADS = BM * LPR / NT;      // 16-byte loads per thread per step
+  constexpr int A_ROWS = NT / LPR;            // activation rows covered by one load round
   constexpr int A_BYTES = BM * LDS_K * 2, B_BYTES = BN * LDS_K * 2;
-  constexpr int G_BYTES = 2 * (A_BYTES + B_BYTES);  // a group's double-buffered tiles
+  constexpr int G_BYTES = 2 * NL * (A_BYTES + B_BYTES);  // a group's double-buffered tiles
   static_assert(KG == 1 || BM * BN * 4 <= G_BYTES, "the partial tile of a group fits its buffers");
   __shared__ __attribute__((aligned(16))) uint8_t SM[KG * G_BYTES];
 
@@ -71,21 +86,24 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void k_qgemm(const uint8_t *__re
   const int wm = wave / WN, wn = wave % WN;
   const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
   uint8_t *const G = SM + grp * G_BYTES;
-  auto As = [&](int buf) { return reinterpret_cast<uint16_t *>(G + buf * A_BYTES); };
-  auto Bs = [&](int buf) { return reinterpret_cast<uint16_t *>(G + 2 * A_BYTES + buf * B_BYTES); };
+  // tile l (0 = hi, 1 = lo) of buffer buf
+  auto As = [&](int buf, int l = 0) { return reinterpret_cast<uint16_t *>(G + (NL * buf + l) * A_BYTES); };
+  auto Bs = [&](int buf, int l = 0) {
+    return reinterpret_cast<uint16_t *>(G + 2 * NL * A_BYTES + (NL * buf + l) * B_BYTES);
+  };
 
   // Weight piece of this thread: row n0 + (tid >> 1), half h = tid & 1;
-  // activation slots: row (tid >> 3) + A_ROWS * i, 8 bf16 at column
-  // 8 * (tid & 7).  Rows past n or m re-read the last row (unconditional
+  // activation slots: row tid / LPR + A_ROWS * i, EPL activations at column
+  // EPL * (tid % LPR).  Rows past n or m re-read the last row (unconditional
   // loads); their products land in outputs that are never stored.
   const int brow = tid >> 1, bh = tid & 1;
   const int64_t gn = n0 + brow < n ? n0 + brow : n - 1;
-  const int arow = tid >> 3, acol = 8 * (tid & 7);
-  const uint16_t *xa[A_LOADS];
+  const int arow = tid / LPR, acol = EPL * (tid % LPR);
+  const uint8_t *xa[A_LOADS];
 #pragma unroll
   for (int i = 0; i < A_LOADS; ++i) {
     const int64_t gm = m0 + arow + A_ROWS * i;
-    xa[i] = x + (gm < m ? gm : m - 1) * k + acol;
+    xa[i] = static_cast<const uint8_t *>(xv) + ((gm < m ? gm : m - 1) * k + acol) * XB;
   }
 
   // Loads run D K-steps ahead in D register slots (LLVM vector types: a
@@ -98,22 +116,58 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void k_qgemm(const uint8_t *__re
   auto gload = [&](int slot, int64_t s) {  // local step s, clamped to the group's steps
     const int64_t kt = kt0 + (s < nk ? s : nk - 1);
 #pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) ra[slot][i] = *reinterpret_cast<const u32x4 *>(xa[i] + kt * BK);
+    for (int i = 0; i < A_LOADS; ++i) ra[slot][i] = *reinterpret_cast<const u32x4 *>(xa[i] + kt * BK * XB);
     pb[slot] = F::load(w, aux, gn, k, (int)(2 * kt + bh));
   };
-  auto sstore = [&](int slot, int buf) {
-    uint16_t *A = As(buf), *B = Bs(buf);
-#pragma unroll
-    for (int i = 0; i < A_LOADS; ++i)
-      *reinterpret_cast<u32x4 *>(&A[(arow + A_ROWS * i) * LDS_K + acol]) = ra[slot][i];
-    uint32_t ob[16];
-    F::decode_bf16(pb[slot], ob);
+  // The 16 weights of run r, pairs q (8 weights each) of limb l to the LDS tile.
+  auto store_b = [&](uint16_t *B, const uint32_t (&ob)[16]) {
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       u32x4 *dst = reinterpret_cast<u32x4 *>(&B[brow * LDS_K + 16 * bh + 32 * r]);
 #pragma unroll
       for (int q = 0; q < 2; ++q)
         dst[q] = (u32x4){ob[8 * r + 4 * q], ob[8 * r + 4 * q + 1], ob[8 * r + 4 * q + 2], ob[8 * r + 4 * q + 3]};
+    }
+  };
+  auto sstore = [&](int slot, int buf) {
+    if constexpr (!LIMBS) {
+      uint16_t *A = As(buf);
+#pragma unroll
+      for (int i = 0; i < A_LOADS; ++i)
+        *reinterpret_cast<u32x4 *>(&A[(arow + A_ROWS * i) * LDS_K + acol]) = ra[slot][i];
+      uint32_t ob[16];
+      F::decode_bf16(pb[slot], ob);
+      store_b(Bs(buf), ob);
+    } else {
+      uint16_t *Ah = As(buf, 0), *Al = As(buf, 1);
+#pragma unroll
+      for (int i = 0; i < A_LOADS; ++i) {
+        const u32x4 v = ra[slot][i];
+        const int off = (arow + A_ROWS * i) * LDS_K + acol;
+        if constexpr (XT == RQ_F32) {  // 4 activations: 8 bytes of each limb
+          uint32_t h0, l0, h1, l1;
+          limbs2(__uint_as_float(v.x), __uint_as_float(v.y), h0, l0);
+          limbs2(__uint_as_float(v.z), __uint_as_float(v.w), h1, l1);
+          *reinterpret_cast<uint2 *>(&Ah[off]) = make_uint2(h0, h1);
+          *reinterpret_cast<uint2 *>(&Al[off]) = make_uint2(l0, l1);
+        } else {  // 8 f16 activations: 16 bytes of each limb
+          const _Float16 *hv = reinterpret_cast<const _Float16 *>(&v);
+          uint32_t h[4], l[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) limbs2((float)hv[2 * q], (float)hv[2 * q + 1], h[q], l[q]);
+          *reinterpret_cast<u32x4 *>(&Ah[off]) = (u32x4){h[0], h[1], h[2], h[3]};
+          *reinterpret_cast<u32x4 *>(&Al[off]) = (u32x4){l[0], l[1], l[2], l[3]};
+        }
+      }
+      float wv[2][16];
+      F::decode(pb[slot], wv);
+      uint32_t oh[16], ol[16];
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) limbs2(wv[r][2 * j], wv[r][2 * j + 1], oh[8 * r + j], ol[8 * r + j]);
+      store_b(Bs(buf, 0), oh);
+      store_b(Bs(buf, 1), ol);
     }
   };
 
@@ -124,22 +178,30 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void k_qgemm(const uint8_t *__re
     for (int j = 0; j < NI; ++j) acc[i][j] = (f32x16){0};
 
   auto mfma_step = [&](int buf) {
-    const uint16_t *A = As(buf), *B = Bs(buf);
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       const int kc = ks * 16 + 8 * (lane >> 5);
-      bf16x8 fa[MI], fb[NI];
+      bf16x8 fa[NL][MI], fb[NL][NI];
 #pragma unroll
-      for (int i = 0; i < MI; ++i)
-        fa[i] = *reinterpret_cast<const bf16x8 *>(&A[(wm * (BM / WM) + i * 32 + (lane & 31)) * LDS_K + kc]);
+      for (int l = 0; l < NL; ++l) {
+        const uint16_t *A = As(buf, l), *B = Bs(buf, l);
 #pragma unroll
-      for (int j = 0; j < NI; ++j)
-        fb[j] = *reinterpret_cast<const bf16x8 *>(&B[(wn * (BN / WN) + j * 32 + (lane & 31)) * LDS_K + kc]);
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
+        for (int i = 0; i < MI; ++i)
+          fa[l][i] = *reinterpret_cast<const bf16x8 *>(&A[(wm * (BM / WM) + i * 32 + (lane & 31)) * LDS_K + kc]);
 #pragma unroll
         for (int j = 0; j < NI; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+          fb[l][j] = *reinterpret_cast<const bf16x8 *>(&B[(wn * (BN / WN) + j * 32 + (lane & 31)) * LDS_K + kc]);
+      }
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+          if constexpr (LIMBS) {  // the small cross terms first
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[1][i], fb[0][j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[0][i], fb[1][j], acc[i][j], 0, 0, 0);
+          }
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[0][i], fb[0][j], acc[i][j], 0, 0, 0);
+        }
     }
   };
 
@@ -712,7 +774,7 @@ int splits_for(int64_t tiles, int64_t nk) {
   return sp;
 }
 
-template <class F, int BM, int BN, int WM, int WN, int D = 3, int KG = 1>
+template <class F, int BM, int BN, int WM, int WN, int D = 3, int KG = 1, int XT = RQ_BF16>
 int launch(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease &ws,
            int sp_force = 0) {
   const int64_t nk = wt->k / BK;
@@ -720,7 +782,7 @@ int launch(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStrea
   const int sp = sp_force > 0 ? sp_force : splits_for(gx * gy, nk);
   // K-groups need equal shares of every split's steps.
   if constexpr (KG > 1) {
-    if (nk % ((int64_t)sp * KG) != 0) return launch<F, BM, BN, WM, WN, D, 1>(wt, x, m, o, s, ws, sp);
+    if (nk % ((int64_t)sp * KG) != 0) return launch<F, BM, BN, WM, WN, D, 1, XT>(wt, x, m, o, s, ws, sp);
   }
   const int64_t steps = (nk + sp - 1) / sp;
   const int used = (int)((nk + steps - 1) / steps);  // splits that own at least one step
@@ -731,8 +793,8 @@ int launch(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStrea
     if (!part) return rc;
   }
   const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)used);
-  hipLaunchKernelGGL((k_qgemm<F, BM, BN, WM, WN, D, KG>), grid, dim3(64 * WM * WN * KG), 0, s, wt->data,
-                     wt->data + wt->aux_off, static_cast<const uint16_t *>(x), m, wt->n, wt->k, o, steps, part);
+  hipLaunchKernelGGL((k_qgemm<F, BM, BN, WM, WN, D, KG, XT>), grid, dim3(64 * WM * WN * KG), 0, s, wt->data,
+                     wt->data + wt->aux_off, x, m, wt->n, wt->k, o, steps, part);
   if (part) {
     const int64_t mn = m * wt->n;
     if (wt->n % 4 == 0 && (reinterpret_cast<uintptr_t>(o.y) & 15) == 0 && used <= 8) {
@@ -800,7 +862,45 @@ int by_m(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_
   return launch<F, 128, 128, 2, 2, 1, 2>(wt, x, m, o, s, ws);
 }
 
+// f32 / f16 activations, m > 64: the two-limb tiles (twice the LDS of the
+// bf16 tiles, so one K-group of 128 x 128 or two of 64 x 64).  Tile shapes
+// follow by_m: 64 x 64 where 128 x 128 tiles are too few for the CUs with
+// short K, K split four ways for long K on few tiles.
+template <class F, int XT>
+int by_m_limbs(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease &ws) {
+  const int64_t tiles128 = ((m + 127) / 128) * ((wt->n + 127) / 128), nk = wt->k / BK;
+  if (tiles128 < 128 && nk <= 32) return launch<F, 64, 64, 2, 1, 1, 2, XT>(wt, x, m, o, s, ws);
+  if (tiles128 < 128 && nk >= 64) {
+    const int sp = (int)(nk / 32 < 4 ? nk / 32 : 4);
+    return launch<F, 128, 128, 2, 2, 1, 1, XT>(wt, x, m, o, s, ws, sp);
+  }
+  return launch<F, 128, 128, 2, 2, 1, 1, XT>(wt, x, m, o, s, ws);
+}
+
+template <int XT>
+int limbs_fmt(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease &ws) {
+  switch (wt->qtype) {
+    case RQ_Q4_K: return by_m_limbs<FmtQ4K, XT>(wt, x, m, o, s, ws);
+    case RQ_Q6_K: return by_m_limbs<FmtQ6KG, XT>(wt, x, m, o, s, ws);
+    case RQ_Q8_0: return by_m_limbs<FmtQ8, XT>(wt, x, m, o, s, ws);
+    case RQ_Q5_K: return by_m_limbs<FmtQ5K, XT>(wt, x, m, o, s, ws);
+    case RQ_Q4_0: return by_m_limbs<FmtQx0<false>, XT>(wt, x, m, o, s, ws);
+    case RQ_Q5_0: return by_m_limbs<FmtQx0<true>, XT>(wt, x, m, o, s, ws);
+    default: return RQ_E_UNSUPPORTED;
+  }
+}
+
 }  // namespace
+
+// f32 / f16 activations, m > 64, k % 64 == 0, 16-byte aligned x: the
+// two-limb tiles of k_qgemm.
+int launch_linear_mfma_limbs(const rq_weight *wt, const void *x, int xtype, int64_t m, const Out &o, hipStream_t s,
+                             WsLease &ws) {
+  if (wt->k % 64 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
+  if (xtype == RQ_F32) return limbs_fmt<RQ_F32>(wt, x, m, o, s, ws);
+  if (xtype == RQ_F16) return limbs_fmt<RQ_F16>(wt, x, m, o, s, ws);
+  return RQ_E_UNSUPPORTED;
+}
 
 // bf16 activations, m > 1, k % 64 == 0, 16-byte aligned x.
 int launch_linear_mfma(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease &ws) {

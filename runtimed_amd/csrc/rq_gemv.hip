@@ -836,9 +836,14 @@ int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m
     if (rc != RQ_E_UNSUPPORTED) return rc;
   }
   // More rows (prefill with f32 activations, the reference's compute type):
-  // the same kernel on slices of 64 activation rows (the weights are read
-  // once per slice, mostly from cache), a last slice of 2 or 3 rows on the
-  // VALU kernel and a single row on the GEMV.
+  // the tiled GEMM on two bf16 limbs per operand.
+  if (m > 64 && f32x) {
+    const int rc = launch_linear_mfma_limbs(wt, x, xtype, m, o, s, ws);
+    if (rc != RQ_E_UNSUPPORTED) return rc;
+  }
+  // Otherwise the small-M f32 kernel on slices of 64 activation rows (the
+  // weights are read once per slice, mostly from cache), a last slice of 2
+  // or 3 rows on the VALU kernel and a single row on the GEMV.
   if (m > 64 && f32x && wt->k % 64 == 0) {
     const size_t xb = xtype == RQ_F32 ? 4 : 2, yb = o.ytype == RQ_F32 ? 4 : 2;
     // The whole slices in one launch (side by side, the weight tiles shared

@@ -255,6 +255,10 @@ int launch_linear_multi(const rq_weight *const *w, int count, const void *x, int
 // MFMA GEMM for bf16 activations and m > 1 (RQ_E_UNSUPPORTED if the shape or
 // format has no tiled kernel).
 int launch_linear_mfma(const rq_weight *w, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease &ws);
+// f32 / f16 activations, m > 64 (k % 64 == 0, x 16-byte aligned): the same
+// tiles on two bf16 limbs per operand (exact weights, f32-accurate sums).
+int launch_linear_mfma_limbs(const rq_weight *w, const void *x, int xtype, int64_t m, const Out &o, hipStream_t s,
+                             WsLease &ws);
 // Matrix-core kernel for bf16 activations and 2 <= m <= 64 (speculative
 // verify), RQ_E_UNSUPPORTED outside that or for formats it has no decoder for.
 // With a workspace (ws not null), few row tiles split K over several

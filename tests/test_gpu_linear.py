@@ -219,10 +219,10 @@ def test_small_m_f32_activations(dev, qtype, m, n, k):
     assert norm_err(y, ref(x.numpy(), wf)) <= TOL_F32
 
 
-# More than 64 f32 rows run as slices of 64 side by side in one launch, with
-# the rest (a last slice of 1..3 rows on the VALU kernel or the GEMV) after
-# it; (512, 1000, 1024) splits K two ways over eight slices (tile counters
-# and partials per slice), (300, 2048, 640) runs four slices unsplit.
+# More than 64 f32 rows run on the tiled GEMM with two bf16 limbs per
+# operand (exact weights split into hi + lo, f32 accumulation): tiles past
+# m and n, rows straddling Q4_K blocks (k = 896), k not a multiple of 128
+# (640), and 64 x 64 / 128 x 128 tiles all occur here.
 @pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0, rq.Q5_0])
 @pytest.mark.parametrize("m,n,k", [(200, 300, 512), (129, 130, 256), (66, 64, 2048), (131, 96, 896),
                                    (512, 1000, 1024), (300, 2048, 640)])
