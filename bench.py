@@ -777,6 +777,8 @@ def main():
                                                                multi=True)),
                          ("verify_f32", lambda: extra_verify(torch, rq, W, dev, args.steps, args.warmup,
                                                              torch.float32, (2, 4, 16, 64))),
+                         ("verify_f32_multi", lambda: extra_verify(torch, rq, W, dev, args.steps, args.warmup,
+                                                                   torch.float32, (4, 16, 64), multi=True)),
                          ("prefill_f32", lambda: extra_prefill(torch, rq, synth, dev, args.steps, args.warmup,
                                                                f32=True)),
                          ("prefill", lambda: extra_prefill(torch, rq, synth, dev, args.steps, args.warmup)),

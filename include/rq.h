@@ -213,12 +213,13 @@ int rq_linear_bias(const rq_weight *w, const void *x, int xtype, int64_t m, int6
  * otherwise).  At m = 1 and 2, runs of up to 4 consecutive weights of one
  * format whose rows hold at most 64 pieces (k <= 2048 for Q4_K / Q5_K /
  * Q8_0 / Q4_0 / Q5_0, k <= 4096 for Q6_K) take one launch, and so do bf16 activations
- * with 3 <= m <= 64 (the small-M matrix-core kernel); other weights
+ * with 3 <= m <= 64 and f32 activations with 4 <= m <= 64 (the small-M
+ * matrix-core kernel; f32 on two bf16 limbs per operand); other weights
  * take the launches rq_linear_bias would make.  At m <= 2 each output equals
- * that call's output bit for bit; with bf16 activations and 3 <= m <= 64
- * the set may split K over a different number of workgroups than a single
- * weight would, so sums can differ in their last bits (every result is
- * deterministic: the same call gives the same bits). */
+ * that call's output bit for bit; in the small-M sets the K split (and, for
+ * f32, the kernel) can differ from a single weight's, so sums can differ in
+ * their last bits (every result is deterministic: the same call gives the
+ * same bits). */
 int rq_linear_multi(int count, const rq_weight *const *ws, const void *x, int xtype, int64_t m, int64_t k,
                     const void *const *biases, int btype, void *const *ys, int ytype, void *stream);
 

@@ -905,10 +905,12 @@ int launch_linear_multi(const rq_weight *const *w, int count, const void *x, int
   const int64_t k = w[0]->k;
   for (int j = 1; j < count; ++j)
     if (w[j]->qtype != qt || w[j]->k != k) return RQ_E_UNSUPPORTED;
-  // bf16 activations beyond two rows: the small-M matrix-core kernel, as
-  // rq_linear takes them (two rows stay on the segment kernel below, or go
-  // one by one where rq_linear gives them other layouts).
-  if (xtype == RQ_BF16 && m >= 3 && m <= 64) return launch_linear_smallm_set(w, count, x, m, o, s, &ws);
+  // bf16 activations beyond two rows, f32 ones from four: the small-M
+  // matrix-core kernel (bf16, or two bf16 limbs for f32), as rq_linear takes
+  // them (two rows stay on the segment kernel below, f32 three rows one by
+  // one where rq_linear gives them other layouts).
+  if (xtype == RQ_BF16 && m >= 3 && m <= 64) return launch_linear_smallm_set(w, count, x, xtype, m, o, s, &ws);
+  if (xtype == RQ_F32 && m >= 4 && m <= 64) return launch_linear_smallm_set(w, count, x, xtype, m, o, s, &ws);
   if (m != 1 && m != 2) return RQ_E_UNSUPPORTED;
   switch (qt) {
     case RQ_Q4_K: return k % 64 ? RQ_E_UNSUPPORTED : run_seg_set<FmtQ4K>(w, count, x, xtype, m, o, s);

@@ -264,9 +264,10 @@ int launch_linear_mfma_limbs(const rq_weight *w, const void *x, int xtype, int64
 // With a workspace (ws not null), few row tiles split K over several
 // workgroups (partials and counters in the workspace).
 int launch_linear_smallm(const rq_weight *w, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease *ws);
-// The same kernel on a set of weights sharing x (equal k).
-int launch_linear_smallm_set(const rq_weight *const *w, int count, const void *x, int64_t m, const Out *o,
-                             hipStream_t s, WsLease *ws);
+// The same kernel on a set of weights sharing x (equal k); xtype RQ_BF16,
+// or RQ_F32 on the two-limb variant.
+int launch_linear_smallm_set(const rq_weight *const *w, int count, const void *x, int xtype, int64_t m,
+                             const Out *o, hipStream_t s, WsLease *ws);
 // The same for f32 / f16 activations on the f32 matrix cores with exact f32
 // weights (f32 accumulation).
 int launch_linear_smallm_f32(const rq_weight *wt, const void *x, int xtype, int64_t m, const Out &o,

@@ -400,14 +400,40 @@ __device__ __forceinline__ void xs_store(uint8_t *xs, const u32x4 (&v)[XR], cons
   }
 }
 
-// The rest of the copy after its first round (loaded by the caller ahead of
-// other loads), then the workgroup barrier.
+// The same pieces of f32 activations (4 a piece) split into bf16 limbs on
+// their way to LDS: the hi limbs where a bf16 copy would put them (row
+// stride xstr), the lo limbs lo_off bytes further.
 template <int NT, int XR>
-__device__ __forceinline__ void xs_finish(uint8_t *xs, u32x4 (&v)[XR], const XStage &st) {
-  xs_store<NT, XR>(xs, v, st, 0);
+__device__ __forceinline__ void xs_store_limbs(uint8_t *xs, const u32x4 (&v)[XR], const XStage &st, int base,
+                                               int lo_off) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
+  typedef __attribute__((address_space(3))) uint8_t lds_u8;
+#pragma unroll
+  for (int i = 0; i < XR; ++i) {
+    int r, c;
+    st.at(base + i * NT + (int)threadIdx.x, r, c);
+    uint32_t h0, l0, h1, l1;
+    limbs2(__uint_as_float(v[i].x), __uint_as_float(v[i].y), h0, l0);
+    limbs2(__uint_as_float(v[i].z), __uint_as_float(v[i].w), h1, l1);
+    uint8_t *d = xs + r * st.xstr + 8 * c;
+    *reinterpret_cast<lds_u32x2 *>((lds_u8 *)d) = (u32x2){h0, h1};
+    *reinterpret_cast<lds_u32x2 *>((lds_u8 *)(d + lo_off)) = (u32x2){l0, l1};
+  }
+}
+
+// The rest of the copy after its first round (loaded by the caller ahead of
+// other loads), then the workgroup barrier.  XT = RQ_F32: the limb copy.
+template <int NT, int XR, int XT = RQ_BF16>
+__device__ __forceinline__ void xs_finish(uint8_t *xs, u32x4 (&v)[XR], const XStage &st, int lo_off = 0) {
+  auto put = [&](int base) {
+    if constexpr (XT == RQ_BF16) xs_store<NT, XR>(xs, v, st, base);
+    else xs_store_limbs<NT, XR>(xs, v, st, base, lo_off);
+  };
+  put(0);
   for (int base = XR * NT; base < st.total; base += XR * NT) {
     xs_load<NT, XR>(v, st, base);
-    xs_store<NT, XR>(xs, v, st, base);
+    put(base);
   }
   __syncthreads();
 }
@@ -469,6 +495,108 @@ __device__ __forceinline__ void mma_chunk(const typename C::Chunk &c, const XFra
   for (int ct = 0; ct < MT; ++ct)
     acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f1, pick(xf.a[ct].z, xf.a[ct].w, xf.b[ct].z, xf.b[ct].w),
                                                       acc[ct], 0, 0, 0);
+}
+
+// ---- f32 activations as two bf16 limbs -----------------------------------
+//
+// The limb variant (XT = RQ_F32): activations split into hi + lo bf16 limbs
+// (limbs2), weights decoded to their exact f32 values (the reference's
+// dequantized weights) and split the same way, each product taken as
+// lo*hi + hi*lo + hi*hi on the bf16 matrix cores (three MFMAs, f32 sums; the
+// dropped lo*lo term and the limbs' rounding leave about 2^-16 of each
+// product).  XFragL holds the hi and lo limbs at XFrag's positions; XRaw
+// the 16 f32 activations of a fragment as loaded from global memory (four
+// 16-byte pieces), split when used.
+template <int MT>
+struct XFragL {
+  u32x4 a[MT], b[MT], al[MT], bl[MT];
+};
+template <int MT>
+struct XRaw {
+  u32x4 v[MT][4];
+};
+
+// xr: byte address of element 8g of chunk 0 in each column tile's row.
+template <int MT>
+__device__ __forceinline__ void load_xraw(XRaw<MT> &f, const uint8_t *const (&xr)[MT], int64_t t) {
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) {
+    const uint8_t *p = xr[ct] + 256 * t;
+    f.v[ct][0] = *reinterpret_cast<const u32x4 *>(p);
+    f.v[ct][1] = *reinterpret_cast<const u32x4 *>(p + 16);
+    f.v[ct][2] = *reinterpret_cast<const u32x4 *>(p + 128);
+    f.v[ct][3] = *reinterpret_cast<const u32x4 *>(p + 144);
+  }
+}
+
+// Eight f32 activations (two 16-byte pieces) as hi / lo bf16 pairs in
+// element order.
+__device__ __forceinline__ void split8_f32(const u32x4 &a, const u32x4 &b, u32x4 &h, u32x4 &l) {
+  uint32_t hh[4], ll[4];
+  limbs2(__uint_as_float(a.x), __uint_as_float(a.y), hh[0], ll[0]);
+  limbs2(__uint_as_float(a.z), __uint_as_float(a.w), hh[1], ll[1]);
+  limbs2(__uint_as_float(b.x), __uint_as_float(b.y), hh[2], ll[2]);
+  limbs2(__uint_as_float(b.z), __uint_as_float(b.w), hh[3], ll[3]);
+  h = (u32x4){hh[0], hh[1], hh[2], hh[3]};
+  l = (u32x4){ll[0], ll[1], ll[2], ll[3]};
+}
+
+template <int MT>
+__device__ __forceinline__ void split_raw(const XRaw<MT> &r, XFragL<MT> &f) {
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) {
+    split8_f32(r.v[ct][0], r.v[ct][1], f.a[ct], f.al[ct]);
+    split8_f32(r.v[ct][2], r.v[ct][3], f.b[ct], f.bl[ct]);
+  }
+}
+
+// Limb fragments of chunk tl of the LDS slice: hi limbs where lds_x reads,
+// lo limbs lo_off bytes further.
+template <int MT>
+__device__ __forceinline__ void lds_xl(XFragL<MT> &f, const XSlice &xs, int64_t tl, int lo_off) {
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) {
+    const uint8_t *p = xs.row[ct] + 128 * tl;
+    f.a[ct] = ds_read16(p);
+    f.b[ct] = ds_read16(p + 64);
+    f.al[ct] = ds_read16(p + lo_off);
+    f.bl[ct] = ds_read16(p + lo_off + 64);
+  }
+}
+
+// mma_chunk on limbs: the chunk's exact weights split into hi / lo pairs
+// (same order as decode_chunk's pairs), three MFMAs per column tile and
+// quarter, the small cross terms first.
+template <class C, int MT>
+__device__ __forceinline__ void mma_chunk_limbs(const typename C::Chunk &c, const XFragL<MT> &xf, f32x4 (&acc)[MT],
+                                                int g, uint32_t vm) {
+  float f[16];
+  decode_chunk_f32<C>(c, f, g);
+  uint32_t oh[8], ol[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    limbs2(f[2 * i], f[2 * i + 1], oh[i], ol[i]);
+    oh[i] &= vm;
+    ol[i] &= vm;
+  }
+  const bf16x8 h0 = pick(oh[0], oh[1], oh[4], oh[5]), h1 = pick(oh[2], oh[3], oh[6], oh[7]);
+  const bf16x8 l0 = pick(ol[0], ol[1], ol[4], ol[5]), l1 = pick(ol[2], ol[3], ol[6], ol[7]);
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) {
+    const bf16x8 xh = pick(xf.a[ct].x, xf.a[ct].y, xf.b[ct].x, xf.b[ct].y);
+    const bf16x8 xl = pick(xf.al[ct].x, xf.al[ct].y, xf.bl[ct].x, xf.bl[ct].y);
+    acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l0, xh, acc[ct], 0, 0, 0);
+    acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h0, xl, acc[ct], 0, 0, 0);
+    acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h0, xh, acc[ct], 0, 0, 0);
+  }
+#pragma unroll
+  for (int ct = 0; ct < MT; ++ct) {
+    const bf16x8 xh = pick(xf.a[ct].z, xf.a[ct].w, xf.b[ct].z, xf.b[ct].w);
+    const bf16x8 xl = pick(xf.al[ct].z, xf.al[ct].w, xf.bl[ct].z, xf.bl[ct].w);
+    acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(l1, xh, acc[ct], 0, 0, 0);
+    acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h1, xl, acc[ct], 0, 0, 0);
+    acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h1, xh, acc[ct], 0, 0, 0);
+  }
 }
 
 // Lane slot l of the (row tile rt, column tile ct) output tile: activation
@@ -594,9 +722,12 @@ __device__ __forceinline__ void reduce_split(f32x4 (&part)[NW][1][MT][64], const
 // past the end load a valid chunk again and are masked; so does a wave with
 // no chunk in the slice when x is in LDS (it still joins the copy and the
 // barrier); without LDS such a wave skips the work.
-template <class C, int MT, int NW, int B, int RT, bool XL>
+// XT: the activation type, RQ_BF16 or (the limb variant) RQ_F32;
+// with XL and limbs the LDS slice holds the hi limbs at row stride xstr and
+// the lo limbs m * xstr bytes further.
+template <class C, int MT, int NW, int B, int RT, bool XL, int XT = RQ_BF16>
 __device__ __forceinline__ void smallm_tiles(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
-                                             const uint16_t *__restrict__ x, int64_t m, const Out &o, int64_t n,
+                                             const void *__restrict__ xv, int64_t m, const Out &o, int64_t n,
                                              int64_t k, int64_t tile, int S, int s, f32x4 *__restrict__ wsp,
                                              uint32_t *__restrict__ cnt, f32x4 (&part)[NW][RT][MT][64],
                                              uint8_t *xs, int xstr) {
@@ -610,7 +741,17 @@ __device__ __forceinline__ void smallm_tiles(const uint8_t *__restrict__ w, cons
     row[rt] = r < n ? r : n - 1;
   }
   constexpr bool HALF = C::CE == 128;
-  typedef typename std::conditional<HALF, XFragH<MT>, XFrag<MT>>::type XF;
+  constexpr bool LIMBS = XT != RQ_BF16;
+  static_assert(XT == RQ_BF16 || XT == RQ_F32, "bf16 activations, or f32 ones on limbs");
+  static_assert(!(HALF && LIMBS), "limbs take 64-element chunks");
+  constexpr int XB = LIMBS ? 4 : 2;  // bytes of an activation in memory
+  // fragments as loaded in a batch: bf16 (XFrag / XFragH), raw f32 (XRaw,
+  // limbs from global memory) or limbs read from LDS (XFragL)
+  typedef typename std::conditional<
+      LIMBS, typename std::conditional<XL, XFragL<MT>, XRaw<MT>>::type,
+      typename std::conditional<HALF, XFragH<MT>, XFrag<MT>>::type>::type XF;
+  const uint16_t *x = static_cast<const uint16_t *>(xv);
+  const int lo_off = LIMBS ? (int)m * xstr : 0;
   const int64_t nk = k / C::CE, cps = (nk + S - 1) / S;
   const int64_t lo = s * cps, hi = lo + cps < nk ? lo + cps : nk;
 
@@ -624,11 +765,13 @@ __device__ __forceinline__ void smallm_tiles(const uint8_t *__restrict__ w, cons
   // m - 1; their results are not stored), at its lane group's offset.
   const int xo = HALF ? 64 * (g >> 1) + 16 * (g & 1) : 8 * g;  // elements
   const uint16_t *xr[MT];
+  const uint8_t *xrb[MT];  // the same rows as byte addresses (raw f32 / f16 activations)
   XSlice xsl;
 #pragma unroll
   for (int ct = 0; ct < MT; ++ct) {
     const int64_t mr = 16 * ct + (lane & 15) < m ? 16 * ct + (lane & 15) : m - 1;
     xr[ct] = x + mr * k + xo;
+    xrb[ct] = static_cast<const uint8_t *>(xv) + (mr * k + xo) * XB;
     if constexpr (XL) xsl.row[ct] = xs + mr * xstr + 2 * xo;
   }
 
@@ -639,7 +782,8 @@ __device__ __forceinline__ void smallm_tiles(const uint8_t *__restrict__ w, cons
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) c[i][rt] = C::load(w, aux, row[rt], k, ti, g);
       if constexpr (!XL) {
-        if constexpr (HALF) load_xh<MT>(xf[i], xr, ti);
+        if constexpr (LIMBS) load_xraw<MT>(xf[i], xrb, ti);
+        else if constexpr (HALF) load_xh<MT>(xf[i], xr, ti);
         else load_x<MT>(xf[i], xr, ti);
       }
     }
@@ -649,14 +793,23 @@ __device__ __forceinline__ void smallm_tiles(const uint8_t *__restrict__ w, cons
     for (int i = 0; i < B; ++i) {
       const int64_t ti = t + i * NW < hi ? t + i * NW : (t < hi ? t : lo);
       if constexpr (XL) {
-        if constexpr (HALF) lds_xh<MT>(xf[i], xsl, ti - lo);
+        if constexpr (LIMBS) lds_xl<MT>(xf[i], xsl, ti - lo, lo_off);
+        else if constexpr (HALF) lds_xh<MT>(xf[i], xsl, ti - lo);
         else lds_x<MT>(xf[i], xsl, ti - lo);
       }
       const uint32_t vm = (!XL && i == 0) ? 0xFFFFFFFFu : opaque(t + i * NW < hi ? 0xFFFFFFFFu : 0u);
+      if constexpr (LIMBS) {
+        XFragL<MT> lf;
+        if constexpr (XL) lf = xf[i];
+        else split_raw<MT>(xf[i], lf);
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        if constexpr (HALF) mma_chunk_h<MT>(c[i][rt], xf[i], acc[rt], vm);
-        else mma_chunk<C, MT>(c[i][rt], xf[i], acc[rt], g, vm);
+        for (int rt = 0; rt < RT; ++rt) mma_chunk_limbs<C, MT>(c[i][rt], lf, acc[rt], g, vm);
+      } else {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          if constexpr (HALF) mma_chunk_h<MT>(c[i][rt], xf[i], acc[rt], vm);
+          else mma_chunk<C, MT>(c[i][rt], xf[i], acc[rt], g, vm);
+        }
       }
     }
   };
@@ -666,8 +819,8 @@ __device__ __forceinline__ void smallm_tiles(const uint8_t *__restrict__ w, cons
     const int64_t t0 = lo + wave;
     if constexpr (XL) {
       constexpr int NT = 64 * NW, XR = 8;
-      const XStage st = make_stage(reinterpret_cast<const uint8_t *>(x + lo * C::CE), 2 * k, m,
-                                   2 * (hi - lo) * C::CE, xstr);
+      const XStage st = make_stage(static_cast<const uint8_t *>(xv) + lo * C::CE * XB, XB * k, m,
+                                   XB * (hi - lo) * C::CE, xstr);
       u32x4 v[XR];
       xs_load<NT, XR>(v, st, 0);
       __builtin_amdgcn_sched_barrier(0);  // the copy's loads first: its wait then skips the weights
@@ -676,7 +829,7 @@ __device__ __forceinline__ void smallm_tiles(const uint8_t *__restrict__ w, cons
       load_batch(t0, c0, xf0);
       // the copy's loads and the first weight loads are all in flight here
       __builtin_amdgcn_sched_barrier(0);
-      xs_finish<NT, XR>(xs, v, st);
+      xs_finish<NT, XR, XT>(xs, v, st, lo_off);
       run_batch(t0, c0, xf0);
       for (int64_t t = t0 + B * NW; t < hi; t += B * NW) {
         typename C::Chunk c[B][RT];
@@ -722,24 +875,24 @@ __device__ __forceinline__ int split_order(int b, int grid, int S) {
 
 // One weight: workgroup b takes row tiles [(b / S) RT, + RT), K slice b % S
 // (split partials at wsp + (b / S) S MT 64, counters cnt[b / S]).
-template <class C, int MT, int NW, int B, int RT, bool XL>
+template <class C, int MT, int NW, int B, int RT, bool XL, int XT = RQ_BF16>
 __global__ __launch_bounds__(64 * NW) void k_smallm(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
-                                                    const uint16_t *__restrict__ x, int64_t m, const Out o,
+                                                    const void *__restrict__ x, int64_t m, const Out o,
                                                     int64_t n, int64_t k, int S, f32x4 *__restrict__ wsp,
                                                     uint32_t *__restrict__ cnt, int xstr) {
   __shared__ f32x4 part[NW][RT][MT][64];
   extern __shared__ __attribute__((aligned(16))) uint8_t xs_dyn[];
   const int bid = split_order((int)blockIdx.x, (int)gridDim.x, S);
   const int64_t tile = bid / S;
-  smallm_tiles<C, MT, NW, B, RT, XL>(w, aux, x, m, o, n, k, tile, S, bid % S, wsp + tile * S * MT * 64, cnt + tile,
-                                     part, xs_dyn, xstr);
+  smallm_tiles<C, MT, NW, B, RT, XL, XT>(w, aux, x, m, o, n, k, tile, S, bid % S, wsp + tile * S * MT * 64,
+                                         cnt + tile, part, xs_dyn, xstr);
 }
 
 // A set of weights sharing x (pick_entry chooses this workgroup's weight;
 // every entry's workgroups are a multiple of S, so b / S numbers the tiles
 // of the whole set).
-template <class C, int MT, int NW, int B, int RT, bool XL>
-__global__ __launch_bounds__(64 * NW) void k_smallm_set(const WeightSet set, const uint16_t *__restrict__ x,
+template <class C, int MT, int NW, int B, int RT, bool XL, int XT = RQ_BF16>
+__global__ __launch_bounds__(64 * NW) void k_smallm_set(const WeightSet set, const void *__restrict__ x,
                                                         int64_t m, int64_t k, int S, f32x4 *__restrict__ wsp,
                                                         uint32_t *__restrict__ cnt, int xstr) {
   __shared__ f32x4 part[NW][RT][MT][64];
@@ -747,8 +900,8 @@ __global__ __launch_bounds__(64 * NW) void k_smallm_set(const WeightSet set, con
   const int bid = split_order((int)blockIdx.x, (int)gridDim.x, S);
   const SetEntry e = pick_entry(set, bid);
   const int gt = bid / S;
-  smallm_tiles<C, MT, NW, B, RT, XL>(e.w, e.aux, x, m, e.o, e.n, k, (bid - e.g0) / S, S, bid % S,
-                                     wsp + (int64_t)gt * S * MT * 64, cnt + gt, part, xs_dyn, xstr);
+  smallm_tiles<C, MT, NW, B, RT, XL, XT>(e.w, e.aux, x, m, e.o, e.n, k, (bid - e.g0) / S, S, bid % S,
+                                         wsp + (int64_t)gt * S * MT * 64, cnt + gt, part, xs_dyn, xstr);
 }
 
 // Largest LDS copy of the activation slice (beside the reduction buffer of
@@ -1033,16 +1186,16 @@ SmPlan smallm_plan(int64_t tiles, int64_t nk, bool can_split, int64_t m) {
   return p;
 }
 
-template <class C, int MT, int NW, int B, int RT, bool XL>
-int launch_mt(const rq_weight *const *w, int count, bool set, const uint16_t *x, int64_t m, const Out *o, int S,
+template <class C, int MT, int NW, int B, int RT, bool XL, int XT = RQ_BF16>
+int launch_mt(const rq_weight *const *w, int count, bool set, const void *x, int64_t m, const Out *o, int S,
               f32x4 *wsp, uint32_t *cnt, hipStream_t s, int xstr, size_t xbytes) {
   // the reduction buffer and the activation slice share the CU's 160 KB
   if (XL && (size_t)NW * RT * MT * 64 * sizeof(f32x4) + xbytes > 160 * 1024) return RQ_E_UNSUPPORTED;
   if (!set) {
     const rq_weight *wt = w[0];
     const int64_t tiles = ((wt->n + 15) / 16 + RT - 1) / RT;
-    if (!lds_allow<&k_smallm<C, MT, NW, B, RT, XL>>(xbytes)) return RQ_E_UNSUPPORTED;
-    hipLaunchKernelGGL((k_smallm<C, MT, NW, B, RT, XL>), dim3((unsigned)(tiles * S)), dim3(64 * NW), xbytes, s,
+    if (!lds_allow<&k_smallm<C, MT, NW, B, RT, XL, XT>>(xbytes)) return RQ_E_UNSUPPORTED;
+    hipLaunchKernelGGL((k_smallm<C, MT, NW, B, RT, XL, XT>), dim3((unsigned)(tiles * S)), dim3(64 * NW), xbytes, s,
                        wt->data, wt->data + wt->aux_off, x, m, o[0], wt->n, wt->k, S, wsp, cnt, xstr);
   } else {
     WeightSet ws;
@@ -1050,15 +1203,22 @@ int launch_mt(const rq_weight *const *w, int count, bool set, const uint16_t *x,
     const int rc = fill_set(ws, w, count, o, [&](const rq_weight *wj) { return ((wj->n + 15) / 16 + RT - 1) / RT * S; },
                             &total);
     if (rc) return rc;
-    if (!lds_allow<&k_smallm_set<C, MT, NW, B, RT, XL>>(xbytes)) return RQ_E_UNSUPPORTED;
-    hipLaunchKernelGGL((k_smallm_set<C, MT, NW, B, RT, XL>), dim3((unsigned)total), dim3(64 * NW), xbytes, s, ws, x,
-                       m, w[0]->k, S, wsp, cnt, xstr);
+    if (!lds_allow<&k_smallm_set<C, MT, NW, B, RT, XL, XT>>(xbytes)) return RQ_E_UNSUPPORTED;
+    hipLaunchKernelGGL((k_smallm_set<C, MT, NW, B, RT, XL, XT>), dim3((unsigned)total), dim3(64 * NW), xbytes, s, ws,
+                       x, m, w[0]->k, S, wsp, cnt, xstr);
   }
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "small-M launch failed");
 }
 
-template <class C, int MT, int NW, int B>
+// Chunks a wave loads per batch: the planned B, fewer where the fragments
+// are large (half-block chunks; limb fragments hold twice the activation
+// registers of bf16 ones).
+template <class C, int MT, int NW, int B, int XT = RQ_BF16>
 constexpr int sm_batch() {
+  if constexpr (XT != RQ_BF16) {
+    constexpr int cap = MT == 1 ? 2 : 1;
+    return B < cap ? B : cap;
+  }
   if constexpr (C::CE == 128) {
     constexpr int cap = MT == 1 ? (NW == 16 ? 3 : 4) : (MT == 2 ? (NW == 16 ? 1 : 2) : 1);
     return B < cap ? B : cap;
@@ -1066,11 +1226,12 @@ constexpr int sm_batch() {
   return B;
 }
 
-// Plans and launches one weight or a set (every weight of format C, one k).
-template <class C, int MT>
-int run_plan(const rq_weight *const *w, int count, bool set, const void *xv, int64_t m, const Out *o, hipStream_t s,
+// Plans and launches one weight or a set (every weight of format C, one k);
+// XT: bf16 activations, or f32 ones on the limb variant (the LDS slice then
+// holds a hi and a lo copy).
+template <class C, int MT, int XT = RQ_BF16>
+int run_plan(const rq_weight *const *w, int count, bool set, const void *x, int64_t m, const Out *o, hipStream_t s,
              WsLease *ws) {
-  const uint16_t *x = static_cast<const uint16_t *>(xv);
   int64_t tiles = 0;
   for (int j = 0; j < count; ++j) tiles += (w[j]->n + 15) / 16;
   // No K split for rows of up to 1024 elements at m <= 32: the slice copy
@@ -1103,7 +1264,7 @@ int run_plan(const rq_weight *const *w, int count, bool set, const void *xv, int
   // workgroup per CU: 11.3 -> 14.8 us).
   const int64_t cps = (w[0]->k / C::CE + p.s - 1) / p.s;
   const int xstr = (int)(cps * C::CE * 2 + 16);
-  const size_t xbytes = (size_t)m * (size_t)xstr;
+  const size_t xbytes = (size_t)m * (size_t)xstr * (XT == RQ_BF16 ? 1 : 2);
   // A copy above 80 KB leaves one workgroup per CU: only where the grid is
   // about one round (the 4864 x 896 gate at M = 64, 304 workgroups, gains;
   // gate and up in one launch, 608, lose: 14.0 -> 14.6 us).
@@ -1116,12 +1277,12 @@ int run_plan(const rq_weight *const *w, int count, bool set, const void *xv, int
 #define RQ_SM(NW, B, RT)                                                                                     \
   {                                                                                                          \
     if (xl) {                                                                                                \
-      const int rc_ = launch_mt<C, MT, NW, sm_batch<C, MT, NW, B>(), RT, true>(w, count, set, x, m, o, p.s, wsp, \
-                                                                              cnt, s, xstr, xbytes);        \
+      const int rc_ = launch_mt<C, MT, NW, sm_batch<C, MT, NW, B, XT>(), RT, true, XT>(                      \
+          w, count, set, x, m, o, p.s, wsp, cnt, s, xstr, xbytes);                                           \
       if (rc_ != RQ_E_UNSUPPORTED) return rc_;                                                               \
     }                                                                                                        \
-    return launch_mt<C, MT, NW, sm_batch<C, MT, NW, B>(), RT, false>(w, count, set, x, m, o, p.s, wsp, cnt, s, 0, \
-                                                                     0);                                    \
+    return launch_mt<C, MT, NW, sm_batch<C, MT, NW, B, XT>(), RT, false, XT>(w, count, set, x, m, o, p.s, wsp, \
+                                                                             cnt, s, 0, 0);                  \
   }
   if constexpr (MT == 4) {
     if (p.nw == 16) RQ_SM(16, 1, 1);
@@ -1146,12 +1307,27 @@ int run_plan(const rq_weight *const *w, int count, bool set, const void *xv, int
 #undef RQ_SM
 }
 
-template <class C>
+template <class C, int XT = RQ_BF16>
 int run(const rq_weight *const *w, int count, bool set, const void *x, int64_t m, const Out *o, hipStream_t s,
         WsLease *ws) {
-  if (m <= 16) return run_plan<C, 1>(w, count, set, x, m, o, s, ws);
-  if (m <= 32) return run_plan<C, 2>(w, count, set, x, m, o, s, ws);
-  return run_plan<C, 4>(w, count, set, x, m, o, s, ws);
+  if (m <= 16) return run_plan<C, 1, XT>(w, count, set, x, m, o, s, ws);
+  if (m <= 32) return run_plan<C, 2, XT>(w, count, set, x, m, o, s, ws);
+  return run_plan<C, 4, XT>(w, count, set, x, m, o, s, ws);
+}
+
+// f32 activations on the limb variant (64-element chunks for every format).
+template <int XT>
+int dispatch_limbs(const rq_weight *const *w, int count, bool set, const void *x, int64_t m, const Out *o,
+                   hipStream_t s, WsLease *ws) {
+  switch (w[0]->qtype) {
+    case RQ_Q4_K: return run<SmQ4K, XT>(w, count, set, x, m, o, s, ws);
+    case RQ_Q6_K: return run<SmQ6K, XT>(w, count, set, x, m, o, s, ws);
+    case RQ_Q8_0: return run<SmQ8, XT>(w, count, set, x, m, o, s, ws);
+    case RQ_Q5_K: return run<SmQ5K, XT>(w, count, set, x, m, o, s, ws);
+    case RQ_Q4_0: return run<SmQx0<false>, XT>(w, count, set, x, m, o, s, ws);
+    case RQ_Q5_0: return run<SmQx0<true>, XT>(w, count, set, x, m, o, s, ws);
+    default: return RQ_E_UNSUPPORTED;
+  }
 }
 
 int dispatch_bf16(const rq_weight *const *w, int count, bool set, const void *x, int64_t m, const Out *o,
@@ -1175,6 +1351,11 @@ int dispatch_bf16(const rq_weight *const *w, int count, bool set, const void *x,
 // f32 / f16 activations, 2 <= m <= 64, k % 64 == 0, 16-byte aligned x
 // (dispatched from m = 4, and at m = 2..3 for rows the VALU layouts do not
 // take).
+// One weight runs on the f32 matrix cores (exact weights, 16 MFMAs of K = 4
+// a chunk): for a lone weight it beats the two-limb variant, whose weight
+// split costs about four VALU instructions a weight (Qwen2-0.5B layer at
+// M = 16, rocprof medians: gate 7.96 vs 8.48 us, o 5.75 vs 6.12, down 10.5 vs
+// 11.5; 7 launches a layer M = 64: 218 vs 153 GB/s).
 int launch_linear_smallm_f32(const rq_weight *wt, const void *x, int xtype, int64_t m, const Out &o,
                              hipStream_t s, WsLease *ws) {
   if (m < 2 || m > 64 || wt->k % 64 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
@@ -1192,14 +1373,20 @@ int launch_linear_smallm_f32_slices(const rq_weight *wt, const void *x, int xtyp
   return RQ_E_UNSUPPORTED;
 }
 
-// bf16 activations, 2 <= m <= 64, k % 64 == 0, 16-byte aligned x, weights of
-// one format and k.
-int launch_linear_smallm_set(const rq_weight *const *w, int count, const void *x, int64_t m, const Out *o,
-                             hipStream_t s, WsLease *ws) {
+// bf16 (or, on the limb variant, f32) activations, 2 <= m <= 64, k % 64 ==
+// 0, 16-byte aligned x, weights of one format and k.  A set of f32 weights
+// takes the limb variant: one launch for the set beats the f32 kernel's one
+// launch a weight (Qwen2-0.5B layer, q/k/v and gate/up as sets, 4 launches a
+// layer: M = 4 / 16 / 64 292 / 291 / 224 GB/s against 207 / 211 / 218 with 7
+// launches on the f32 kernel).
+int launch_linear_smallm_set(const rq_weight *const *w, int count, const void *x, int xtype, int64_t m,
+                             const Out *o, hipStream_t s, WsLease *ws) {
   const int64_t k = w[0]->k;
   if (m < 2 || m > 64 || k % 64 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return RQ_E_UNSUPPORTED;
   for (int j = 1; j < count; ++j)
     if (w[j]->qtype != w[0]->qtype || w[j]->k != k) return RQ_E_UNSUPPORTED;
+  if (xtype == RQ_F32) return dispatch_limbs<RQ_F32>(w, count, true, x, m, o, s, ws);
+  if (xtype != RQ_BF16) return RQ_E_UNSUPPORTED;
   return dispatch_bf16(w, count, true, x, m, o, s, ws);
 }
 
