@@ -20,7 +20,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 SOURCES = ["csrc/rq_api.cpp", "csrc/rq_dequant.hip", "csrc/rq_gemv.hip", "csrc/rq_gemv_mx.hip", "csrc/rq_fp8.hip",
-           "csrc/rq_gemm.hip", "csrc/rq_smallm.hip", "csrc/rq_marlin.hip", "csrc/rq_kv.hip", "csrc/rq_upload.hip",
+           "csrc/rq_gemm.hip", "csrc/rq_smallm.hip", "csrc/rq_smallm_codes.hip", "csrc/rq_marlin.hip", "csrc/rq_kv.hip", "csrc/rq_upload.hip",
            "csrc/rq_workspace.cpp", "csrc/rq_noalloc.hip", "host/rq_host.cpp"]
 ROOT = PKG.parent
 HOST_TEST_SRC = ROOT / "tests" / "cpp" / "test_host.cpp"

@@ -831,6 +831,12 @@ int launch_linear_fused(const rq_weight *wt, const void *x, int xtype, int64_t m
   // VALU kernels' few FMAs per weight are cheaper: 37 vs 47 us per 0.5B
   // layer at m = 2, 150 vs 54 us at m = 16).
   const bool f32x = xtype == RQ_F32 || xtype == RQ_F16;
+  // f32 rows of Q4_K / Q6_K / Q8_0: the integer codes on the bf16 matrix
+  // cores against two bf16 limbs of x, scales applied per run of 16 or 32.
+  if (m >= 4 && m <= 64 && xtype == RQ_F32) {
+    const int rc = launch_linear_smallm_codes(&wt, 1, false, x, m, &o, s, &ws);
+    if (rc != RQ_E_UNSUPPORTED) return rc;
+  }
   if (m >= 4 && m <= 64 && f32x) {
     const int rc = launch_linear_smallm_f32(wt, x, xtype, m, o, s, &ws);
     if (rc != RQ_E_UNSUPPORTED) return rc;
@@ -910,7 +916,10 @@ int launch_linear_multi(const rq_weight *const *w, int count, const void *x, int
   // them (two rows stay on the segment kernel below, f32 three rows one by
   // one where rq_linear gives them other layouts).
   if (xtype == RQ_BF16 && m >= 3 && m <= 64) return launch_linear_smallm_set(w, count, x, xtype, m, o, s, &ws);
-  if (xtype == RQ_F32 && m >= 4 && m <= 64) return launch_linear_smallm_set(w, count, x, xtype, m, o, s, &ws);
+  if (xtype == RQ_F32 && m >= 4 && m <= 64) {
+    const int rc = launch_linear_smallm_codes(w, count, true, x, m, o, s, &ws);
+    return rc != RQ_E_UNSUPPORTED ? rc : launch_linear_smallm_set(w, count, x, xtype, m, o, s, &ws);
+  }
   if (m != 1 && m != 2) return RQ_E_UNSUPPORTED;
   switch (qt) {
     case RQ_Q4_K: return k % 64 ? RQ_E_UNSUPPORTED : run_seg_set<FmtQ4K>(w, count, x, xtype, m, o, s);

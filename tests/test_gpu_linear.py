@@ -219,6 +219,39 @@ def test_small_m_f32_activations(dev, qtype, m, n, k):
     assert norm_err(y, ref(x.numpy(), wf)) <= TOL_F32
 
 
+# f32 activations with 4 <= M <= 16 on Q4_K / Q6_K / Q8_0 (17..32 rows on rows
+# longer than 2048) take the integer codes on the bf16 matrix cores (128 + q,
+# or the int8 code, exact in bf16) against two bf16 limbs of x, the scales
+# applied per run of 16 or 32 weights to the f32 sums.  x spans six decades
+# (every 7th element x300, every 11th x1e-3); few row tiles on long rows split
+# K over up to four workgroups (7 x 4096, 16 x 4096, 24 x 8192), the
+# activation slice is staged in LDS (16 x 896, 16 x 4096 in four slices,
+# 17 x 4864) or read from memory (m < 16, 16 x 8192, 31 x 4096), rows straddle
+# blocks (k = 896 for the 256-element formats), and m, n end in partial tiles.
+@pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0])
+@pytest.mark.parametrize("m,n,k", [(4, 4864, 896), (7, 100, 4096), (16, 896, 896), (16, 64, 4096),
+                                   (16, 64, 8192), (17, 896, 4864), (31, 200, 4096), (24, 40, 8192)])
+def test_small_m_f32_codes(dev, qtype, m, n, k):
+    print(f"codes qtype={qtype} m={m} n={n} k={k}", flush=True)
+    w, wf = make(qtype, n, k, 41 + m + n + k)
+    x = synth.activations(9 + m, m, k)
+    x[:, ::7] *= 300.0
+    x[:, 3::11] *= 1e-3
+    r = ref(x, wf)
+    y = w.forward(torch.from_numpy(x).to(dev)).cpu().numpy()
+    assert norm_err(y, r) <= TOL_F32
+    # per row as well: a row of small activations is not hidden by the others
+    for i in range(m):
+        assert norm_err(y[i:i + 1], r[i:i + 1]) <= TOL_F32, i
+    # a set of three weights of the format sharing x, each as its own call
+    others = [make(qtype, nn, k, 43 + nn + i) for i, nn in enumerate((n, 16, 34))]
+    xt = torch.from_numpy(x).to(dev)
+    outs = rq.linear_multi([o for o, _ in others], xt, out_dtype=torch.float32)
+    for (o, of), yo in zip(others, outs):
+        assert norm_err(yo.cpu().numpy(), ref(x, of)) <= TOL_F32
+        assert norm_err(yo.cpu().numpy(), o.forward(xt).cpu().numpy()) <= 1e-5
+
+
 # More than 64 f32 rows run on the tiled GEMM with two bf16 limbs per
 # operand (exact weights split into hi + lo, f32 accumulation): tiles past
 # m and n, rows straddling Q4_K blocks (k = 896), k not a multiple of 128

@@ -6,7 +6,7 @@ barrier orders instruction issue only, so every thread has to wait for its
 own partial stores to be acknowledged (s_waitcnt vmcnt(0)) before that
 barrier, or the counter can move while a partial is still in flight and the
 last workgroup adds stale data.  This test disassembles the gfx950 code of
-rq_smallm.hip and checks, for every kernel with a split counter, that the
+rq_smallm.hip and rq_smallm_codes.hip and checks, for every kernel with a split counter, that the
 barrier before each counter atomic is reached with no agent-scope store
 still unwaited."""
 import re
@@ -58,3 +58,18 @@ def test_split_partials_complete_before_count(tmp_path):
         bad = unwaited_counts(body)
         assert not bad, (name, [body[b] for b in bad[:3]])
     assert checked == {"k_smallm", "k_smallm_set", "k_smallm_f32"}, checked
+
+
+@pytest.mark.skipif(not HAVE_TOOLS, reason="ROCm toolchain not present")
+def test_codes_split_partials_complete_before_count(tmp_path):
+    ks = kernels(disassembly("rq_smallm_codes.hip", tmp_path), r"k_smallm_codes")
+    assert ks, "no k_smallm_codes kernels in the code object"
+    checked = set()
+    for name, body in ks.items():
+        if not any(ins.startswith("global_atomic_add") for ins in body):
+            continue
+        assert any(re.search(r"^global_store\S*\s.*\bsc1\b", ins) for ins in body), name
+        checked.add("k_smallm_codes_set" if "k_smallm_codes_set" in name else "k_smallm_codes")
+        bad = unwaited_counts(body)
+        assert not bad, (name, [body[b] for b in bad[:3]])
+    assert checked == {"k_smallm_codes", "k_smallm_codes_set"}, checked
