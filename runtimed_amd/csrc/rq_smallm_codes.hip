@@ -254,74 +254,91 @@ __device__ __forceinline__ void cx_stage(uint8_t *xs, u32x4 (&v)[XR], const XSta
   __syncthreads();
 }
 
-// One chunk of one row tile on MT column tiles: S = codes, X = ones; the
-// lane's outputs += D S - M' X per run (or per run pair).  vm masks the codes
-// of a chunk past the end (zero codes and zero scales add nothing).
-template <class C, int MT>
-__device__ __forceinline__ void codes_chunk(const typename C::Chunk &c, const CxFrag<MT> &xf, f32x4 (&acc)[MT],
-                                            int g, bool live) {
-  bf16x8 b[4];
-  float d[4], mn[4];
-  C::decode(c, g, b, d, mn);
-  if (!live) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) d[r] = mn[r] = 0.0f;
-  }
+// One chunk of RT row tiles on MT column tiles: X = ones (per column tile and
+// run, shared by the row tiles), S = codes; the lane's outputs += D S - M' X
+// per run (or per run pair).  live false (a chunk past the end of the slice,
+// loaded from a valid place) zeroes the scales, so it adds nothing.
+template <class C, int MT, int RT>
+__device__ __forceinline__ void codes_chunk(const typename C::Chunk (&c)[RT], const CxFrag<MT> &xf,
+                                            f32x4 (&acc)[RT][MT], int g, bool live) {
   const bf16x8 ones = __builtin_bit_cast(bf16x8, (u32x4){0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
   const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
   constexpr int G = C::PAIR ? 2 : 1;  // runs sharing a scale
+  f32x4 X[MT][4 / G];
+  if constexpr (C::MIN) {
 #pragma unroll
-  for (int r0 = 0; r0 < 4; r0 += G) {
+    for (int ct = 0; ct < MT; ++ct)
 #pragma unroll
-    for (int ct = 0; ct < MT; ++ct) {
-      f32x4 S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.a[ct][r0], b[r0], zero, 0, 0, 0);
-      if (G == 2) S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.a[ct][r0 + 1], b[r0 + 1], S, 0, 0, 0);
-      if constexpr (C::MIN) {
-        f32x4 X = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.a[ct][r0], ones, zero, 0, 0, 0);
-        if (G == 2) X = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.a[ct][r0 + 1], ones, X, 0, 0, 0);
+      for (int r0 = 0; r0 < 4; r0 += G) {
+        X[ct][r0 / G] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.a[ct][r0], ones, zero, 0, 0, 0);
+        if (G == 2)
+          X[ct][r0 / G] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.a[ct][r0 + 1], ones, X[ct][r0 / G], 0, 0, 0);
+      }
+  }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[ct][i] = fmaf(d[r0], S[i], fmaf(-mn[r0], X[i], acc[ct][i]));
-      } else {
+  for (int rt = 0; rt < RT; ++rt) {
+    bf16x8 b[4];
+    float d[4], mn[4];
+    C::decode(c[rt], g, b, d, mn);
+    if (!live) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[ct][i] = fmaf(d[r0], S[i], acc[ct][i]);
+      for (int r = 0; r < 4; ++r) d[r] = mn[r] = 0.0f;
+    }
+#pragma unroll
+    for (int r0 = 0; r0 < 4; r0 += G) {
+#pragma unroll
+      for (int ct = 0; ct < MT; ++ct) {
+        f32x4 S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.a[ct][r0], b[r0], zero, 0, 0, 0);
+        if (G == 2) S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.a[ct][r0 + 1], b[r0 + 1], S, 0, 0, 0);
+        if constexpr (C::MIN) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            acc[rt][ct][i] = fmaf(d[r0], S[i], fmaf(-mn[r0], X[ct][r0 / G][i], acc[rt][ct][i]));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[rt][ct][i] = fmaf(d[r0], S[i], acc[rt][ct][i]);
+        }
       }
     }
   }
 }
 
-// Lane slot l of column tile ct: activation rows 16 ct + 4 (l / 16) + i,
-// weight row n0 + l % 16.
+// Output slot q = (rt MT + ct) 64 + l of a workgroup: activation rows
+// 16 ct + 4 (l / 16) + i, weight row n0 + 16 rt + l % 16.
 template <int MT>
-__device__ __forceinline__ void codes_store(const f32x4 &v, int ct, int l, int64_t m, int64_t n, int64_t n0,
-                                            const Out &o) {
-  const int64_t wr = n0 + (l & 15);
-  if (wr >= n) return;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t ar = 16 * ct + 4 * (l >> 4) + i;
-    if (ar < m) store_linear(o, ar, n, wr, v[i]);
-  }
+__device__ __forceinline__ void codes_store(float v, int q, int i, int64_t m, int64_t n, int64_t n0, const Out &o) {
+  const int l = q & 63, ct = (q >> 6) % MT, rt = (q >> 6) / MT;
+  const int64_t wr = n0 + 16 * rt + (l & 15), ar = 16 * ct + 4 * (l >> 4) + i;
+  if (wr < n && ar < m) store_linear(o, ar, n, wr, v);
 }
 
-// The tiles of one workgroup: 16 weight rows (tile), K slice s of S, NW
-// waves; xs / xstr: the LDS slice with XL.
-template <class C, int MT, int NW, int B, bool XL>
+// The tiles of one workgroup: RT row tiles of 16 weight rows from tile
+// group tg, K slice s of S, NW waves; xs / xstr: the LDS slice with XL.
+template <class C, int MT, int NW, int B, int RT, bool XL>
 __device__ __forceinline__ void codes_tiles(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
                                             const float *__restrict__ x, int64_t m, const Out &o, int64_t n,
-                                            int64_t k, int64_t tile, int S, int s, f32x4 *__restrict__ wsp,
-                                            uint32_t *__restrict__ cnt, f32x4 (&part)[NW][MT][64], uint8_t *xs,
-                                            int xstr) {
+                                            int64_t k, int64_t tg, int S, int s, f32x4 *__restrict__ wsp,
+                                            uint32_t *__restrict__ cnt, f32x4 (&part)[NW][RT * MT * 64],
+                                            uint8_t *xs, int xstr) {
+  constexpr int NSLOT = RT * MT * 64;
   const int lane = threadIdx.x & 63, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t n0 = tile * 16;
-  const int64_t row = n0 + (lane & 15) < n ? n0 + (lane & 15) : n - 1;
+  const int64_t n0 = tg * 16 * RT;
+  int64_t row[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int64_t r = n0 + 16 * rt + (lane & 15);
+    row[rt] = r < n ? r : n - 1;
+  }
   const int64_t nk = k / 64, cps = (nk + S - 1) / S;
   const int64_t lo = s * cps, hi = lo + cps < nk ? lo + cps : nk;
   typedef typename std::conditional<XL, CxFrag<MT>, CxRaw<MT>>::type XF;
 
-  f32x4 acc[MT];
+  f32x4 acc[RT][MT];
 #pragma unroll
-  for (int ct = 0; ct < MT; ++ct) acc[ct] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < MT; ++ct) acc[rt][ct] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 
   // The lane's activation row in each column tile (rows past m read row m - 1;
   // their outputs are not stored), at its lane group's element 4g.
@@ -334,22 +351,23 @@ __device__ __forceinline__ void codes_tiles(const uint8_t *__restrict__ w, const
     xsr[ct] = XL ? xs + mr * xstr + 16 * g : nullptr;
   }
 
-  auto load_batch = [&](int64_t t, typename C::Chunk (&c)[B], XF (&xf)[B]) {
+  auto load_batch = [&](int64_t t, typename C::Chunk (&c)[B][RT], XF (&xf)[B]) {
 #pragma unroll
     for (int i = 0; i < B; ++i) {
       const int64_t ti = t + i * NW < hi ? t + i * NW : (t < hi ? t : lo);
-      c[i] = C::load(w, aux, row, k, ti, g);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) c[i][rt] = C::load(w, aux, row[rt], k, ti, g);
       if constexpr (!XL) cx_load<MT>(xf[i], xr, ti);
     }
   };
-  auto run_batch = [&](int64_t t, const typename C::Chunk (&c)[B], XF (&xf)[B]) {
+  auto run_batch = [&](int64_t t, const typename C::Chunk (&c)[B][RT], XF (&xf)[B]) {
 #pragma unroll
     for (int i = 0; i < B; ++i) {
       const int64_t ti = t + i * NW < hi ? t + i * NW : (t < hi ? t : lo);
       CxFrag<MT> f;
       if constexpr (XL) cx_lds<MT>(f, xsr, ti - lo);
       else cx_split<MT>(xf[i], f);
-      codes_chunk<C, MT>(c[i], f, acc, g, t + i * NW < hi);
+      codes_chunk<C, MT, RT>(c[i], f, acc, g, t + i * NW < hi);
     }
   };
 
@@ -361,14 +379,14 @@ __device__ __forceinline__ void codes_tiles(const uint8_t *__restrict__ w, const
       u32x4 v[XR];
       xs_load<NT, XR>(v, st, 0);
       __builtin_amdgcn_sched_barrier(0);  // the copy's loads first: its wait then skips the weights
-      typename C::Chunk c0[B];
+      typename C::Chunk c0[B][RT];
       XF xf0[B];
       load_batch(t0, c0, xf0);
       __builtin_amdgcn_sched_barrier(0);
       cx_stage<NT, XR>(xs, v, st);
       run_batch(t0, c0, xf0);
       for (int64_t t = t0 + B * NW; t < hi; t += B * NW) {
-        typename C::Chunk c[B];
+        typename C::Chunk c[B][RT];
         XF xf[B];
         load_batch(t, c, xf);
         __builtin_amdgcn_sched_barrier(0);
@@ -376,7 +394,7 @@ __device__ __forceinline__ void codes_tiles(const uint8_t *__restrict__ w, const
       }
     } else {
       for (int64_t t = t0; t < hi; t += B * NW) {
-        typename C::Chunk c[B];
+        typename C::Chunk c[B][RT];
         XF xf[B];
         load_batch(t, c, xf);
         __builtin_amdgcn_sched_barrier(0);
@@ -386,87 +404,136 @@ __device__ __forceinline__ void codes_tiles(const uint8_t *__restrict__ w, const
   }
 
 #pragma unroll
-  for (int ct = 0; ct < MT; ++ct) part[wave][ct][lane] = acc[ct];
-  __syncthreads();
-  auto sum = [&](int slot) {
-    const int ct = slot >> 6, l = slot & 63;
-    f32x4 v = part[0][ct][l];
+  for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-    for (int q = 1; q < NW; ++q) v += part[q][ct][l];
-    return v;
-  };
-  auto put = [&](int slot, const f32x4 &v) { codes_store<MT>(v, slot >> 6, slot & 63, m, n, n0, o); };
+    for (int ct = 0; ct < MT; ++ct) part[wave][(rt * MT + ct) * 64 + lane] = acc[rt][ct];
+  __syncthreads();
   if (S > 1) {
-    split_finish<MT * 64, 64 * NW>(sum, put, S, s, wsp, cnt);
+    auto sum = [&](int q) {
+      f32x4 v = part[0][q];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) v += part[w2][q];
+      return v;
+    };
+    auto put = [&](int q, const f32x4 &v) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) codes_store<MT>(v[i], q, i, m, n, n0, o);
+    };
+    split_finish<NSLOT, 64 * NW>(sum, put, S, s, wsp, cnt);
     return;
   }
-  for (int slot = threadIdx.x; slot < MT * 64; slot += 64 * NW) put(slot, sum(slot));
+  // The waves' partials summed one float a thread (in wave order), every
+  // thread of the workgroup taking part: all NW reads issued at once.
+  const float *pf = reinterpret_cast<const float *>(&part[0][0]);
+  for (int f = threadIdx.x; f < NSLOT * 4; f += 64 * NW) {
+    float p[NW];
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) p[w2] = pf[w2 * NSLOT * 4 + f];
+    float v = p[0];
+#pragma unroll
+    for (int w2 = 1; w2 < NW; ++w2) v += p[w2];
+    codes_store<MT>(v, f >> 2, f & 3, m, n, n0, o);
+  }
 }
 
-template <class C, int MT, int NW, int B, bool XL>
+template <class C, int MT, int NW, int B, int RT, bool XL>
 __global__ __launch_bounds__(64 * NW) void k_smallm_codes(const uint8_t *__restrict__ w,
                                                           const uint8_t *__restrict__ aux,
                                                           const float *__restrict__ x, int64_t m, const Out o,
                                                           int64_t n, int64_t k, int S, f32x4 *__restrict__ wsp,
                                                           uint32_t *__restrict__ cnt, int xstr) {
-  __shared__ f32x4 part[NW][MT][64];
+  __shared__ f32x4 part[NW][RT * MT * 64];
   extern __shared__ __attribute__((aligned(16))) uint8_t xs_dyn[];
   const int bid = split_order((int)blockIdx.x, (int)gridDim.x, S);
-  const int64_t tile = bid / S;
-  codes_tiles<C, MT, NW, B, XL>(w, aux, x, m, o, n, k, tile, S, bid % S, wsp + tile * S * MT * 64, cnt + tile, part,
-                                xs_dyn, xstr);
+  const int64_t tg = bid / S;
+  codes_tiles<C, MT, NW, B, RT, XL>(w, aux, x, m, o, n, k, tg, S, bid % S, wsp + tg * S * RT * MT * 64, cnt + tg,
+                                    part, xs_dyn, xstr);
 }
 
-template <class C, int MT, int NW, int B, bool XL>
+template <class C, int MT, int NW, int B, int RT, bool XL>
 __global__ __launch_bounds__(64 * NW) void k_smallm_codes_set(const WeightSet set, const float *__restrict__ x,
                                                               int64_t m, int64_t k, int S, f32x4 *__restrict__ wsp,
                                                               uint32_t *__restrict__ cnt, int xstr) {
-  __shared__ f32x4 part[NW][MT][64];
+  __shared__ f32x4 part[NW][RT * MT * 64];
   extern __shared__ __attribute__((aligned(16))) uint8_t xs_dyn[];
   const int bid = split_order((int)blockIdx.x, (int)gridDim.x, S);
   const SetEntry e = pick_entry(set, bid);
   const int gt = bid / S;
-  codes_tiles<C, MT, NW, B, XL>(e.w, e.aux, x, m, e.o, e.n, k, (bid - e.g0) / S, S, bid % S,
-                                wsp + (int64_t)gt * S * MT * 64, cnt + gt, part, xs_dyn, xstr);
+  codes_tiles<C, MT, NW, B, RT, XL>(e.w, e.aux, x, m, e.o, e.n, k, (bid - e.g0) / S, S, bid % S,
+                                    wsp + (int64_t)gt * S * RT * MT * 64, cnt + gt, part, xs_dyn, xstr);
 }
 
-template <class C, int MT, int NW, int B, bool XL>
+// Tile groups (RT row tiles each) of a weight.
+template <int RT>
+int64_t tile_groups(const rq_weight *w) {
+  return ((w->n + 15) / 16 + RT - 1) / RT;
+}
+
+template <class C, int MT, int NW, int B, int RT, bool XL>
 int codes_launch(const rq_weight *const *w, int count, bool set, const float *x, int64_t m, const Out *o, int S,
                  f32x4 *wsp, uint32_t *cnt, hipStream_t s, int xstr, size_t xbytes) {
-  if (XL && (size_t)NW * MT * 64 * sizeof(f32x4) + xbytes > 160 * 1024) return RQ_E_UNSUPPORTED;
+  if (XL && (size_t)NW * RT * MT * 64 * sizeof(f32x4) + xbytes > 160 * 1024) return RQ_E_UNSUPPORTED;
   if (!set) {
     const rq_weight *wt = w[0];
-    const int64_t tiles = (wt->n + 15) / 16;
-    if (!lds_allow<&k_smallm_codes<C, MT, NW, B, XL>>(xbytes)) return RQ_E_UNSUPPORTED;
-    hipLaunchKernelGGL((k_smallm_codes<C, MT, NW, B, XL>), dim3((unsigned)(tiles * S)), dim3(64 * NW), xbytes, s,
-                       wt->data, wt->data + wt->aux_off, x, m, o[0], wt->n, wt->k, S, wsp, cnt, xstr);
+    if (!lds_allow<&k_smallm_codes<C, MT, NW, B, RT, XL>>(xbytes)) return RQ_E_UNSUPPORTED;
+    hipLaunchKernelGGL((k_smallm_codes<C, MT, NW, B, RT, XL>), dim3((unsigned)(tile_groups<RT>(wt) * S)),
+                       dim3(64 * NW), xbytes, s, wt->data, wt->data + wt->aux_off, x, m, o[0], wt->n, wt->k, S, wsp,
+                       cnt, xstr);
   } else {
     WeightSet ws;
     int64_t total = 0;
-    const int rc = fill_set(ws, w, count, o, [&](const rq_weight *wj) { return (wj->n + 15) / 16 * S; }, &total);
+    const int rc = fill_set(ws, w, count, o, [&](const rq_weight *wj) { return tile_groups<RT>(wj) * S; }, &total);
     if (rc) return rc;
-    if (!lds_allow<&k_smallm_codes_set<C, MT, NW, B, XL>>(xbytes)) return RQ_E_UNSUPPORTED;
-    hipLaunchKernelGGL((k_smallm_codes_set<C, MT, NW, B, XL>), dim3((unsigned)total), dim3(64 * NW), xbytes, s, ws, x,
-                       m, w[0]->k, S, wsp, cnt, xstr);
+    if (!lds_allow<&k_smallm_codes_set<C, MT, NW, B, RT, XL>>(xbytes)) return RQ_E_UNSUPPORTED;
+    hipLaunchKernelGGL((k_smallm_codes_set<C, MT, NW, B, RT, XL>), dim3((unsigned)total), dim3(64 * NW), xbytes, s,
+                       ws, x, m, w[0]->k, S, wsp, cnt, xstr);
   }
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "small-M codes launch failed");
 }
 
 // Plan: K split over S workgroups (up to 4) where few row tiles leave CUs idle
 // and there are 16 or more rows (or long rows); eight waves, one chunk a
-// batch; the activation slice in LDS from 16 rows when it fits.  Graph-timed
-// against the f32 matrix-core kernel (one weight) and the two-limb set kernel
-// (q/k/v, gate/up), 32 distinct Q4_K copies of the 0.5B layer, us a launch,
-// old -> this plan:
-//   M = 4:  gate/up set 9.1 -> 6.9, q/k/v set 4.8 -> 4.2, o 4.5 -> 4.0,
-//           down 9.4 -> 7.6, gate 6.8 -> 5.7
-//   M = 16: gate/up set 10.6 -> 8.7, q/k/v set 5.4 -> 4.5, o 4.8 -> 4.3,
-//           down 10.1 -> 8.6, gate 7.1 -> 6.1
+// batch; two row tiles a workgroup from 256 workgroups (a launch that would
+// fill the CUs more than once, or nearly); the activation slice in LDS from
+// 16 rows when it fits.  Graph-timed, 32 distinct Q4_K copies of the 0.5B
+// layer, us a launch, against the f32 matrix-core kernel (one weight) and the
+// two-limb set kernel (q/k/v, gate/up) -> this kernel:
+//   M = 4:  gate/up set 9.2 -> 7.1, q/k/v set 4.9 -> 3.9, o 4.5 -> 3.6,
+//           down 9.3 -> 7.5, gate 6.8 -> 4.7
+//   M = 16: gate/up set 10.7 -> 7.7, q/k/v set 5.5 -> 4.2, o 4.9 -> 3.9,
+//           down 10.2 -> 8.6, gate 7.1 -> 5.2
 //   M = 32: down 16.7 -> 10.9, but gate/up set 11.6 -> 13.5, o 5.0 -> 5.6
 //   M = 64: gate/up set 27.7 -> 23.2, but o 5.1 -> 9.9, gate 13.8 -> 16.9
-// Four waves with batches of two or four chunks, sixteen waves, and other
-// K splits were slower.  So this kernel takes 4 <= m <= 16, and 17..32 rows
-// on rows longer than 2048 elements; the rest stay on the other kernels.
+// (M = 32 / 64 with one row tile and the epilogue of one wave.)  Four waves
+// with batches of two or four chunks, sixteen waves and other K splits were
+// slower; two row tiles on the 56- and 72-tile launches lost 10-25%.  So this
+// kernel takes 4 <= m <= 16, and 17..32 rows on rows longer than 2048
+// elements; the rest stay on the other kernels.
+template <class C, int MT, int RT>
+int codes_go(const rq_weight *const *w, int count, bool set, const float *x, int64_t m, const Out *o, hipStream_t s,
+             WsLease *ws, int S) {
+  int64_t groups = 0;
+  for (int j = 0; j < count; ++j) groups += tile_groups<RT>(w[j]);
+  f32x4 *wsp = nullptr;
+  uint32_t *cnt = nullptr;
+  if (S > 1) {
+    int rc = RQ_OK;
+    cnt = groups <= WsLease::kCounters ? ws->counters() : nullptr;
+    wsp = cnt ? static_cast<f32x4 *>(ws->get((size_t)groups * S * RT * MT * 64 * sizeof(f32x4), &rc, true))
+              : nullptr;
+    if (!wsp) S = 1;
+  }
+  const int64_t nk = w[0]->k / 64, cps = (nk + S - 1) / S;
+  const int xstr = (int)(cps * 64 * 4 + 16);
+  const size_t xbytes = (size_t)m * (size_t)xstr;
+  const bool xl = m >= 16 && cps * 64 <= 2048 && xbytes <= kSmXsMax;
+  if (xl) {
+    const int rc = codes_launch<C, MT, 8, 1, RT, true>(w, count, set, x, m, o, S, wsp, cnt, s, xstr, xbytes);
+    if (rc != RQ_E_UNSUPPORTED) return rc;
+  }
+  return codes_launch<C, MT, 8, 1, RT, false>(w, count, set, x, m, o, S, wsp, cnt, s, 0, 0);
+}
+
 template <class C, int MT>
 int codes_plan(const rq_weight *const *w, int count, bool set, const float *x, int64_t m, const Out *o,
                hipStream_t s, WsLease *ws) {
@@ -477,23 +544,9 @@ int codes_plan(const rq_weight *const *w, int count, bool set, const float *x, i
   if (ws != nullptr && tiles <= WsLease::kCounters && tiles < 128 && !(w[0]->k <= 1024 && m <= 64) &&
       (m >= 16 || nk > 32))
     while (S < 4 && tiles * S * 2 <= 512 && nk >= 4 * S) S *= 2;
-  f32x4 *wsp = nullptr;
-  uint32_t *cnt = nullptr;
-  if (S > 1) {
-    int rc = RQ_OK;
-    cnt = ws->counters();
-    wsp = cnt ? static_cast<f32x4 *>(ws->get((size_t)tiles * S * MT * 64 * sizeof(f32x4), &rc, true)) : nullptr;
-    if (!wsp) S = 1;
-  }
-  const int64_t cps = (nk + S - 1) / S;
-  const int xstr = (int)(cps * 64 * 4 + 16);
-  const size_t xbytes = (size_t)m * (size_t)xstr;
-  const bool xl = m >= 16 && cps * 64 <= 2048 && xbytes <= kSmXsMax;
-  if (xl) {
-    const int rc = codes_launch<C, MT, 8, 1, true>(w, count, set, x, m, o, S, wsp, cnt, s, xstr, xbytes);
-    if (rc != RQ_E_UNSUPPORTED) return rc;
-  }
-  return codes_launch<C, MT, 8, 1, false>(w, count, set, x, m, o, S, wsp, cnt, s, 0, 0);
+  const int rt = tiles * S >= 256 ? 2 : 1;
+  if (rt == 2) return codes_go<C, MT, 2>(w, count, set, x, m, o, s, ws, S);
+  return codes_go<C, MT, 1>(w, count, set, x, m, o, s, ws, S);
 }
 
 template <class C>

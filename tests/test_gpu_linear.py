@@ -223,14 +223,17 @@ def test_small_m_f32_activations(dev, qtype, m, n, k):
 # longer than 2048) take the integer codes on the bf16 matrix cores (128 + q,
 # or the int8 code, exact in bf16) against two bf16 limbs of x, the scales
 # applied per run of 16 or 32 weights to the f32 sums.  x spans six decades
-# (every 7th element x300, every 11th x1e-3); few row tiles on long rows split
+# (every 7th element x300, every 11th x1e-3); launches of 256 or more row
+# tiles take two a workgroup (4864 rows, and 4100 = 256.25 tiles: a last
+# workgroup with one); few row tiles on long rows split
 # K over up to four workgroups (7 x 4096, 16 x 4096, 24 x 8192), the
 # activation slice is staged in LDS (16 x 896, 16 x 4096 in four slices,
 # 17 x 4864) or read from memory (m < 16, 16 x 8192, 31 x 4096), rows straddle
 # blocks (k = 896 for the 256-element formats), and m, n end in partial tiles.
 @pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0])
 @pytest.mark.parametrize("m,n,k", [(4, 4864, 896), (7, 100, 4096), (16, 896, 896), (16, 64, 4096),
-                                   (16, 64, 8192), (17, 896, 4864), (31, 200, 4096), (24, 40, 8192)])
+                                   (16, 64, 8192), (17, 896, 4864), (31, 200, 4096), (24, 40, 8192),
+                                   (31, 4100, 4096)])
 def test_small_m_f32_codes(dev, qtype, m, n, k):
     print(f"codes qtype={qtype} m={m} n={n} k={k}", flush=True)
     w, wf = make(qtype, n, k, 41 + m + n + k)
