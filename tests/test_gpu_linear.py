@@ -271,6 +271,29 @@ def test_f32_activations_sliced(dev, qtype, m, n, k):
         assert norm_err(y, ref(x.numpy(), wf)) <= tol
 
 
+# f32 activations with m > 64 on the two-limb tiles, row by row: rows of very
+# different magnitudes (1e-30, 1e-3, 1e20), a row of zeros, x spanning six
+# decades inside rows; 64 x 64 tiles in K-groups (k = 2048, 896, 256),
+# 128 x 128 tiles (512 x 4096) and K split four ways (k = 8192).
+@pytest.mark.parametrize("m,n,k", [(96, 512, 2048), (200, 300, 896), (130, 2048, 8192), (65, 8192, 256),
+                                   (512, 4096, 512)])
+def test_f32_prefill_row_magnitudes(dev, m, n, k):
+    print(f"f32 prefill rows m={m} n={n} k={k}", flush=True)
+    w, wf = make(rq.Q4_K, n, k, 61 + m)
+    x = synth.activations(62 + m, m, k)
+    x[:, ::7] *= 300.0
+    x[:, 3::11] *= 1e-3
+    x[1] *= 1e-30
+    x[2] *= 1e20
+    x[3] = 0.0
+    x[4] *= 1e-3
+    r = ref(x, wf)
+    y = w.forward(torch.from_numpy(x).to(dev)).cpu().numpy()
+    assert np.all(y[3] == 0.0)
+    for i in [i for i in range(m) if i != 3]:
+        assert norm_err(y[i:i + 1], r[i:i + 1]) <= TOL_F32, i
+
+
 @pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0])
 @pytest.mark.parametrize("m", [3, 33])
 def test_small_m_f16_activations(dev, qtype, m):
