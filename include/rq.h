@@ -214,7 +214,8 @@ int rq_linear_bias(const rq_weight *w, const void *x, int xtype, int64_t m, int6
  * format whose rows hold at most 64 pieces (k <= 2048 for Q4_K / Q5_K /
  * Q8_0 / Q4_0 / Q5_0, k <= 4096 for Q6_K) take one launch, and so do bf16 activations
  * with 3 <= m <= 64 and f32 activations with 4 <= m <= 64 (the small-M
- * matrix-core kernel; f32 on two bf16 limbs per operand); other weights
+ * matrix-core kernels; f32 as two bf16 limbs per activation, against the
+ * weights' integer codes for Q4_K / Q6_K / Q8_0 at m <= 16); other weights
  * take the launches rq_linear_bias would make.  At m <= 2 each output equals
  * that call's output bit for bit; in the small-M sets the K split (and, for
  * f32, the kernel) can differ from a single weight's, so sums can differ in
