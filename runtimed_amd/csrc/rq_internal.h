@@ -272,11 +272,11 @@ int launch_linear_smallm_set(const rq_weight *const *w, int count, const void *x
 // weights (f32 accumulation).
 int launch_linear_smallm_f32(const rq_weight *wt, const void *x, int xtype, int64_t m, const Out &o,
                              hipStream_t s, WsLease *ws);
-// f32 activations, 4 <= m <= 16 (17..32 on rows longer than 2048), Q4_K /
-// Q6_K / Q8_0: the integer codes on the bf16 matrix cores against two bf16
-// limbs of x, the scales applied per run to the f32 sums; one weight (set
-// false) or a set of count weights of one format and k sharing x.
-// RQ_E_UNSUPPORTED for other formats / shapes.
+// f32 activations, 4 <= m <= 16 (and 17..64 rows on the launches its plan
+// names), Q4_K / Q6_K / Q8_0: the integer codes on the bf16 matrix cores
+// against two bf16 limbs of x, the scales applied per run to the f32 sums;
+// one weight (set false) or a set of count weights of one format and k
+// sharing x.  RQ_E_UNSUPPORTED for other formats / shapes.
 int launch_linear_smallm_codes(const rq_weight *const *w, int count, bool set, const void *x, int64_t m,
                                const Out *o, hipStream_t s, WsLease *ws);
 // 64 * slices f32 / f16 activation rows as slices of 64 rows in one launch.

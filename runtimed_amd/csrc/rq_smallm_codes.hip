@@ -502,13 +502,15 @@ int codes_launch(const rq_weight *const *w, int count, bool set, const float *x,
 //           down 9.3 -> 7.5, gate 6.8 -> 4.7
 //   M = 16: gate/up set 10.7 -> 7.7, q/k/v set 5.5 -> 4.2, o 4.9 -> 3.9,
 //           down 10.2 -> 8.6, gate 7.1 -> 5.2
-//   M = 32: down 16.7 -> 10.9, but gate/up set 11.6 -> 13.5, o 5.0 -> 5.6
-//   M = 64: gate/up set 27.7 -> 23.2, but o 5.1 -> 9.9, gate 13.8 -> 16.9
-// (M = 32 / 64 with one row tile and the epilogue of one wave.)  Four waves
-// with batches of two or four chunks, sixteen waves and other K splits were
-// slower; two row tiles on the 56- and 72-tile launches lost 10-25%.  So this
-// kernel takes 4 <= m <= 16, and 17..32 rows on rows longer than 2048
-// elements; the rest stay on the other kernels.
+//   M = 32: down 16.9 -> 10.9, gate 9.5 -> 7.0, q/k/v set 7.3 -> 5.8, gate/up
+//           set 11.8 -> 12.1, but o 4.8 -> 5.6
+//   M = 64: gate/up set 27.5 -> 22.9, gate 13.7 -> 12.6, but o 5.0 -> 10.2,
+//           q/k/v set 9.8 -> 10.5, down 15.0 -> 15.3
+// Four waves with batches of two or four chunks, sixteen waves and other K
+// splits were slower; two row tiles on the 56- and 72-tile launches lost
+// 10-25%.  So this kernel takes 4 <= m <= 16; 17..32 rows on rows longer
+// than 2048 elements, on 256 or more row tiles and for sets; 33..64 rows on
+// 256 or more row tiles; the rest stay on the other kernels.
 template <class C, int MT, int RT>
 int codes_go(const rq_weight *const *w, int count, bool set, const float *x, int64_t m, const Out *o, hipStream_t s,
              WsLease *ws, int S) {
@@ -553,16 +555,19 @@ template <class C>
 int codes_run(const rq_weight *const *w, int count, bool set, const float *x, int64_t m, const Out *o, hipStream_t s,
               WsLease *ws) {
   if (m <= 16) return codes_plan<C, 1>(w, count, set, x, m, o, s, ws);
-  if (m <= 32 && w[0]->k > 2048) return codes_plan<C, 2>(w, count, set, x, m, o, s, ws);
+  int64_t tiles = 0;
+  for (int j = 0; j < count; ++j) tiles += (w[j]->n + 15) / 16;
+  if (m <= 32 && (w[0]->k > 2048 || tiles >= 256 || set)) return codes_plan<C, 2>(w, count, set, x, m, o, s, ws);
+  if (m > 32 && tiles >= 256) return codes_plan<C, 4>(w, count, set, x, m, o, s, ws);
   return RQ_E_UNSUPPORTED;
 }
 
 }  // namespace
 
-// f32 activations, 4 <= m <= 16 (or up to 32 on rows longer than 2048),
-// k % 64 == 0, 16-byte aligned x, one weight or a set of one format and k:
-// Q4_K, Q6_K and Q8_0 (RQ_E_UNSUPPORTED otherwise: the two-limb or f32
-// kernels take those).
+// f32 activations, 4 <= m <= 64 where the plan above takes them, k % 64 ==
+// 0, 16-byte aligned x, one weight or a set of one format and k: Q4_K, Q6_K
+// and Q8_0 (RQ_E_UNSUPPORTED otherwise: the two-limb or f32 kernels take
+// those).
 int launch_linear_smallm_codes(const rq_weight *const *w, int count, bool set, const void *x, int64_t m,
                                const Out *o, hipStream_t s, WsLease *ws) {
   const int64_t k = w[0]->k;

@@ -220,7 +220,9 @@ def test_small_m_f32_activations(dev, qtype, m, n, k):
 
 
 # f32 activations with 4 <= M <= 16 on Q4_K / Q6_K / Q8_0 (17..32 rows on rows
-# longer than 2048) take the integer codes on the bf16 matrix cores (128 + q,
+# longer than 2048, on 256 or more row tiles and in sets; 33..64 rows on 256 or
+# more row tiles: 40 x 4100, 64 x 4864; 20 x 300 only as the set below) take
+# the integer codes on the bf16 matrix cores (128 + q,
 # or the int8 code, exact in bf16) against two bf16 limbs of x, the scales
 # applied per run of 16 or 32 weights to the f32 sums.  x spans six decades
 # (every 7th element x300, every 11th x1e-3); launches of 256 or more row
@@ -233,7 +235,7 @@ def test_small_m_f32_activations(dev, qtype, m, n, k):
 @pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0])
 @pytest.mark.parametrize("m,n,k", [(4, 4864, 896), (7, 100, 4096), (16, 896, 896), (16, 64, 4096),
                                    (16, 64, 8192), (17, 896, 4864), (31, 200, 4096), (24, 40, 8192),
-                                   (31, 4100, 4096)])
+                                   (31, 4100, 4096), (20, 300, 896), (40, 4100, 1024), (64, 4864, 896)])
 def test_small_m_f32_codes(dev, qtype, m, n, k):
     print(f"codes qtype={qtype} m={m} n={n} k={k}", flush=True)
     w, wf = make(qtype, n, k, 41 + m + n + k)
