@@ -195,18 +195,18 @@ __device__ __forceinline__ void store_tile32(const rq_f32x16 &acc, const Out &o,
 // leaves as whole rows: 32 lanes x 16 bytes per row, two rows per wave
 // instruction.
 
-// A wave's 128 x 128 block (4 x 4 MFMA tiles of 32 x 32, rows rb.., columns
-// cb.. of the staged tile) into T; values scaled by sx * sw when SCALED,
+// A wave's MI x NI block of 32 x 32 MFMA tiles (rows rb.., columns cb.. of
+// the staged tile) into T; values scaled by sx * sw when SCALED,
 // plus the biases bb (rounded as tile_col_bias leaves them; 0 without one).
 // twice: a bias is present, so each value is rounded to y's type before its
 // bias is added (with_bias).
-template <bool SCALED>
-__device__ __forceinline__ void stage_block_2b(const rq_f32x16 (&acc)[4][4], uint8_t *T, int rb, int cb, int ytype,
-                                               const float (&sx)[4][4], const float (&sw)[4][4],
-                                               const float (&bb)[4][4], bool twice, int lane) {
+template <bool SCALED, int MI, int NI>
+__device__ __forceinline__ void stage_block_2b(const rq_f32x16 (&acc)[MI][NI], uint8_t *T, int rb, int cb, int ytype,
+                                               const float (&sx)[MI][4], const float (&sw)[NI][4],
+                                               const float (&bb)[NI][4], bool twice, int lane) {
   const int h = lane >> 5, t = lane & 3;
-  static_for<4>([&](auto I) {
-    static_for<4>([&](auto J) {
+  static_for<MI>([&](auto I) {
+    static_for<NI>([&](auto J) {
       static_for<4>([&](auto G) {
         constexpr int g = decltype(G)::value;
         const rq_f32x16 &a = acc[I][J];
@@ -240,14 +240,15 @@ __device__ __forceinline__ void stage_block_2b(const rq_f32x16 (&acc)[4][4], uin
 }
 
 // The staged tile to y[m0 .. m0 + 256, n0 .. n0 + 256) (2-byte elements, row
-// stride n), 256 threads.
+// stride n), NTH threads (256 or 512).
+template <int NTH = 256>
 __device__ __forceinline__ void store_staged_2b(const uint8_t *T, void *y, int64_t n, int64_t m0, int64_t n0,
                                                 int tid) {
   const int c = tid & 31;
   uint8_t *base = static_cast<uint8_t *>(y) + (m0 * n + n0) * 2 + 16 * c;
 #pragma unroll 4
-  for (int i = 0; i < 32; ++i) {
-    const int r = 8 * i + (tid >> 5);
+  for (int i = 0; i < 256 / (NTH / 32); ++i) {
+    const int r = (NTH / 32) * i + (tid >> 5);
     const uint4 v = *reinterpret_cast<const uint4 *>(T + r * 512 + ((c ^ (4 * (r & 3))) << 4));
     *reinterpret_cast<uint4 *>(base + (int64_t)r * n * 2) = v;
   }

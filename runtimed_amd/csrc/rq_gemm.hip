@@ -509,7 +509,7 @@ __global__ __launch_bounds__(256) void k_qgemm_pipe(const uint8_t *__restrict__ 
 // load instructions and quant bytes of the per-chunk pieces, and a quarter
 // of the decode work per step instead of half of it on every other step.
 // Pairs alternate between two register slots, so the loop is unrolled by
-// eight steps (k % 256 == 0); everything else is k_qgemm_pipe's.
+// eight steps (k % 256 == 0).
 struct Q6Pair {
   u32x4 a, b, h;
   uint32_t sc0, sc1;  // the half's int8 scales: bytes 0..3 (chunk 2j), 4..7 (chunk 2j + 1)
@@ -553,56 +553,109 @@ __device__ __forceinline__ void q6_pair_run(const Q6Pair &p, int hh, uint32_t (&
   }
 }
 
-// LDS addresses as base registers plus compile-time offsets: stage st of a
-// base sits at (st % 2) * 32768 from it, and the bases of stages 2 and 3 are
-// 65536 above those of 0 and 1 (the offset field holds 16 bits).  Each base
-// folds the lane's row and its swizzled chunk, which do not change between
-// tiles 32 rows apart: (r >> 2) & 3 depends on r % 32 only.
-struct PipeBases {
-  uint32_t rd[2][2][2];  // [stages 2-3][pass H][A, B]: fragment reads
-  uint32_t wa[2];        // [stages 2-3]: activation writes
-  uint32_t wr[2][2];     // [stages 2-3][16-byte chunk q]: weight-run writes
+// Q6_K in chunk pairs on eight waves (two a SIMD): a 256 x 256 output tile,
+// each wave 128 (M) x 64 (N) of it (4 x 2 MFMA tiles of 32 x 32, 128
+// accumulators), so that a SIMD interleaves two waves' decode and MFMAs.  A
+// single wave a SIMD issues VALU instructions at about half the SIMD's rate
+// (a probe of 28 independent FMAs per four 32x32x16 MFMAs: one wave 128-138
+// ns an iteration against 72-77 for the MFMAs alone; two waves, twice the
+// work, 163-168 ns), and the decode costs about six VALU instructions per
+// MFMA.  Each thread decodes one weight row a step (row t / 2, piece t % 2)
+// and loads two 16-byte activation chunks; the tile rows' activations of
+// step s + 4 are loaded during step s, the chunk pair of steps 4j .. 4j + 3
+// during step 4j - 7, and both are written into LDS stage (s + 2) % 4 during
+// step s.  Four stages, one barrier a step, LDS rows of 64 bytes with the
+// 16-byte chunk index XOR-ed with (row / 4) % 4.  Workgroups take tiles
+// XCD by XCD (XCD x the x-th eighth of the tiles, M fastest) so that the
+// workgroups sharing a weight tile share an L2.
+struct Pass8 {
+  u32x4 x[6];  // A of tiles 0..3, then B of tiles 0..1
 };
 
-// The 16 MFMAs of one pass on `cur`, reading pass H of stage ST into `nxt`
-// (as mfma_pass).
-template <int ST, int H>
-__device__ __forceinline__ void mfma_pass_o(const Pass &cur, Pass &nxt, const PipeBases &pb, f32x16 (&acc)[4][4]) {
+__device__ __forceinline__ void wait_pass8(Pass8 &P) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(P.x[0]), "+v"(P.x[1]), "+v"(P.x[2]));
+  asm volatile("" : "+v"(P.x[3]), "+v"(P.x[4]), "+v"(P.x[5]));
+}
+
+// q6_pair_run in pieces, to be placed between MFMAs: the run's scale, then
+// words 2J, 2J + 1 (part J < 4).  Same arithmetic, same bits.
+struct RunScale {
+  float ds, z;
+};
+
+template <int CC, int RR>
+__device__ __forceinline__ RunScale q6_run_scale(const Q6Pair &p, int hh) {
+  const float d = h2f(p.d);
+  const uint32_t scw = CC ? p.sc1 : p.sc0;
+  const float ds = d * (float)(int8_t)((scw >> (8 * (2 * RR + hh))) & 0xFFu);
+  return {ds, -32.0f * ds};
+}
+
+template <int CC, int RR, int J>
+__device__ __forceinline__ void q6_run_part(const Q6Pair &p, const RunScale &sc, uint32_t (&o)[8]) {
+  const uint32_t src = RR ? p.b[J] : p.a[J];
+  const uint32_t hb = p.h[J] >> (4 * CC);
+  const uint32_t q = opaque(((src >> (4 * CC)) & 0x0F0F0F0Fu) |
+                            (RR ? ((hb & 0x0C0C0C0Cu) << 2) : ((hb & 0x03030303u) << 4)));
+  o[2 * J] = pk_bf16(fmaf(ub(q, 0), sc.ds, sc.z), fmaf(ub(q, 1), sc.ds, sc.z));
+  o[2 * J + 1] = pk_bf16(fmaf(ub(q, 2), sc.ds, sc.z), fmaf(ub(q, 3), sc.ds, sc.z));
+  asm volatile("" : "+v"(o[2 * J]), "+v"(o[2 * J + 1]));  // computed here, not next to its use
+}
+
+// LDS of the eight-wave kernel: the A (activation) parts of the four stages
+// side by side (16 KB each), then the four B (weight-run) parts, so one base
+// register per role reaches every stage through the 16-bit offset field.
+constexpr int P8_A = 16384, P8_B = 65536;
+
+struct PipeBases8 {
+  uint32_t rd[2][2];  // [pass H][A, B]: fragment reads
+  uint32_t wa;        // activation writes
+  uint32_t wr[2];     // [16-byte chunk q]: weight-run writes
+};
+
+// The 8 MFMAs of one pass on `cur`, reading pass H of stage ST into `nxt`
+// (one read after each of the first six) and running hook(f) after MFMA f:
+// the order is fixed (nothing is moved across the scheduling barriers), so
+// the hook's VALU work issues while the MFMAs before it run.
+template <int ST, int H, class Hook>
+__device__ __forceinline__ void mfma_pass8(const Pass8 &cur, Pass8 &nxt, const PipeBases8 &pb, f32x16 (&acc)[4][2],
+                                           Hook &&hook) {
   static_for<4>([&](auto I) {
-    static_for<4>([&](auto J) {
+    static_for<2>([&](auto J) {
       acc[I][J] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16(cur.x[I]), as_bf16(cur.x[4 + J]), acc[I][J], 0, 0,
                                                           0);
-      if constexpr (J == 0 || J == 2) {
-        constexpr int f = 2 * decltype(I)::value + J / 2;
-        __builtin_amdgcn_sched_barrier(0x6);  // VALU / SALU may cross
-        nxt.x[f] = ds_read16_off<(ST & 1) * P_STAGE + 2048 * (f & 3)>(pb.rd[ST >> 1][H][f >> 2]);
-        __builtin_amdgcn_sched_barrier(0x6);
-      }
+      constexpr int f = 2 * decltype(I)::value + decltype(J)::value;
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (f < 6) nxt.x[f] = ds_read16_off<ST * P8_A + 2048 * (f < 4 ? f : f - 4)>(pb.rd[H][f < 4 ? 0 : 1]);
+      hook(std::integral_constant<int, f>{});
+      __builtin_amdgcn_sched_barrier(0);
     });
   });
 }
 
 template <int ST>
-__device__ __forceinline__ void write_a_o(const PipeBases &pb, const u32x4 (&a)[4]) {
-  static_for<4>([&](auto J) {
-    ds_write16_off<(ST & 1) * P_STAGE + 1024 * decltype(J)::value>(pb.wa[ST >> 1], a[J]);
-  });
+__device__ __forceinline__ void write_a8(const PipeBases8 &pb, const u32x4 (&a)[2]) {
+  ds_write16_off<ST * P8_A>(pb.wa, a[0]);
+  ds_write16_off<ST * P8_A + 1024>(pb.wa, a[1]);
 }
 
-// Run words of weight row br (R = 0) or br + 128 (R = 1) into stage ST.
-template <int ST, int R>
-__device__ __forceinline__ void write_run_o(const PipeBases &pb, const uint32_t (&o)[8]) {
-  ds_write16_off<(ST & 1) * P_STAGE + 8192 * R>(pb.wr[ST >> 1][0], (u32x4){o[0], o[1], o[2], o[3]});
-  ds_write16_off<(ST & 1) * P_STAGE + 8192 * R>(pb.wr[ST >> 1][1], (u32x4){o[4], o[5], o[6], o[7]});
+template <int ST>
+__device__ __forceinline__ void write_run8(const PipeBases8 &pb, const uint32_t (&o)[8]) {
+  ds_write16_off<ST * P8_A>(pb.wr[0], (u32x4){o[0], o[1], o[2], o[3]});
+  ds_write16_off<ST * P8_A>(pb.wr[1], (u32x4){o[4], o[5], o[6], o[7]});
 }
 
-__global__ __launch_bounds__(256) void k_q6_pipe(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
-                                                 const uint16_t *__restrict__ x, int64_t m, int64_t n, int64_t k,
-                                                 const Out o) {
+__device__ __forceinline__ void load_a8(const uint8_t *const (&src)[2], int64_t s, u32x4 (&a)[2]) {
+  a[0] = *reinterpret_cast<const u32x4 *>(src[0] + 64 * s);
+  a[1] = *reinterpret_cast<const u32x4 *>(src[1] + 64 * s);
+}
+
+__global__ __launch_bounds__(512) void k_q6_pipe8(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
+                                                  const uint16_t *__restrict__ x, int64_t m, int64_t n, int64_t k,
+                                                  const Out o) {
   __shared__ __attribute__((aligned(1024))) uint8_t SM[4 * P_STAGE];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  // tile order as in k_qgemm_pipe (XCD x takes the x-th eighth, M fastest)
+  const int wm = wave >> 2, wn = wave & 3;
   const int64_t gm = gridDim.y, tiles = (int64_t)gridDim.x * gridDim.y;
   const int64_t b = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
   const int64_t lin = tiles % 8 == 0 ? (b % 8) * (tiles / 8) + b / 8 : b;
@@ -610,80 +663,69 @@ __global__ __launch_bounds__(256) void k_q6_pipe(const uint8_t *__restrict__ w, 
   const int64_t nk = k / 32, np = nk / 4;  // K-steps, chunk pairs
   const int last = (int)nk - 1;
 
-  const uint8_t *asrc[4];
+  // Activation rows 32 wave + 16 j + lane / 4 (j < 2), chunk lane % 4.
+  const uint8_t *asrc[2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t gr = m0 + 64 * wave + 16 * j + (lane >> 2);
+  for (int j = 0; j < 2; ++j) {
+    const int64_t gr = m0 + 32 * wave + 16 * j + (lane >> 2);
     asrc[j] = reinterpret_cast<const uint8_t *>(x + (gr < m ? gr : m - 1) * k) + 16 * (lane & 3);
   }
   const int hh = tid & 1, br = tid >> 1;
   const uint64_t rk0 = (uint64_t)(n0 + br < n ? n0 + br : n - 1) * (uint64_t)k;
-  const uint64_t rk1 = (uint64_t)(n0 + br + 128 < n ? n0 + br + 128 : n - 1) * (uint64_t)k;
 
-  PipeBases pb;
+  PipeBases8 pb;
   {
-    const uint32_t s0 = lds_addr(SM);
+    const uint32_t sa = lds_addr(SM), sb = sa + P8_B;
     const int l = lane & 31, g = lane >> 5, sw = (l >> 2) & 3;
-    const int ra_ = lane >> 2, swa = (lane >> 4) & 3;
 #pragma unroll
-    for (int hi = 0; hi < 2; ++hi) {
-      const uint32_t sb = s0 + 65536u * hi;
-#pragma unroll
-      for (int H = 0; H < 2; ++H) {
-        pb.rd[hi][H][0] = sb + 8192 * wm + 64 * l + 16 * ((2 * g + H) ^ sw);
-        pb.rd[hi][H][1] = sb + P_B + 8192 * wn + 64 * l + 16 * ((2 * g + H) ^ sw);
-      }
-      pb.wa[hi] = sb + 4096 * wave + 64 * ra_ + 16 * ((lane & 3) ^ swa);
-#pragma unroll
-      for (int q = 0; q < 2; ++q) pb.wr[hi][q] = sb + P_B + 64 * br + 16 * ((2 * hh + q) ^ swz(br));
+    for (int H = 0; H < 2; ++H) {
+      pb.rd[H][0] = sa + 8192 * wm + 64 * l + 16 * ((2 * g + H) ^ sw);
+      pb.rd[H][1] = sb + 4096 * wn + 64 * l + 16 * ((2 * g + H) ^ sw);
     }
+    pb.wa = sa + 2048 * wave + 64 * (lane >> 2) + 16 * ((lane & 3) ^ ((lane >> 4) & 3));
+#pragma unroll
+    for (int q = 0; q < 2; ++q) pb.wr[q] = sb + 64 * br + 16 * ((2 * hh + q) ^ swz(br));
   }
 
-  f32x16 acc[4][4];
+  f32x16 acc[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = (f32x16){0};
+    for (int j = 0; j < 2; ++j) acc[i][j] = (f32x16){0};
 
-  // Prologue: stages 0 and 1 (chunk 0 of pair 0) written, pairs 0 and 1 in
+  // Prologue: stages 0 and 1 written (chunk 0 of pair 0), pairs 0 and 1 in
   // slots 0 and 1, activations of steps 2 and 3 in flight, pass 0 of step 0
   // read.
-  u32x4 ra[2][4];
-  Q6Pair pp[2][2];  // [slot][row]
+  u32x4 ra[2][2];
+  Q6Pair pp[2];  // [slot]
   {
-    u32x4 a0[4], a1[4];
-    load_a(asrc, 0, a0);
-    load_a(asrc, 1, a1);
-    pp[0][0] = load_q6_pair(w, aux, rk0, 0, hh);
-    pp[0][1] = load_q6_pair(w, aux, rk1, 0, hh);
-    load_a(asrc, 2 < nk ? 2 : last, ra[0]);
-    load_a(asrc, 3 < nk ? 3 : last, ra[1]);
-    const int64_t p1 = np > 1 ? 1 : 0;
-    pp[1][0] = load_q6_pair(w, aux, rk0, p1, hh);
-    pp[1][1] = load_q6_pair(w, aux, rk1, p1, hh);
-    write_a_o<0>(pb, a0);
-    write_a_o<1>(pb, a1);
+    u32x4 a0[2], a1[2];
+    load_a8(asrc, 0, a0);
+    load_a8(asrc, 1, a1);
+    pp[0] = load_q6_pair(w, aux, rk0, 0, hh);
+    load_a8(asrc, 2 < nk ? 2 : last, ra[0]);
+    load_a8(asrc, 3 < nk ? 3 : last, ra[1]);
+    pp[1] = load_q6_pair(w, aux, rk0, np > 1 ? 1 : 0, hh);
+    write_a8<0>(pb, a0);
+    write_a8<1>(pb, a1);
     uint32_t o[8];
-    q6_pair_run<0, 0>(pp[0][0], hh, o);
-    write_run_o<0, 0>(pb, o);
-    q6_pair_run<0, 0>(pp[0][1], hh, o);
-    write_run_o<0, 1>(pb, o);
-    q6_pair_run<0, 1>(pp[0][0], hh, o);
-    write_run_o<1, 0>(pb, o);
-    q6_pair_run<0, 1>(pp[0][1], hh, o);
-    write_run_o<1, 1>(pb, o);
+    q6_pair_run<0, 0>(pp[0], hh, o);
+    write_run8<0>(pb, o);
+    q6_pair_run<0, 1>(pp[0], hh, o);
+    write_run8<1>(pb, o);
   }
   wait_lds_all();
   __builtin_amdgcn_s_barrier();
-  Pass P0, P1;
-  static_for<8>([&](auto F) {
+  Pass8 P0, P1;
+  static_for<6>([&](auto F) {
     constexpr int f = decltype(F)::value;
-    P0.x[f] = ds_read16_off<2048 * (f & 3)>(pb.rd[0][0][f >> 2]);
+    P0.x[f] = ds_read16_off<2048 * (f < 4 ? f : f - 4)>(pb.rd[0][f < 4 ? 0 : 1]);
   });
-  wait_pass(P0);
+  wait_pass8(P0);
 
-  // Step s = 8u + B: the run of step s + 2 (pair (s + 2) / 4, chunk
-  // ((s + 2) / 2) % 2, run (s + 2) % 2) from slot ((B + 2) / 4) % 2; slot 0
+  // Step s = 8u + B: pass 1 of stage s % 4, pass 0 of stage (s + 1) % 4, and
+  // the run of step s + 2 (pair (s + 2) / 4, chunk ((s + 2) / 2) % 2, run
+  // (s + 2) % 2) from slot ((B + 2) / 4) % 2 into stage (s + 2) % 4; slot 0
   // is free after step 8u + 1 and takes pair 2u + 2, slot 1 after 8u + 5 and
   // takes pair 2u + 3.
   auto step = [&](int64_t s, auto Bc) {
@@ -691,22 +733,26 @@ __global__ __launch_bounds__(256) void k_q6_pipe(const uint8_t *__restrict__ w, 
     constexpr int T = (B + 2) & 7, CC = (T >> 1) & 1, RR = T & 1, SLOT = ((B + 2) >> 2) & 1;
     constexpr int ST = B & 3, ST1 = (B + 1) & 3, ST2 = (B + 2) & 3;
     __builtin_amdgcn_s_barrier();
-    uint32_t o0[8], o1[8];
-    q6_pair_run<CC, RR>(pp[SLOT][0], hh, o0);
-    q6_pair_run<CC, RR>(pp[SLOT][1], hh, o1);
-    mfma_pass_o<ST, 1>(P0, P1, pb, acc);
-    wait_pass(P1);
-    mfma_pass_o<ST1, 0>(P1, P0, pb, acc);
-    write_a_o<ST2>(pb, ra[B & 1]);
-    load_a(asrc, s + 4 < nk ? s + 4 : last, ra[B & 1]);
-    write_run_o<ST2, 0>(pb, o0);
-    write_run_o<ST2, 1>(pb, o1);
+    // stage (s + 2) % 4 was last read in steps s - 3 and s - 2: its activation
+    // part is written first, the decoded run (during the first pass) early in
+    // the second, so that no write is left to complete at the end of the step
+    write_a8<ST2>(pb, ra[B & 1]);
+    load_a8(asrc, s + 4 < nk ? s + 4 : last, ra[B & 1]);
+    uint32_t o0[8];
+    const RunScale sc = q6_run_scale<CC, RR>(pp[SLOT], hh);
+    mfma_pass8<ST, 1>(P0, P1, pb, acc, [&](auto F) {
+      constexpr int f = decltype(F)::value;
+      if constexpr (f & 1) q6_run_part<CC, RR, f / 2>(pp[SLOT], sc, o0);
+    });
+    wait_pass8(P1);
+    mfma_pass8<ST1, 0>(P1, P0, pb, acc, [&](auto F) {
+      if constexpr (decltype(F)::value == 0) write_run8<ST2>(pb, o0);
+    });
     if constexpr (B == 1 || B == 5) {
       const int64_t jn = (s + 7) >> 2 < np ? (s + 7) >> 2 : np - 1;
-      pp[B == 1 ? 0 : 1][0] = load_q6_pair(w, aux, rk0, jn, hh);
-      pp[B == 1 ? 0 : 1][1] = load_q6_pair(w, aux, rk1, jn, hh);
+      pp[B == 1 ? 0 : 1] = load_q6_pair(w, aux, rk0, jn, hh);
     }
-    wait_pass(P0);
+    wait_pass8(P0);
     wait_lds_all();
   };
   for (int64_t t = 0; t < nk; t += 8) {
@@ -719,7 +765,28 @@ __global__ __launch_bounds__(256) void k_q6_pipe(const uint8_t *__restrict__ w, 
     step(t + 6, std::integral_constant<int, 6>{});
     step(t + 7, std::integral_constant<int, 7>{});
   }
-  pipe_store(acc, SM, o, m, n, m0, n0, wm, wn, lane, tid);
+
+  // The tile to y: 16-bit outputs of whole tiles staged in LDS (the four
+  // stages, free after the loop), other tiles straight from the accumulators.
+  const bool vec = vec_stores_ok(o.y, n);
+  float bb[2][4];  // biases, loaded before the first store
+#pragma unroll
+  for (int j = 0; j < 2; ++j) tile_col_bias(o, n, n0 + 64 * wn + j * 32, lane, bb[j]);
+  if (o.ytype != RQ_F32 && vec && n % 8 == 0 && m0 + 256 <= m && n0 + 256 <= n) {
+    __syncthreads();  // every wave's stage reads are done
+    const float unused_x[4][4] = {}, unused_w[2][4] = {};  // scales: none (SCALED false)
+    stage_block_2b<false>(acc, SM, 128 * wm, 64 * wn, o.ytype, unused_x, unused_w, bb, o.bias != nullptr, lane);
+    __syncthreads();
+    store_staged_2b<512>(SM, o.y, n, m0, n0, tid);
+    return;
+  }
+  const float one[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  static_for<4>([&](auto I) {
+    static_for<2>([&](auto J) {
+      store_tile32<false>(acc[I][J], o, m, n, m0 + 128 * wm + I * 32, n0 + 64 * wn + J * 32, one, one, bb[J],
+                          nullptr, nullptr, lane, vec);
+    });
+  });
 }
 
 // y = sum over s < splits of part[s] (f32 partials of m * n outputs), with
@@ -821,7 +888,7 @@ template <class F>
 int launch_pipe(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s) {
   const dim3 grid((unsigned)((wt->n + 255) / 256), (unsigned)((m + 255) / 256));
   if (std::is_same<F, FmtQ6KG>::value && wt->k % 256 == 0)
-    hipLaunchKernelGGL(k_q6_pipe, grid, dim3(256), 0, s, wt->data, wt->data + wt->aux_off,
+    hipLaunchKernelGGL(k_q6_pipe8, grid, dim3(512), 0, s, wt->data, wt->data + wt->aux_off,
                        static_cast<const uint16_t *>(x), m, wt->n, wt->k, o);
   else
     hipLaunchKernelGGL((k_qgemm_pipe<F>), grid, dim3(256), 0, s, wt->data, wt->data + wt->aux_off,

@@ -35,7 +35,7 @@ def bias_vec(n, seed, dtype, dev):
 
 # Every kernel family of the fused path: segment / team / long-row /
 # matrix-core GEMVs (M = 1, 2), the small-M matrix-core kernels (bf16 and f32), the tiled GEMM
-# with and without split K, the pipelined 256 x 256 kernel, the f32 slices,
+# with and without split K, the pipelined 256 x 256 kernels, the f32 slices,
 # and the generic kernel (k % 64 != 0).
 ROUTES = [
     # (qtype, n, k, m, xdtype)
@@ -52,6 +52,7 @@ ROUTES = [
     (rq.Q4_K, 1024, 2048, 300, torch.bfloat16),  # tiled GEMM
     (rq.Q6_K, 256, 8192, 300, torch.bfloat16),  # split K
     (rq.Q4_K, 32768, 256, 512, torch.bfloat16),  # pipelined 256 x 256
+    (rq.Q6_K, 32768, 256, 512, torch.bfloat16),  # pipelined 256 x 256, eight waves (Q6_K chunk pairs)
     (rq.Q8_0, 130, 256, 131, torch.float32),    # f32 slices with a 3-row tail
     (rq.Q4_K, 8, 160, 5, torch.float32),        # generic (rows cut mid-chunk)
 ]

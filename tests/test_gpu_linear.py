@@ -399,6 +399,8 @@ def test_mfma_gemm_edge_tiles(dev, qtype, m, n, k):
     (rq.Q4_K, 512, 32768, 64),
     (rq.Q6_K, 512, 32768, 448),
     (rq.Q6_K, 768, 32768, 256),  # pipelined kernel, three M tiles per weight tile in the XCD-aware order
+    (rq.Q6_K, 300, 32868, 512),  # pipelined Q6_K, ragged rows and columns (accumulator stores)
+    (rq.Q6_K, 512, 32776, 1024),  # pipelined Q6_K, ragged last column tile, whole tiles staged
 ])
 def test_large_gemm(dev, qtype, m, n, k):
     w, wf = make(qtype, n, k, 5 + m + k)
