@@ -438,6 +438,170 @@ __global__ __launch_bounds__(256) void k_fp8_gemm_pipe(const uint8_t *__restrict
   });
 }
 
+// ---- the same with eight waves (two a SIMD) ------------------------------
+//
+// Eight waves of 128 (M) x 64 (N) on the 256 x 256 tile (4 x 2 MFMA tiles,
+// 128 accumulators), two waves a SIMD: while one wave waits on its LDS reads
+// or the step's barrier the other issues MFMAs (2048 x 14336 x 4096: 148-155
+// -> 131-134 us against the four-wave kernel).  The four stages keep their A parts
+// side by side (16 KB each) and their B parts side by side (64 KB above), so
+// that one base register per operand and pass half reaches every stage and
+// tile through the ds_read offset field; each wave fills 32 A rows and 32 B
+// rows of a stage (two direct loads each), three steps ahead.
+constexpr int F8_A = 16384, F8_B = 65536;
+
+struct Frags8 {
+  u32x4 x[12];  // A tiles 0..3 (halves 2t, 2t + 1), then B tiles 0..1 (8 + 2t, 9 + 2t)
+};
+
+__device__ __forceinline__ void wait_lds8(Frags8 &F) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(F.x[0]), "+v"(F.x[1]), "+v"(F.x[2]), "+v"(F.x[3]));
+  asm volatile("" : "+v"(F.x[4]), "+v"(F.x[5]), "+v"(F.x[6]), "+v"(F.x[7]));
+  asm volatile("" : "+v"(F.x[8]), "+v"(F.x[9]), "+v"(F.x[10]), "+v"(F.x[11]));
+}
+
+// Fragment f of stage ST (f < 8: A tile f / 2, else B tile (f - 8) / 2; half f % 2).
+template <int ST, int F>
+__device__ __forceinline__ u32x4 frag8(const uint32_t (&rd)[2][2]) {
+  constexpr int t = F < 8 ? F / 2 : (F - 8) / 2;
+  return ds_read16_off<ST * F8_A + 2048 * t>(rd[F & 1][F < 8 ? 0 : 1]);
+}
+
+__device__ __forceinline__ i32x8 frag8_op(const Frags8 &F, int f) {
+  const u32x4 x0 = F.x[f], x1 = F.x[f + 1];
+  return (i32x8){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+}
+
+// The 8 MFMAs of one K-step on `cur`; after MFMA f < 6, reads 2f and 2f + 1
+// of the next step's fragments from stage ST.
+template <int ST>
+__device__ __forceinline__ void mfma_step8(const Frags8 &cur, Frags8 &nxt, const uint32_t (&rd)[2][2],
+                                           f32x16 (&acc)[4][2]) {
+  static_for<4>([&](auto I) {
+    static_for<2>([&](auto J) {
+      constexpr int f = 2 * decltype(I)::value + decltype(J)::value;
+      acc[I][J] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(frag8_op(cur, 2 * I), frag8_op(cur, 8 + 2 * J),
+                                                                  acc[I][J], 0, 0, 0, 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (f < 6) {
+        nxt.x[2 * f] = frag8<ST, 2 * f>(rd);
+        nxt.x[2 * f + 1] = frag8<ST, 2 * f + 1>(rd);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  });
+}
+
+__global__ __launch_bounds__(512) void k_fp8_gemm_pipe8(const uint8_t *__restrict__ a,
+                                                       const float *__restrict__ xs, int64_t m,
+                                                       const uint8_t *__restrict__ b,
+                                                       const float *__restrict__ ws, int64_t n,
+                                                       int64_t k, void *__restrict__ y, int ytype) {
+  __shared__ __attribute__((aligned(1024))) uint8_t SM[4 * P_STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int64_t m0 = (int64_t)blockIdx.y * 256, n0 = (int64_t)blockIdx.x * 256;
+  const int64_t nk = k / 64;
+
+  // Wave w fills rows 32 w .. 32 w + 31 of the A and B parts of a stage, 16
+  // rows (4 lanes x 16 bytes a row) an instruction, lane L at byte 16 L of
+  // the instruction's kilobyte; rows past m or n re-read the last valid row.
+  const uint8_t *ga[2], *gb[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = 32 * wave + 16 * j + (lane >> 2);
+    const int gc = (lane & 3) ^ swz(r);
+    const int64_t gm = m0 + r < m ? m0 + r : m - 1;
+    const int64_t gn = n0 + r < n ? n0 + r : n - 1;
+    ga[j] = a + gm * k + 16 * gc;
+    gb[j] = b + gn * k + 16 * gc;
+  }
+  uint8_t *const dA = SM + 2048 * wave, *const dB = SM + F8_B + 2048 * wave;
+  auto issue = [&](int st, int64_t k0) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_global_load_lds(ga[j] + k0, (lds_void *)(dA + st * F8_A + 1024 * j), 16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_global_load_lds(gb[j] + k0, (lds_void *)(dB + st * F8_A + 1024 * j), 16, 0, 0);
+  };
+  uint32_t rd[2][2];  // [half][A, B]
+  {
+    const uint32_t sa = lds_addr(SM), sb = sa + F8_B;
+    const int l = lane & 31, g = lane >> 5, sw = (l >> 2) & 3;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      rd[h][0] = sa + 8192 * wm + 64 * l + 16 * ((2 * g + h) ^ sw);
+      rd[h][1] = sb + 4096 * wn + 64 * l + 16 * ((2 * g + h) ^ sw);
+    }
+  }
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = (f32x16){0};
+
+  // Stages 0..3 in flight; fragments of step 0 in registers.
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    if (s < nk) issue(s, 64 * s);
+  if (nk > 3) wait_vm<12>();
+  else if (nk > 2) wait_vm<8>();
+  else if (nk > 1) wait_vm<4>();
+  else wait_vm<0>();
+  __builtin_amdgcn_s_barrier();
+  Frags8 F0, F1;
+  static_for<12>([&](auto Fc) { F0.x[decltype(Fc)::value] = frag8<0, decltype(Fc)::value>(rd); });
+  wait_lds8(F0);
+
+  // Step t (stage t % 4 in registers): make stage t + 1 resident (wait for its
+  // loads, then a bare barrier), refill stage t % 4 with K-step t + 4 (every
+  // wave has read it), then the MFMAs of step t with the reads of step t + 1.
+  // The last step reads a stale stage (in bounds, never used), so that every
+  // step has the same straight-line MFMA code (k % 256 == 0: whole groups of
+  // four steps).
+  auto step = [&](const Frags8 &cur, Frags8 &nxt, int64_t t, auto STc) {
+    constexpr int ST = decltype(STc)::value;
+    if (t + 3 < nk) wait_vm<8>();
+    else if (t + 2 < nk) wait_vm<4>();
+    else wait_vm<0>();
+    __builtin_amdgcn_s_barrier();
+    if (t + 4 < nk) issue(ST, 64 * (t + 4));
+    mfma_step8<(ST + 1) & 3>(cur, nxt, rd, acc);
+    wait_lds8(nxt);
+  };
+  for (int64_t t = 0; t < nk; t += 4) {
+    step(F0, F1, t, std::integral_constant<int, 0>{});
+    step(F1, F0, t + 1, std::integral_constant<int, 1>{});
+    step(F0, F1, t + 2, std::integral_constant<int, 2>{});
+    step(F1, F0, t + 3, std::integral_constant<int, 3>{});
+  }
+
+  const bool vec = vec_stores_ok(y, n);
+  float sx[4][4], sw[2][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) tile_row_scales(xs, m, m0 + 128 * wm + i * 32, lane, sx[i]);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) tile_col_scales(ws, n, n0 + 64 * wn + j * 32, lane, sw[j]);
+  if (ytype != RQ_F32 && vec && n % 8 == 0 && m0 + 256 <= m && n0 + 256 <= n) {
+    __syncthreads();  // every wave's stage reads are done
+    const float nob[2][4] = {};
+    stage_block_2b<true>(acc, SM, 128 * wm, 64 * wn, ytype, sx, sw, nob, false, lane);
+    __syncthreads();
+    store_staged_2b<512>(SM, y, n, m0, n0, tid);
+    return;
+  }
+  const Out o{y, nullptr, ytype, 0};
+  const float nob[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  static_for<4>([&](auto I) {
+    static_for<2>([&](auto J) {
+      store_tile32<true>(acc[I][J], o, m, n, m0 + 128 * wm + I * 32, n0 + 64 * wn + J * 32, sx[I], sw[J], nob, xs,
+                         ws, lane, vec);
+    });
+  });
+}
+
 template <int BM, int BN, int WM, int WN, int BK>
 void launch_tiled(const uint8_t *xq, const float *xs, int64_t m, const uint8_t *w, const float *ws,
                   int64_t n, int64_t k, void *y, int ytype, hipStream_t s) {
@@ -479,12 +643,16 @@ int launch_fp8_gemm(const uint8_t *xq, const float *xs, int64_t m, const uint8_t
   const bool aligned = (reinterpret_cast<uintptr_t>(xq) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(w) % 16 == 0);
   if (k % 128 == 0 && aligned) {
-    // 256 x 256 tiles (128 x 128 per wave) when there are enough of them to
-    // cover the CUs, else 128 x 128.
+    // 256 x 256 tiles when there are enough of them to cover the CUs (eight
+    // waves of 128 x 64 for whole groups of four K-steps, else four of
+    // 128 x 128), else 128 x 128.
     const int64_t big = ((m + 255) / 256) * ((n + 255) / 256);
     if (big >= 200) {
       const dim3 grid((unsigned)((n + 255) / 256), (unsigned)((m + 255) / 256));
-      hipLaunchKernelGGL(k_fp8_gemm_pipe, grid, dim3(256), 0, s, xq, xs, m, w, ws, n, k, y, ytype);
+      if (k % 256 == 0)
+        hipLaunchKernelGGL(k_fp8_gemm_pipe8, grid, dim3(512), 0, s, xq, xs, m, w, ws, n, k, y, ytype);
+      else
+        hipLaunchKernelGGL(k_fp8_gemm_pipe, grid, dim3(256), 0, s, xq, xs, m, w, ws, n, k, y, ytype);
     } else {
       launch_tiled<128, 128, 2, 2, 128>(xq, xs, m, w, ws, n, k, y, ytype, s);
     }

@@ -136,10 +136,11 @@ def test_fp8_gemm_full_size_sampled(dev):
     print(f"per-token fp8 vs unquantized-x reference: {norm_err(y[rows].float().cpu().numpy(), ref_sem):.4f}")
 
 
-@pytest.mark.parametrize("m,n,k", [(1300, 10000, 640), (513, 25700, 256), (2048, 14336, 192)])
+@pytest.mark.parametrize("m,n,k", [(1300, 10000, 640), (513, 25700, 256), (1300, 10000, 1280), (2048, 14336, 192)])
 def test_fp8_gemm_pipelined_ragged(dev, m, n, k):
-    # >= 200 tiles of 256 x 256: the 4-stage direct-to-LDS kernel, with ragged
-    # M/N edges and K-step counts that are not a multiple of the stage count
+    # >= 200 tiles of 256 x 256: the 4-stage direct-to-LDS kernels (eight
+    # waves for k % 256 == 0, four otherwise), with ragged M/N edges and K-step
+    # counts that are not a multiple of the stage count
     xb, wq, ws = _fp8_problem(m, n, k, 300 + m)
     y = rq.fp8_gemm(xb, wq, ws, out_dtype=torch.float32)
     rows = np.array([0, 1, m // 2, m - 2, m - 1])
