@@ -269,230 +269,36 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void k_qgemm(const uint8_t *__re
   });
 }
 
-// ---- pipelined 256 x 256 kernel ------------------------------------------
+// ---- pipelined 256 x 256 kernels ------------------------------------------
 //
-// Four waves of 128 x 128 (4 x 4 MFMA tiles of 32 x 32, 256 accumulators in
-// AGPRs), K-steps of 32 inputs (64 bytes of bf16 per row) through four LDS
-// stages of 32 KB: 256 activation rows then 256 weight rows, swizzled as in
-// rq_pipe.h.  Every global load goes to registers (the compiler then counts
-// its waits exactly; mixed with direct-to-LDS loads it would wait for all of
-// them) and every LDS access is explicit (ordered against the bare barriers).
+// Eight waves (two a SIMD) of 128 (M) x 64 (N): 4 x 2 MFMA tiles of 32 x 32,
+// 128 accumulators a wave.  K-steps of 32 inputs (64 bytes of bf16 a row)
+// pass through four LDS stages: the activation parts of the stages side by
+// side (256 rows x 64 bytes, 16 KB each), the weight parts 64 KB above,
+// rows unpadded with the 16-byte chunk index XOR-ed with (row / 4) % 4, so
+// that one base register per role reaches every stage through the 16-bit
+// ds offset field.  Every global load goes to registers (the compiler then
+// counts its waits exactly; mixed with direct-to-LDS loads it would wait for
+// all of them) and every LDS access is explicit (ordered against the bare
+// barriers).  With one wave a SIMD (four waves of 128 x 128, 256
+// accumulators) a wave issued its decode and address VALU work at about half
+// the SIMD's rate between its MFMAs; two waves a SIMD hide one another's
+// waits: the Q6_K head 262144 x 2048 at M = 512 704 -> 634 us, Q4_K
+// 2048 x 14336 x 4096 308 -> 283 us, Q8_0 512 x 151936 x 1024 289 -> 222 us
+// (outputs bit-identical).
 //
-// Step s: each thread writes its four 16-byte activation chunks of step
-// s + 2 (loaded at step s - 2; 4 lanes per row, 16 rows per load
-// instruction) into their stage and loads those of step s + 4.  On even
-// steps it decodes piece h = t % 2 of weight rows t / 2 and t / 2 + 128 for
-// chunk (s + 2) / 2 (loaded at step s - 4; the two lanes of a row read
-// adjacent bytes): run 0 of piece 2c + h holds inputs 16h .. 16h + 15 of
-// K-step 2c and run 1 those of K-step 2c + 1, so the chunk fills the weight
-// rows of steps s + 2 and s + 3; then it loads chunk (s + 6) / 2.  The
-// MFMAs run in two passes (pass H takes 16-byte chunk 2g + H of every row,
-// g = lane / 32, for A and B alike); the fragments of pass 1 are read from
-// LDS during pass 0 and those of the next step's pass 0 during pass 1, so a
-// stage is read during steps s - 1 and s and written during s - 2 or s - 3.
-// Indices past the end are clamped (their loads and writes land in stages
-// that are never read), so the loop body has no branches; k must be a
-// multiple of 128 (four steps per iteration).
-
-// Fragments of one MFMA pass: A of tiles 0..3, then B of tiles 0..3.
-struct Pass {
-  u32x4 x[8];
-};
-
-__device__ __forceinline__ void wait_pass(Pass &P) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(P.x[0]), "+v"(P.x[1]), "+v"(P.x[2]), "+v"(P.x[3]));
-  asm volatile("" : "+v"(P.x[4]), "+v"(P.x[5]), "+v"(P.x[6]), "+v"(P.x[7]));
-}
-
-// LDS address of fragment f (0..3 A tiles, 4..7 B tiles) of pass H.
-__device__ __forceinline__ const uint8_t *pass_addr(const uint8_t *S, int f, int H, int wm, int wn, int lane) {
-  const int t = f & 3, r = (f < 4 ? 128 * wm : 128 * wn) + 32 * t + (lane & 31);
-  return S + (f < 4 ? 0 : P_B) + r * 64 + 16 * ((2 * (lane >> 5) + H) ^ swz(r));
-}
+// Step s: each thread writes its two 16-byte activation chunks of step s + 2
+// (loaded at step s - 2; 4 lanes a row, 16 rows a load instruction) into
+// their stage and loads those of step s + 4, and writes the weight runs it
+// decoded for the stages of steps s + 2 (and s + 3).  The MFMAs run in two
+// passes (pass H takes 16-byte chunk 2g + H of every row, g = lane / 32, for
+// A and B alike); the fragments of pass 1 are read from LDS during pass 0
+// and those of the next step's pass 0 during pass 1, so a stage is read
+// during steps s - 1 and s and written during s - 2 or s - 3.
 
 __device__ __forceinline__ bf16x8 as_bf16(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-// The 16 MFMAs of one pass on `cur`, each followed by one LDS read of the
-// pass `nxt` (stage S, pass H), pinned in that order so the reads run under
-// the matrix work.
-__device__ __forceinline__ void mfma_pass(const Pass &cur, Pass &nxt, const uint8_t *S, int H,
-                                          f32x16 (&acc)[4][4], int wm, int wn, int lane) {
-  static_for<4>([&](auto I) {
-    static_for<4>([&](auto J) {
-      acc[I][J] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16(cur.x[I]), as_bf16(cur.x[4 + J]), acc[I][J], 0, 0,
-                                                          0);
-      if constexpr (J == 0 || J == 2) {
-        constexpr int f = 2 * I + J / 2;
-        __builtin_amdgcn_sched_barrier(0x6);  // VALU / SALU may cross
-        nxt.x[f] = ds_read16(pass_addr(S, f, H, wm, wn, lane));
-        __builtin_amdgcn_sched_barrier(0x6);
-      }
-    });
-  });
-}
-
-__device__ __forceinline__ void write_runs(uint8_t *S0, uint8_t *S1, int row, int h, const uint32_t (&o)[16]) {
-#pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-      ds_write16((r ? S1 : S0) + P_B + row * 64 + 16 * ((2 * h + q) ^ swz(row)),
-                 (u32x4){o[8 * r + 4 * q], o[8 * r + 4 * q + 1], o[8 * r + 4 * q + 2], o[8 * r + 4 * q + 3]});
-}
-
-// Activation chunk `lane % 4` of rows 64 wave + 16 j + lane / 4 (j < 4).
-__device__ __forceinline__ void write_a(uint8_t *S, int wave, int lane, const u32x4 (&a)[4]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = 64 * wave + 16 * j + (lane >> 2);
-    ds_write16(S + r * 64 + 16 * ((lane & 3) ^ swz(r)), a[j]);
-  }
-}
-
-__device__ __forceinline__ void load_a(const uint8_t *const (&src)[4], int64_t s, u32x4 (&a)[4]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) a[j] = *reinterpret_cast<const u32x4 *>(src[j] + 64 * s);
-}
-
 __device__ __forceinline__ void wait_lds_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-
-// The 256 x 256 tile of a pipelined kernel to y: 16-bit outputs of whole
-// tiles through LDS (the four stages, free after the loop) as full rows,
-// other tiles straight from the accumulators.
-__device__ __forceinline__ void pipe_store(const f32x16 (&acc)[4][4], uint8_t *SM, const Out &o, int64_t m,
-                                           int64_t n, int64_t m0, int64_t n0, int wm, int wn, int lane, int tid) {
-  const bool vec = vec_stores_ok(o.y, n);
-  float bb[4][4];  // biases, loaded before the first store
-#pragma unroll
-  for (int j = 0; j < 4; ++j) tile_col_bias(o, n, n0 + 128 * wn + j * 32, lane, bb[j]);
-  if (o.ytype != RQ_F32 && vec && n % 8 == 0 && m0 + 256 <= m && n0 + 256 <= n) {
-    __syncthreads();  // every wave's stage reads are done
-    const float ones[4][4] = {};
-    stage_block_2b<false>(acc, SM, 128 * wm, 128 * wn, o.ytype, ones, ones, bb, o.bias != nullptr, lane);
-    __syncthreads();
-    store_staged_2b(SM, o.y, n, m0, n0, tid);
-    return;
-  }
-  const float one[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-  static_for<4>([&](auto I) {
-    static_for<4>([&](auto J) {
-      store_tile32<false>(acc[I][J], o, m, n, m0 + 128 * wm + I * 32, n0 + 128 * wn + J * 32, one, one, bb[J],
-                          nullptr, nullptr, lane, vec);
-    });
-  });
-}
-
-template <class F>
-__global__ __launch_bounds__(256) void k_qgemm_pipe(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
-                                                    const uint16_t *__restrict__ x, int64_t m, int64_t n,
-                                                    int64_t k, const Out o) {
-  // four stages, one array: after the loop it holds the staged output tile
-  __shared__ __attribute__((aligned(1024))) uint8_t SM[4 * P_STAGE];
-  uint8_t *const S0 = SM, *const S1 = SM + P_STAGE, *const S2 = SM + 2 * P_STAGE, *const S3 = SM + 3 * P_STAGE;
-  uint8_t *const SB[4] = {S0, S1, S2, S3};
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  // Tile order: workgroup b runs on XCD b % 8 (workgroups are dealt to the
-  // eight XCDs in turn, each with its own L2).  XCD x takes the x-th eighth
-  // of the tiles in M-fastest order, so the M tiles that share a weight tile
-  // run back to back on one XCD and read it from that XCD's L2 after the
-  // first (without the remap they ran half a launch apart on different
-  // XCDs).  Grids whose tile count is not a multiple of 8 keep b.
-  const int64_t gm = gridDim.y, tiles = (int64_t)gridDim.x * gridDim.y;
-  const int64_t b = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
-  const int64_t lin = tiles % 8 == 0 ? (b % 8) * (tiles / 8) + b / 8 : b;
-  const int64_t m0 = (lin % gm) * 256, n0 = (lin / gm) * 256;
-  const int64_t nk = k / 32;
-  const int last = (int)nk - 1;
-
-  // Activation rows past m re-read row m - 1 and weight rows past n re-read
-  // row n - 1; their results are never stored.
-  const uint8_t *asrc[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t gm = m0 + 64 * wave + 16 * j + (lane >> 2);
-    asrc[j] = reinterpret_cast<const uint8_t *>(x + (gm < m ? gm : m - 1) * k) + 16 * (lane & 3);
-  }
-  const int h = tid & 1, br = tid >> 1;
-  const uint64_t rk0 = (uint64_t)(n0 + br < n ? n0 + br : n - 1) * (uint64_t)k;
-  const uint64_t rk1 = (uint64_t)(n0 + br + 128 < n ? n0 + br + 128 : n - 1) * (uint64_t)k;
-
-  f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = (f32x16){0};
-
-  // Prologue: stages 0 and 1 written, activations of steps 2 and 3 and the
-  // pieces of chunk 1 in flight, pass 0 of step 0 read.
-  u32x4 ra[2][4];
-  typename F::Piece pb[2][2];  // [chunk % 2][row]: chunks c + 1 and c + 2 in flight
-  {
-    u32x4 a0[4], a1[4];
-    load_a(asrc, 0, a0);
-    load_a(asrc, 1, a1);
-    const typename F::Piece p0 = F::load_e(w, aux, rk0, h), p1 = F::load_e(w, aux, rk1, h);
-    load_a(asrc, 2 < nk ? 2 : last, ra[0]);
-    load_a(asrc, 3 < nk ? 3 : last, ra[1]);
-    // piece h of chunks 1 and 2 (clamped to the last chunk)
-    const int c1 = (2 < nk ? 2 : last - 1) + h, c2 = (4 < nk ? 4 : last - 1) + h;
-    pb[1][0] = F::load_e(w, aux, rk0, c1);
-    pb[1][1] = F::load_e(w, aux, rk1, c1);
-    pb[0][0] = F::load_e(w, aux, rk0, c2);
-    pb[0][1] = F::load_e(w, aux, rk1, c2);
-    write_a(S0, wave, lane, a0);
-    write_a(S1, wave, lane, a1);
-    uint32_t o[16];
-    F::decode_bf16(p0, o);
-    write_runs(S0, S1, br, h, o);
-    F::decode_bf16(p1, o);
-    write_runs(S0, S1, br + 128, h, o);
-  }
-  wait_lds_all();
-  __builtin_amdgcn_s_barrier();
-  Pass P0, P1;
-#pragma unroll
-  for (int f = 0; f < 8; ++f) P0.x[f] = ds_read16(pass_addr(S0, f, 0, wm, wn, lane));
-  wait_pass(P0);
-
-  // Step s, stage buffer B = s % 4 (P0 holds pass 0 of step s on entry and
-  // pass 0 of step s + 1 on exit).
-  auto step = [&](int64_t s, auto Bc) {
-    constexpr int B = decltype(Bc)::value;
-    __builtin_amdgcn_s_barrier();
-    // The decode has no memory operations, so it can be scheduled among
-    // the MFMAs; the LDS writes and the next loads follow the matrix work.
-    // chunk (s + 2) / 2 sits in slot ((s + 2) / 2) % 2 = (B / 2 + 1) % 2
-    constexpr int SL = ((B >> 1) + 1) & 1;
-    uint32_t o0[16], o1[16];
-    if constexpr ((B & 1) == 0) {
-      F::decode_bf16(pb[SL][0], o0);
-      F::decode_bf16(pb[SL][1], o1);
-    }
-    mfma_pass(P0, P1, SB[B], 1, acc, wm, wn, lane);
-    wait_pass(P1);
-    mfma_pass(P1, P0, SB[(B + 1) & 3], 0, acc, wm, wn, lane);
-    write_a(SB[(B + 2) & 3], wave, lane, ra[B & 1]);
-    load_a(asrc, s + 4 < nk ? s + 4 : last, ra[B & 1]);
-    if constexpr ((B & 1) == 0) {
-      write_runs(SB[(B + 2) & 3], SB[(B + 3) & 3], br, h, o0);
-      write_runs(SB[(B + 2) & 3], SB[(B + 3) & 3], br + 128, h, o1);
-      const int pn = (int)(s + 6 < nk ? s + 6 : last - 1) + h;  // piece h of chunk (s + 6) / 2
-      pb[SL][0] = F::load_e(w, aux, rk0, pn);
-      pb[SL][1] = F::load_e(w, aux, rk1, pn);
-    }
-    wait_pass(P0);
-    wait_lds_all();
-  };
-  for (int64_t t = 0; t < nk; t += 4) {
-    step(t, std::integral_constant<int, 0>{});
-    step(t + 1, std::integral_constant<int, 1>{});
-    step(t + 2, std::integral_constant<int, 2>{});
-    step(t + 3, std::integral_constant<int, 3>{});
-  }
-
-  pipe_store(acc, SM, o, m, n, m0, n0, wm, wn, lane, tid);
-}
 
 // ---- pipelined 256 x 256 kernel, Q6_K in chunk pairs ------------------
 //
@@ -500,8 +306,9 @@ __global__ __launch_bounds__(256) void k_qgemm_pipe(const uint8_t *__restrict__ 
 // dequant_k.rs:87-111) share their quant bytes: ql byte l holds the low four
 // bits of element l of chunk 2j (nibble 0) and of chunk 2j + 1 (nibble 1),
 // qh byte l the high two bits of both (bits 0-1 / 2-3 for chunk 2j, 4-5 / 6-7
-// for 2j + 1).  k_qgemm_pipe loads a piece's 48 quant bytes once per chunk;
-// here a thread loads them once per pair (ql runs [16 hh, + 16) and
+// for 2j + 1).  The generic kernel (k_qgemm_pipe8 with FmtQ6KG) loads a
+// piece's 48 quant bytes once per chunk; here a thread loads them once per
+// pair (ql runs [16 hh, + 16) and
 // [32 + 16 hh, + 16), qh run [16 hh, + 16), the half's eight scales and d)
 // and decodes one 16-weight run of it per K-step: the pair of K-steps
 // 4j .. 4j + 3 is decoded during steps 4j - 2 .. 4j + 1 into the stage of
@@ -789,6 +596,150 @@ __global__ __launch_bounds__(512) void k_q6_pipe8(const uint8_t *__restrict__ w,
   });
 }
 
+// ---- generic formats on eight waves -------------------------------------
+//
+// Each format's pieces (64-element chunks, run 0 of piece 2c + h holding
+// inputs 16h .. 16h + 15 of K-step 2c and run 1 those of K-step 2c + 1, so a
+// chunk fills the weight rows of two consecutive stages) on the eight waves
+// and LDS layout of k_q6_pipe8: each thread decodes piece t % 2 of
+// weight row t / 2 every other step (chunk (s + 2) / 2 in step s, s even),
+// and the pieces of chunks c + 1 and c + 2 are in flight in two register
+// slots.  Indices past the end are clamped (their loads and writes land in
+// stages that are never read); k must be a multiple of 128.
+template <int ST>
+__device__ __forceinline__ void write_run16(const PipeBases8 &pb, const uint32_t *o) {
+  ds_write16_off<ST * P8_A>(pb.wr[0], (u32x4){o[0], o[1], o[2], o[3]});
+  ds_write16_off<ST * P8_A>(pb.wr[1], (u32x4){o[4], o[5], o[6], o[7]});
+}
+
+template <class F>
+__global__ __launch_bounds__(512) void k_qgemm_pipe8(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
+                                                     const uint16_t *__restrict__ x, int64_t m, int64_t n,
+                                                     int64_t k, const Out o) {
+  __shared__ __attribute__((aligned(1024))) uint8_t SM[4 * P_STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int64_t gm = gridDim.y, tiles = (int64_t)gridDim.x * gridDim.y;
+  const int64_t b = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+  const int64_t lin = tiles % 8 == 0 ? (b % 8) * (tiles / 8) + b / 8 : b;
+  const int64_t m0 = (lin % gm) * 256, n0 = (lin / gm) * 256;
+  const int64_t nk = k / 32;
+  const int last = (int)nk - 1;
+
+  const uint8_t *asrc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t gr = m0 + 32 * wave + 16 * j + (lane >> 2);
+    asrc[j] = reinterpret_cast<const uint8_t *>(x + (gr < m ? gr : m - 1) * k) + 16 * (lane & 3);
+  }
+  const int h = tid & 1, br = tid >> 1;
+  const uint64_t rk0 = (uint64_t)(n0 + br < n ? n0 + br : n - 1) * (uint64_t)k;
+
+  PipeBases8 pb;
+  {
+    const uint32_t sa = lds_addr(SM), sb = sa + P8_B;
+    const int l = lane & 31, g = lane >> 5, sw = (l >> 2) & 3;
+#pragma unroll
+    for (int H = 0; H < 2; ++H) {
+      pb.rd[H][0] = sa + 8192 * wm + 64 * l + 16 * ((2 * g + H) ^ sw);
+      pb.rd[H][1] = sb + 4096 * wn + 64 * l + 16 * ((2 * g + H) ^ sw);
+    }
+    pb.wa = sa + 2048 * wave + 64 * (lane >> 2) + 16 * ((lane & 3) ^ ((lane >> 4) & 3));
+#pragma unroll
+    for (int q = 0; q < 2; ++q) pb.wr[q] = sb + 64 * br + 16 * ((2 * h + q) ^ swz(br));
+  }
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = (f32x16){0};
+
+  // Prologue: stages 0 and 1 written (chunk 0), activations of steps 2 and 3
+  // and the pieces of chunks 1 and 2 in flight, pass 0 of step 0 read.
+  u32x4 ra[2][2];
+  typename F::Piece pc[2];  // [chunk % 2]
+  {
+    u32x4 a0[2], a1[2];
+    load_a8(asrc, 0, a0);
+    load_a8(asrc, 1, a1);
+    const typename F::Piece p0 = F::load_e(w, aux, rk0, h);
+    load_a8(asrc, 2 < nk ? 2 : last, ra[0]);
+    load_a8(asrc, 3 < nk ? 3 : last, ra[1]);
+    const int c1 = (2 < nk ? 2 : last - 1) + h, c2 = (4 < nk ? 4 : last - 1) + h;
+    pc[1] = F::load_e(w, aux, rk0, c1);
+    pc[0] = F::load_e(w, aux, rk0, c2);
+    write_a8<0>(pb, a0);
+    write_a8<1>(pb, a1);
+    uint32_t o[16];
+    F::decode_bf16(p0, o);
+    write_run16<0>(pb, o);
+    write_run16<1>(pb, o + 8);
+  }
+  wait_lds_all();
+  __builtin_amdgcn_s_barrier();
+  Pass8 P0, P1;
+  static_for<6>([&](auto Fc) {
+    constexpr int f = decltype(Fc)::value;
+    P0.x[f] = ds_read16_off<2048 * (f < 4 ? f : f - 4)>(pb.rd[0][f < 4 ? 0 : 1]);
+  });
+  wait_pass8(P0);
+
+  // Step s = 4u + B: pass 1 of stage B, pass 0 of stage (B + 1) % 4; on even
+  // steps the chunk (s + 2) / 2 (slot (B / 2 + 1) % 2) into stages
+  // (B + 2) % 4 and (B + 3) % 4, whose last reads were in steps s - 2 and
+  // s - 1, and the piece of chunk (s + 6) / 2 into that slot.
+  auto step = [&](int64_t s, auto Bc) {
+    constexpr int B = decltype(Bc)::value;
+    constexpr int SL = ((B >> 1) + 1) & 1;
+    __builtin_amdgcn_s_barrier();
+    write_a8<(B + 2) & 3>(pb, ra[B & 1]);
+    load_a8(asrc, s + 4 < nk ? s + 4 : last, ra[B & 1]);
+    uint32_t o0[16];
+    if constexpr ((B & 1) == 0) F::decode_bf16(pc[SL], o0);
+    mfma_pass8<B, 1>(P0, P1, pb, acc, [](auto) {});
+    wait_pass8(P1);
+    mfma_pass8<(B + 1) & 3, 0>(P1, P0, pb, acc, [&](auto Fc) {
+      if constexpr ((B & 1) == 0 && decltype(Fc)::value == 0) {
+        write_run16<(B + 2) & 3>(pb, o0);
+        write_run16<(B + 3) & 3>(pb, o0 + 8);
+      }
+    });
+    if constexpr ((B & 1) == 0) {
+      const int pn = (int)(s + 6 < nk ? s + 6 : last - 1) + h;  // piece h of chunk (s + 6) / 2
+      pc[SL] = F::load_e(w, aux, rk0, pn);
+    }
+    wait_pass8(P0);
+    wait_lds_all();
+  };
+  for (int64_t t = 0; t < nk; t += 4) {
+    step(t, std::integral_constant<int, 0>{});
+    step(t + 1, std::integral_constant<int, 1>{});
+    step(t + 2, std::integral_constant<int, 2>{});
+    step(t + 3, std::integral_constant<int, 3>{});
+  }
+
+  const bool vec = vec_stores_ok(o.y, n);
+  float bb[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) tile_col_bias(o, n, n0 + 64 * wn + j * 32, lane, bb[j]);
+  if (o.ytype != RQ_F32 && vec && n % 8 == 0 && m0 + 256 <= m && n0 + 256 <= n) {
+    __syncthreads();
+    const float unused_x[4][4] = {}, unused_w[2][4] = {};
+    stage_block_2b<false>(acc, SM, 128 * wm, 64 * wn, o.ytype, unused_x, unused_w, bb, o.bias != nullptr, lane);
+    __syncthreads();
+    store_staged_2b<512>(SM, o.y, n, m0, n0, tid);
+    return;
+  }
+  const float one[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  static_for<4>([&](auto I) {
+    static_for<2>([&](auto J) {
+      store_tile32<false>(acc[I][J], o, m, n, m0 + 128 * wm + I * 32, n0 + 64 * wn + J * 32, one, one, bb[J],
+                          nullptr, nullptr, lane, vec);
+    });
+  });
+}
+
 // y = sum over s < splits of part[s] (f32 partials of m * n outputs), with
 // o's bias.
 __global__ __launch_bounds__(256) void k_splitk_sum(const float *__restrict__ part, int splits, int64_t mn,
@@ -891,7 +842,7 @@ int launch_pipe(const rq_weight *wt, const void *x, int64_t m, const Out &o, hip
     hipLaunchKernelGGL(k_q6_pipe8, grid, dim3(512), 0, s, wt->data, wt->data + wt->aux_off,
                        static_cast<const uint16_t *>(x), m, wt->n, wt->k, o);
   else
-    hipLaunchKernelGGL((k_qgemm_pipe<F>), grid, dim3(256), 0, s, wt->data, wt->data + wt->aux_off,
+    hipLaunchKernelGGL((k_qgemm_pipe8<F>), grid, dim3(512), 0, s, wt->data, wt->data + wt->aux_off,
                        static_cast<const uint16_t *>(x), m, wt->n, wt->k, o);
   return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemm launch failed");
 }

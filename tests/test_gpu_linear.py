@@ -401,6 +401,8 @@ def test_mfma_gemm_edge_tiles(dev, qtype, m, n, k):
     (rq.Q6_K, 768, 32768, 256),  # pipelined kernel, three M tiles per weight tile in the XCD-aware order
     (rq.Q6_K, 300, 32868, 512),  # pipelined Q6_K, ragged rows and columns (accumulator stores)
     (rq.Q6_K, 512, 32776, 1024),  # pipelined Q6_K, ragged last column tile, whole tiles staged
+    (rq.Q6_K, 300, 32868, 384),  # Q6_K with k % 256 != 0: the per-chunk pipelined kernel, ragged
+    (rq.Q8_0, 512, 32768, 640),  # pipelined, whole tiles staged
 ])
 def test_large_gemm(dev, qtype, m, n, k):
     w, wf = make(qtype, n, k, 5 + m + k)
@@ -428,7 +430,7 @@ def test_next_formats_gemv_f32(dev, qtype, n, k):
 
 @pytest.mark.parametrize("qtype", NEXT_FORMATS)
 @pytest.mark.parametrize("m,n,k", [(2, 896, 896), (17, 130, 256), (64, 200, 1024), (300, 256, 2048),
-                                   (512, 1024, 512)])
+                                   (512, 1024, 512), (300, 32868, 256)])
 def test_next_formats_matrix_cores(dev, qtype, m, n, k):
     w, wf = make(qtype, n, k, 47 + m)
     xb = torch.from_numpy(synth.activations(49 + m, m, k)).to(torch.bfloat16)

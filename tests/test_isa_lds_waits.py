@@ -94,8 +94,8 @@ def test_fp8_pipe_lds_reads_complete_before_use(tmp_path):
 
 @pytest.mark.skipif(not HAVE_TOOLS, reason="ROCm toolchain not present")
 def test_qgemm_pipe_lds_reads_complete_before_use(tmp_path):
-    # one kernel per GGUF format; 8 reads of the first pass plus 16 per step
-    _check(tmp_path, "rq_gemm.hip", "k_qgemm_pipe", 24)
+    # one eight-wave kernel per GGUF format; 6 reads of the first pass plus 12 per step
+    _check(tmp_path, "rq_gemm.hip", "k_qgemm_pipe8", 18)
 
 
 @pytest.mark.skipif(not HAVE_TOOLS, reason="ROCm toolchain not present")
