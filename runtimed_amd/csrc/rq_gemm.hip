@@ -60,7 +60,7 @@ constexpr int BK = 64, LDS_K = BK + 8;
 // term and the limbs' own rounding leave about 2^-16 of each product, far
 // inside the 1e-3 gate of f32 paths; LDS holds a hi and a lo tile of each
 // operand.
-template <class F, int BM, int BN, int WM, int WN, int D, int KG = 1, int XT = RQ_BF16>
+template <class F, int BM, int BN, int WM, int WN, int D, int KG = 1, int XT = RQ_BF16, int NB = 2>
 __global__ __launch_bounds__(64 * WM * WN * KG) void k_qgemm(const uint8_t *__restrict__ w,
                                                             const uint8_t *__restrict__ aux,
                                                             const void *__restrict__ xv, int64_t m,
@@ -77,7 +77,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void k_qgemm(const uint8_t *__re
   constexpr int A_LOADS = BM * LPR / NT;      // 16-byte loads per thread per step
   constexpr int A_ROWS = NT / LPR;            // activation rows covered by one load round
   constexpr int A_BYTES = BM * LDS_K * 2, B_BYTES = BN * LDS_K * 2;
-  constexpr int G_BYTES = 2 * NL * (A_BYTES + B_BYTES);  // a group's double-buffered tiles
+  constexpr int G_BYTES = NB * NL * (A_BYTES + B_BYTES);  // a group's NB buffers of tiles
   static_assert(KG == 1 || BM * BN * 4 <= G_BYTES, "the partial tile of a group fits its buffers");
   __shared__ __attribute__((aligned(16))) uint8_t SM[KG * G_BYTES];
 
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void k_qgemm(const uint8_t *__re
   // tile l (0 = hi, 1 = lo) of buffer buf
   auto As = [&](int buf, int l = 0) { return reinterpret_cast<uint16_t *>(G + (NL * buf + l) * A_BYTES); };
   auto Bs = [&](int buf, int l = 0) {
-    return reinterpret_cast<uint16_t *>(G + 2 * NL * A_BYTES + (NL * buf + l) * B_BYTES);
+    return reinterpret_cast<uint16_t *>(G + NB * NL * A_BYTES + (NL * buf + l) * B_BYTES);
   };
 
   // Weight piece of this thread: row n0 + (tid >> 1), half h = tid & 1;
@@ -207,7 +207,9 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void k_qgemm(const uint8_t *__re
 
   // Slot (s % D) holds step s once loaded.  Step s: the matrix work on LDS
   // buffer s % 2; step s + 1 (loaded D - 1 steps ago) is written to the other
-  // buffer and its slot refilled with step s + 1 + D; one barrier.  The
+  // buffer and its slot refilled with step s + 1 + D; one barrier.  With one
+  // buffer (NB = 1: half the LDS, so twice the K-groups fit) step s + 1 is
+  // written to the same buffer after a second barrier.  The
   // stores of steps past the end are made anyway (clamped data into a buffer
   // that is never read) and only their matrix work is skipped, so no load is
   // made under a branch.  Every group runs the same number of steps.
@@ -220,9 +222,10 @@ __global__ __launch_bounds__(64 * WM * WN * KG) void k_qgemm(const uint8_t *__re
     static_for<D>([&](auto J) {
       constexpr int j = decltype(J)::value;
       const int64_t s = kt + j;
-      const int buf = (int)(s & 1);
+      const int buf = NB == 2 ? (int)(s & 1) : 0;
       if (s < nk) mfma_step(buf);
-      sstore((j + 1) % D, buf ^ 1);
+      if constexpr (NB == 1) __syncthreads();  // every wave's reads of the one buffer are done
+      sstore((j + 1) % D, NB == 2 ? buf ^ 1 : 0);
       gload((j + 1) % D, s + 1 + D);
       __syncthreads();
     });
@@ -792,7 +795,7 @@ int splits_for(int64_t tiles, int64_t nk) {
   return sp;
 }
 
-template <class F, int BM, int BN, int WM, int WN, int D = 3, int KG = 1, int XT = RQ_BF16>
+template <class F, int BM, int BN, int WM, int WN, int D = 3, int KG = 1, int XT = RQ_BF16, int NB = 2>
 int launch(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease &ws,
            int sp_force = 0) {
   const int64_t nk = wt->k / BK;
@@ -800,7 +803,7 @@ int launch(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStrea
   const int sp = sp_force > 0 ? sp_force : splits_for(gx * gy, nk);
   // K-groups need equal shares of every split's steps.
   if constexpr (KG > 1) {
-    if (nk % ((int64_t)sp * KG) != 0) return launch<F, BM, BN, WM, WN, D, 1, XT>(wt, x, m, o, s, ws, sp);
+    if (nk % ((int64_t)sp * KG) != 0) return launch<F, BM, BN, WM, WN, D, 1, XT, 2>(wt, x, m, o, s, ws, sp);
   }
   const int64_t steps = (nk + sp - 1) / sp;
   const int used = (int)((nk + steps - 1) / steps);  // splits that own at least one step
@@ -811,7 +814,7 @@ int launch(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStrea
     if (!part) return rc;
   }
   const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)used);
-  hipLaunchKernelGGL((k_qgemm<F, BM, BN, WM, WN, D, KG, XT>), grid, dim3(64 * WM * WN * KG), 0, s, wt->data,
+  hipLaunchKernelGGL((k_qgemm<F, BM, BN, WM, WN, D, KG, XT, NB>), grid, dim3(64 * WM * WN * KG), 0, s, wt->data,
                      wt->data + wt->aux_off, x, m, wt->n, wt->k, o, steps, part);
   if (part) {
     const int64_t mn = m * wt->n;
@@ -881,18 +884,31 @@ int by_m(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_
 }
 
 // f32 / f16 activations, m > 64: the two-limb tiles (twice the LDS of the
-// bf16 tiles, so one K-group of 128 x 128 or two of 64 x 64).  Tile shapes
-// follow by_m: 64 x 64 where 128 x 128 tiles are too few for the CUs with
-// short K, K split four ways for long K on few tiles.
+// bf16 tiles).  One LDS buffer a K-group, so that two K-groups of 128 x 128
+// or four of 64 x 64 (eight waves, two a SIMD) fit: against one group of
+// 128 x 128 / two of 64 x 64 double-buffered (one wave a SIMD), M = 512
+// q/k/o 33.6 -> 29.0 us, v 35.2 -> 31.5, gate/up 78.9 -> 73.9, down 91.8 ->
+// 85.3, LM head 2.66 -> 2.51 ms.  Where those forms spill (more than 256
+// registers at two waves a SIMD: Q8_0's pieces on both tiles, Q5_0's on
+// 64 x 64) the double-buffered ones stay (Q8_0 2048 x 2048: 34.0 against
+// 42.6 us with the spills).  Tile shapes follow by_m: 64 x 64 where 128 x 128
+// tiles are too few for the CUs with short K, K split four ways for long K
+// on few tiles.
 template <class F, int XT>
 int by_m_limbs(const rq_weight *wt, const void *x, int64_t m, const Out &o, hipStream_t s, WsLease &ws) {
+  constexpr bool Q8 = std::is_same<F, FmtQ8>::value;
+  constexpr bool WIDE64 = !Q8 && !std::is_same<F, FmtQx0<true>>::value, WIDE128 = !Q8;
+  constexpr int KG128 = WIDE128 ? 2 : 1, NB128 = WIDE128 ? 1 : 2;
   const int64_t tiles128 = ((m + 127) / 128) * ((wt->n + 127) / 128), nk = wt->k / BK;
-  if (tiles128 < 128 && nk <= 32) return launch<F, 64, 64, 2, 1, 1, 2, XT>(wt, x, m, o, s, ws);
+  if (tiles128 < 128 && nk <= 32) {
+    if constexpr (WIDE64) return launch<F, 64, 64, 2, 1, 1, 4, XT, 1>(wt, x, m, o, s, ws);
+    else return launch<F, 64, 64, 2, 1, 1, 2, XT>(wt, x, m, o, s, ws);
+  }
   if (tiles128 < 128 && nk >= 64) {
     const int sp = (int)(nk / 32 < 4 ? nk / 32 : 4);
-    return launch<F, 128, 128, 2, 2, 1, 1, XT>(wt, x, m, o, s, ws, sp);
+    return launch<F, 128, 128, 2, 2, 1, KG128, XT, NB128>(wt, x, m, o, s, ws, sp);
   }
-  return launch<F, 128, 128, 2, 2, 1, 1, XT>(wt, x, m, o, s, ws);
+  return launch<F, 128, 128, 2, 2, 1, KG128, XT, NB128>(wt, x, m, o, s, ws);
 }
 
 template <int XT>

@@ -440,6 +440,18 @@ def test_next_formats_matrix_cores(dev, qtype, m, n, k):
         assert norm_err(y, r) <= TOL_BF16, (ydt, norm_err(y, r))
 
 
+@pytest.mark.parametrize("qtype", NEXT_FORMATS + [rq.Q8_0])
+@pytest.mark.parametrize("m,n,k", [(130, 256, 2048), (300, 2048, 4096), (512, 4096, 512)])
+def test_next_formats_f32_prefill(dev, qtype, m, n, k):
+    # f32 activations above 64 rows: the two-limb tiles (64 x 64 in four
+    # single-buffered K-groups, 128 x 128 in two, split K for long rows; Q8_0
+    # and Q5_0 keep double-buffered groups where the wide form would spill)
+    w, wf = make(qtype, n, k, 53 + m)
+    x = synth.activations(55 + m, m, k)
+    y = w.forward(torch.from_numpy(x).to(dev)).cpu().numpy()
+    assert norm_err(y, ref(x, wf)) <= TOL_F32
+
+
 @pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q8_0, rq.Q6_K])
 def test_fused_weights_concatenate(dev, qtype):
     # q/k/v (and gate/up) each hold a whole number of blocks, so their GGUF
