@@ -548,6 +548,59 @@ __global__ __launch_bounds__(1024) void k_gemv_team(const uint8_t *__restrict__ 
   }
 }
 
+// M = 1, long rows, two rows a workgroup on two teams: team j (waves
+// j T .. j T + T - 1) takes row blockIdx.x + j gridDim.x, one piece a lane.
+// x is staged once in LDS for both teams (its loads issued before the weight
+// loads), so each wave decodes and dots one row: with one team walking both
+// rows a SIMD held about one wave, which issues its VALU work at half the
+// SIMD's rate.  The teams' wave sums meet in LDS; one thread a row adds them
+// in wave order.
+template <class F, int XR, bool PLAIN = false>
+__global__ __launch_bounds__(1024) void k_gemv_team2(const uint8_t *__restrict__ w, const uint8_t *__restrict__ aux,
+                                                    const void *__restrict__ x, int xtype_arg, const Out o_arg,
+                                                    int64_t n, int64_t k) {
+  const int xtype = PLAIN ? RQ_F32 : xtype_arg;
+  const Out o = PLAIN ? Out{o_arg.y, nullptr, RQ_F32, 0} : o_arg;
+  __shared__ float red[2][kTeamMax];
+  extern __shared__ __attribute__((aligned(16))) float xs_dyn[];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int team = (int)(blockDim.x >> 7);  // waves a team
+  const int j = wv >= team ? 1 : 0, tm = wv - j * team;
+  const int P = (int)(k / F::PE);
+  const int p = 64 * tm + lane;
+  const bool live = p < P;
+  const int pl = live ? p : P - 1;
+  const int64_t row = (int64_t)blockIdx.x + j * (int64_t)gridDim.x;
+
+  chunk16 xc[XR];
+  load_x_chunks<XR>(x, xtype, (int)k, xc);
+  __builtin_amdgcn_sched_barrier(0);
+  const typename F::Piece pc = F::load(w, aux, row < n ? row : n - 1, k, pl);
+  __builtin_amdgcn_sched_barrier(0);
+  store_x_chunks<XR>(xtype, (int)k, xc, xs_dyn);  // ends with a barrier
+  float xv[F::RUNS][16], sx[F::RUNS];
+#pragma unroll
+  for (int r = 0; r < F::RUNS; ++r) {
+    load_run_lds<16>(xs_dyn, (int)F::run_off(pl, r), xv[r]);
+    sx[r] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) sx[r] += xv[r][t];
+  }
+  float acc = live ? F::dot(pc, xv, sx) : 0.0f;
+  acc = seg_sum(acc, 64);
+  if (lane == 63) red[j][tm] = acc;
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    const int jj = (int)threadIdx.x;
+    const int64_t r = (int64_t)blockIdx.x + jj * (int64_t)gridDim.x;
+    if (r < n) {
+      float tot = red[jj][0];
+      for (int q = 1; q < team; ++q) tot += red[jj][q];
+      store_linear(o, 0, n, r, tot);
+    }
+  }
+}
+
 // M > 1 (interim path): each piece is decoded once to exact f32 weights and
 // then dotted with every activation row, read from memory.
 template <class F, int PPL>
@@ -660,6 +713,23 @@ int run_team(const rq_weight *wt, const void *x, int xtype, const Out &o, hipStr
   const int64_t grid = (wt->n + per - 1) / per;
   if (grid > 0x7FFFFFFF) return RQ_E_UNSUPPORTED;
   const bool plain = xtype == RQ_F32 && o.ytype == RQ_F32 && !o.bias;
+  if constexpr (MR == 1) {
+    const size_t xb = xlds_bytes(wt->k);
+    const int xr = (x_chunks(wt->k, xtype) + 128 * team - 1) / (128 * team);
+    if (per == 2 && team <= 8 && xb && xr <= 4 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && wt->k % 8 == 0) {
+      const unsigned g2 = (unsigned)((wt->n + 1) / 2);
+#define RQ_TEAM2(XRV, PL)                                                                                     \
+  hipLaunchKernelGGL((k_gemv_team2<F, XRV, PL>), dim3(g2), dim3(128 * team), xb, s, wt->data,               \
+                     wt->data + wt->aux_off, x, xtype, o, wt->n, wt->k)
+      if (plain) {
+        if (xr <= 1) RQ_TEAM2(1, true); else if (xr <= 2) RQ_TEAM2(2, true); else RQ_TEAM2(4, true);
+      } else {
+        if (xr <= 1) RQ_TEAM2(1, false); else if (xr <= 2) RQ_TEAM2(2, false); else RQ_TEAM2(4, false);
+      }
+#undef RQ_TEAM2
+      return hipGetLastError() == hipSuccess ? RQ_OK : set_error(RQ_E_DEVICE, "gemv launch failed");
+    }
+  }
   auto go = [&](auto Dc) {
     constexpr int D = decltype(Dc)::value;
     if constexpr (MR == 1) {
