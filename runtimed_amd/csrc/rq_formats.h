@@ -60,6 +60,42 @@ __device__ __forceinline__ void load_run(const void *x, int xtype, int64_t idx, 
   }
 }
 
+
+// Weight loads.  NT = true marks them non-temporal (streamed once: the M = 1
+// GEMVs, whose weights are not read again before the whole model has passed
+// through the caches); the GEMM tiles re-read a weight tile for each M tile
+// and keep plain loads.  On the decode layer set (128 distinct layer copies)
+// the non-temporal GEMV loads took 437 -> 478 GB/s: the gate GEMV 2.95 ->
+// 2.83 us, the down projection 3.55 -> 3.29.
+typedef uint32_t fmt_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t fmt_u32x2 __attribute__((ext_vector_type(2)));
+
+template <bool NT>
+__device__ __forceinline__ uint4 ld_w16(const uint8_t *p) {
+  if constexpr (NT) {
+    const fmt_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const fmt_u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return *reinterpret_cast<const uint4 *>(p);
+  }
+}
+
+template <bool NT>
+__device__ __forceinline__ uint2 ld_w8(const uint8_t *p) {
+  if constexpr (NT) {
+    const fmt_u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const fmt_u32x2 *>(p));
+    return make_uint2(v.x, v.y);
+  } else {
+    return *reinterpret_cast<const uint2 *>(p);
+  }
+}
+
+template <bool NT, class T>
+__device__ __forceinline__ T ld_w(const T *p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+
 // ---------------------------------------------------------------- formats --
 
 // Q4_K (dequant_k.rs:19-44) on the aligned GGUF stream.
@@ -74,17 +110,19 @@ struct FmtQ4K {
   };
   // The piece of the row whose first element is element rk of the flat
   // stream (rk = row * k).
+  template <bool NT = false>
   __device__ __forceinline__ static Piece load_e(const uint8_t *w, const uint8_t *, uint64_t rk, int p) {
     const uint64_t e = rk + 64u * (uint64_t)(p >> 1);
     const uint8_t *bp = w + (e >> 8) * 144u;
     Piece pc;
     pc.c = (int)((e >> 6) & 3u);
-    pc.hd = *reinterpret_cast<const uint4 *>(bp);
-    pc.qv = *reinterpret_cast<const uint4 *>(bp + 16 + 32 * pc.c + 16 * (p & 1));
+    pc.hd = ld_w16<NT>(bp);
+    pc.qv = ld_w16<NT>(bp + 16 + 32 * pc.c + 16 * (p & 1));
     return pc;
   }
+  template <bool NT = false>
   __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
-    return load_e(w, aux, (uint64_t)row * (uint64_t)k, p);
+    return load_e<NT>(w, aux, (uint64_t)row * (uint64_t)k, p);
   }
   // (d*sc, dmin*m) for sub-blocks 2c (low nibbles) and 2c+1 (high nibbles):
   // scale_min_k4 (dequant_k.rs:8-16) on the packed bytes in hd.y/z/w.
@@ -209,6 +247,7 @@ struct FmtQ6K {
   };
   // The piece of the row whose first element is element rk of the flat
   // stream (rk = row * k).
+  template <bool NT = false>
   __device__ __forceinline__ static Piece load_e(const uint8_t *w, const uint8_t *aux, uint64_t rk, int p) {
     const uint64_t e = rk + 128u * (uint64_t)(p >> 1);
     const uint64_t blk = e >> 8;
@@ -216,15 +255,16 @@ struct FmtQ6K {
     const uint8_t *rec = w + blk * 208u;
     Piece pc;
     pc.s = s;
-    pc.a = *reinterpret_cast<const uint4 *>(rec + 64 * hf + 16 * s);
-    pc.b = *reinterpret_cast<const uint4 *>(rec + 64 * hf + 32 + 16 * s);
-    pc.h = *reinterpret_cast<const uint4 *>(rec + 128 + 32 * hf + 16 * s);
-    pc.sc = *reinterpret_cast<const uint2 *>(rec + 192 + 8 * hf);
-    pc.d = reinterpret_cast<const uint16_t *>(aux)[blk];
+    pc.a = ld_w16<NT>(rec + 64 * hf + 16 * s);
+    pc.b = ld_w16<NT>(rec + 64 * hf + 32 + 16 * s);
+    pc.h = ld_w16<NT>(rec + 128 + 32 * hf + 16 * s);
+    pc.sc = ld_w8<NT>(rec + 192 + 8 * hf);
+    pc.d = ld_w<NT>(reinterpret_cast<const uint16_t *>(aux) + (blk));
     return pc;
   }
+  template <bool NT = false>
   __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
-    return load_e(w, aux, (uint64_t)row * (uint64_t)k, p);
+    return load_e<NT>(w, aux, (uint64_t)row * (uint64_t)k, p);
   }
   // Unsigned 6-bit codes (q + 32) of run r for dword j.
   __device__ __forceinline__ static uint32_t codes(const Piece &pc, int r, int j) {
@@ -288,18 +328,20 @@ struct FmtQ8 {
   };
   // The piece of the row whose first element is element rk of the flat
   // stream (rk = row * k).
+  template <bool NT = false>
   __device__ __forceinline__ static Piece load_e(const uint8_t *w, const uint8_t *aux, uint64_t rk, int p) {
     Piece pc;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const uint64_t e = rk + (uint64_t)run_off(p, r);
-      pc.q[r] = *reinterpret_cast<const uint4 *>(w + e);
-      pc.d[r] = reinterpret_cast<const uint16_t *>(aux)[e >> 5];
+      pc.q[r] = ld_w16<NT>(w + e);
+      pc.d[r] = ld_w<NT>(reinterpret_cast<const uint16_t *>(aux) + (e >> 5));
     }
     return pc;
   }
+  template <bool NT = false>
   __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
-    return load_e(w, aux, (uint64_t)row * (uint64_t)k, p);
+    return load_e<NT>(w, aux, (uint64_t)row * (uint64_t)k, p);
   }
   __device__ __forceinline__ static float dot(const Piece &pc, const float (&xv)[RUNS][16], const float (&sx)[RUNS]) {
     float acc = 0.0f;
@@ -359,18 +401,20 @@ struct FmtQ5K {
   };
   // The piece of the row whose first element is element rk of the flat
   // stream (rk = row * k).
+  template <bool NT = false>
   __device__ __forceinline__ static Piece load_e(const uint8_t *w, const uint8_t *, uint64_t rk, int p) {
     const uint64_t e = rk + 64u * (uint64_t)(p >> 1);
     const uint8_t *bp = w + (e >> 8) * 176u;
     Piece pc;
     pc.c = (int)((e >> 6) & 3u);
-    pc.hd = *reinterpret_cast<const uint4 *>(bp);
-    pc.qv = *reinterpret_cast<const uint4 *>(bp + 48 + 32 * pc.c + 16 * (p & 1));
-    pc.hv = *reinterpret_cast<const uint4 *>(bp + 16 + 16 * (p & 1));
+    pc.hd = ld_w16<NT>(bp);
+    pc.qv = ld_w16<NT>(bp + 48 + 32 * pc.c + 16 * (p & 1));
+    pc.hv = ld_w16<NT>(bp + 16 + 16 * (p & 1));
     return pc;
   }
+  template <bool NT = false>
   __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
-    return load_e(w, aux, (uint64_t)row * (uint64_t)k, p);
+    return load_e<NT>(w, aux, (uint64_t)row * (uint64_t)k, p);
   }
   __device__ __forceinline__ static void scales(const Piece &pc, float &a0, float &b0, float &a1, float &b1) {
     FmtQ4K::Piece q4;
@@ -464,26 +508,28 @@ struct FmtQx0 {
   };
   // The piece of the row whose first element is element rk of the flat
   // stream (rk = row * k).
+  template <bool NT = false>
   __device__ __forceinline__ static Piece load_e(const uint8_t *w, const uint8_t *aux, uint64_t rk, int p) {
     Piece pc;
     pc.h = p & 1;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const uint64_t blk = (rk + (uint64_t)run_off(p, r)) >> 5;
-      pc.q[r] = *reinterpret_cast<const uint4 *>(w + 16 * blk);
+      pc.q[r] = ld_w16<NT>(w + 16 * blk);
       if (Q5) {
-        const uint2 rec = reinterpret_cast<const uint2 *>(aux)[blk];
+        const uint2 rec = ld_w8<NT>(aux + 8 * (blk));
         pc.qh[r] = rec.x;
         pc.d[r] = rec.y;
       } else {
         pc.qh[r] = 0;
-        pc.d[r] = reinterpret_cast<const uint16_t *>(aux)[blk];
+        pc.d[r] = ld_w<NT>(reinterpret_cast<const uint16_t *>(aux) + (blk));
       }
     }
     return pc;
   }
+  template <bool NT = false>
   __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
-    return load_e(w, aux, (uint64_t)row * (uint64_t)k, p);
+    return load_e<NT>(w, aux, (uint64_t)row * (uint64_t)k, p);
   }
   // Unsigned codes (q + 8, or q + 16 for Q5_0) of dword j of run r.
   __device__ __forceinline__ static uint32_t codes(const Piece &pc, int r, int j) {
@@ -554,6 +600,7 @@ struct FmtQ6KG {
   };
   // The piece of the row whose first element is element rk of the flat
   // stream (rk = row * k).
+  template <bool NT = false>
   __device__ __forceinline__ static Piece load_e(const uint8_t *w, const uint8_t *aux, uint64_t rk, int p) {
     const uint64_t e = rk + 64u * (uint64_t)(p >> 1);
     const uint64_t blk = e >> 8;
@@ -561,16 +608,17 @@ struct FmtQ6KG {
     const uint8_t *rec = w + blk * 208u;
     Piece pc;
     pc.ch = (int)((e >> 6) & 1u);
-    pc.a = *reinterpret_cast<const uint4 *>(rec + 64 * hf + 16 * hh);
-    pc.b = *reinterpret_cast<const uint4 *>(rec + 64 * hf + 32 + 16 * hh);
-    pc.h = *reinterpret_cast<const uint4 *>(rec + 128 + 32 * hf + 16 * hh);
+    pc.a = ld_w16<NT>(rec + 64 * hf + 16 * hh);
+    pc.b = ld_w16<NT>(rec + 64 * hf + 32 + 16 * hh);
+    pc.h = ld_w16<NT>(rec + 128 + 32 * hf + 16 * hh);
     // scales[8hf + hh + 2kk] for kk = 2ch and 2ch+1: bytes 4ch+hh and 4ch+hh+2
-    pc.sc = *reinterpret_cast<const uint32_t *>(rec + 192 + 8 * hf + 4 * pc.ch) >> (8 * hh);
-    pc.d = reinterpret_cast<const uint16_t *>(aux)[blk];
+    pc.sc = ld_w<NT>(reinterpret_cast<const uint32_t *>(rec + 192 + 8 * hf + 4 * pc.ch)) >> (8 * hh);
+    pc.d = ld_w<NT>(reinterpret_cast<const uint16_t *>(aux) + (blk));
     return pc;
   }
+  template <bool NT = false>
   __device__ __forceinline__ static Piece load(const uint8_t *w, const uint8_t *aux, int64_t row, int64_t k, int p) {
-    return load_e(w, aux, (uint64_t)row * (uint64_t)k, p);
+    return load_e<NT>(w, aux, (uint64_t)row * (uint64_t)k, p);
   }
   __device__ __forceinline__ static void decode_bf16(const Piece &pc, uint32_t (&o)[16]) {
     const float d = h2f(pc.d);

@@ -242,7 +242,7 @@ __device__ __forceinline__ void gemv_seg(const uint8_t *__restrict__ w, const ui
   uint32_t bv = 0;
   if (o.bias) bv = bias_bits(o.bias, o.btype, row < n ? row : n - 1);
   __builtin_amdgcn_sched_barrier(0);
-  typename F::Piece cur = F::load(w, aux, row < n ? row : n - 1, k, pl);
+  typename F::Piece cur = F::template load<true>(w, aux, row < n ? row : n - 1, k, pl);
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (MR == 1) store_x_chunks<XR>(xtype, (int)k, xc, xs_dyn);
   else store_x_chunks_rows<XR>(xtype, (int)k, mrows, xstride, xc, xs_dyn);
@@ -292,7 +292,7 @@ __device__ __forceinline__ void gemv_seg(const uint8_t *__restrict__ w, const ui
   for (; g < groups; g += gridDim.x) {
     const int64_t gn = g + gridDim.x;
     const int64_t row_n = gn * rows_per_wg + row_in_wg;
-    const typename F::Piece nxt = F::load(w, aux, (gn < groups && row_n < n) ? row_n : (row < n ? row : n - 1), k, pl);
+    const typename F::Piece nxt = F::template load<true>(w, aux, (gn < groups && row_n < n) ? row_n : (row < n ? row : n - 1), k, pl);
     emit(cur, row, bv);
     cur = nxt;
     row = row_n;
@@ -356,7 +356,7 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv_long(const uint8_t *__restric
   auto fill = [&](int j, int64_t r, int64_t fallback) {
     const int64_t rr = r < n ? r : fallback;
 #pragma unroll
-    for (int i = 0; i < PPL; ++i) sl[j][i] = F::load(w, aux, rr, k, pc[i]);
+    for (int i = 0; i < PPL; ++i) sl[j][i] = F::template load<true>(w, aux, rr, k, pc[i]);
   };
   const int64_t first = row0 < n ? row0 : n - 1;
 
@@ -496,7 +496,7 @@ __global__ __launch_bounds__(1024) void k_gemv_team(const uint8_t *__restrict__ 
 #pragma unroll
   for (int j = 0; j < D; ++j) {
     const int64_t r = r0 + j * stride;
-    sl[j] = F::load(w, aux, r < n ? r : first, k, pl);
+    sl[j] = F::template load<true>(w, aux, r < n ? r : first, k, pl);
   }
   __builtin_amdgcn_sched_barrier(0);
   float xv[MR][F::RUNS][16];
@@ -534,7 +534,7 @@ __global__ __launch_bounds__(1024) void k_gemv_team(const uint8_t *__restrict__ 
       const int ir = base + j;
       emit(j, ir);
       const int64_t r = r0 + (int64_t)ir * stride, rn = r + D * stride;
-      sl[j] = F::load(w, aux, rn < n ? rn : r, k, pl);
+      sl[j] = F::template load<true>(w, aux, rn < n ? rn : r, k, pl);
     }
   }
 #pragma unroll
@@ -575,7 +575,7 @@ __global__ __launch_bounds__(1024) void k_gemv_team2(const uint8_t *__restrict__
   chunk16 xc[XR];
   load_x_chunks<XR>(x, xtype, (int)k, xc);
   __builtin_amdgcn_sched_barrier(0);
-  const typename F::Piece pc = F::load(w, aux, row < n ? row : n - 1, k, pl);
+  const typename F::Piece pc = F::template load<true>(w, aux, row < n ? row : n - 1, k, pl);
   __builtin_amdgcn_sched_barrier(0);
   store_x_chunks<XR>(xtype, (int)k, xc, xs_dyn);  // ends with a barrier
   float xv[F::RUNS][16], sx[F::RUNS];
@@ -622,7 +622,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_multi(const uint8_t *__restri
     for (int i = 0; i < PPL; ++i) {
       const int p = sl + (i << seg_log2);
       if (row < n && p < P) {
-        F::decode(F::load(w, aux, row, k, p), wv[i]);
+        F::decode(F::template load<true>(w, aux, row, k, p), wv[i]);
       } else {
 #pragma unroll
         for (int r = 0; r < F::RUNS; ++r)
