@@ -214,7 +214,8 @@ __global__ __launch_bounds__(512) void k_marlin_gemv_x(const mchunk *__restrict_
 #pragma unroll
     for (int j = 0; j < B; ++j) {
       const int64_t c = c0 + j * SLOTS;
-      q[j] = packed[(c < kc ? c : kc - 1) * n + rowc];
+      // non-temporal: the packed weights are streamed once (4864 x 896 3.73 -> 3.17 us)
+      q[j] = __builtin_nontemporal_load(&packed[(c < kc ? c : kc - 1) * n + rowc]);
     }
   };
   fetch(slot);
@@ -346,7 +347,11 @@ __global__ __launch_bounds__(1024) void k_marlin_mx(const mchunk *__restrict__ p
   for (int i = 0; i < CPW; ++i) {
     const int64_t c = (int64_t)wave + (int64_t)W * i;
     const int64_t cc = c < kc ? c : kc - 1;
-    wq[i] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint8_t *>(packed + cc * n + rowc) + 8 * h);
+    {  // non-temporal, as in k_marlin_gemv_x (14336 x 4096 10.6 -> 9.9-10.4 us)
+      typedef uint32_t mw2 __attribute__((ext_vector_type(2)));
+      const mw2 v = __builtin_nontemporal_load(reinterpret_cast<const mw2 *>(reinterpret_cast<const uint8_t *>(packed + cc * n + rowc) + 8 * h));
+      wq[i] = make_uint2(v.x, v.y);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 
