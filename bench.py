@@ -831,7 +831,7 @@ def main():
                      "timing": f"HIP events around graph replays of {GATE_COPIES} launches on {GATE_COPIES} "
                                "distinct weights (1.25 GB) on the replay stream, gaps included: the figure "
                                "bench.py --mode gate prints (profiles/gemv_q4k_gate_4864x896.md)",
-                     "kernel": "k_gemv_m1<FmtQ4K,1,1,true> (gate/up 4864x896; the plain f32 form)",
+                     "kernel": "k_gemv_m1<FmtQ4K,1,1,true> (gate/up 4864x896; the plain f32 form, non-temporal weight loads)",
                      "bytes_per_launch": gate_bytes, "us_per_launch": round(gate_us, 3)},
         "cpu_baseline": cpu,
         "extra": extra,
