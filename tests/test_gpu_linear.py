@@ -48,6 +48,27 @@ def test_decode_gemv_f32(dev, qtype, n, k):
     assert norm_err(y, ref(x, wf)) <= TOL_F32
 
 
+@pytest.mark.parametrize("qtype", [rq.Q4_K, rq.Q6_K, rq.Q8_0])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("n,k", [(777, 4864), (1023, 2304), (513, 8192)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_two_team_gemv(dev, qtype, xdt, n, k, with_bias):
+    # 512 < n <= 1024 rows of more than 64 pieces: two rows a workgroup, one
+    # team each, x staged once in LDS; odd n leaves the last workgroup's second
+    # row past the matrix (loaded clamped, never stored)
+    w, wf = make(qtype, n, k, 71 + n + k)
+    x = synth.activations(73 + n, 1, k)
+    xt = torch.from_numpy(x).to(xdt)
+    r = ref(xt.float().numpy(), wf)
+    if with_bias:
+        b = torch.from_numpy(synth.activations(75 + n, 1, n)[0]).to(dev)
+        y = w.forward(xt.to(dev), out_dtype=torch.float32, bias=b).cpu().numpy()
+        r = r + b.cpu().numpy()[None, :]
+    else:
+        y = w.forward(xt.to(dev), out_dtype=torch.float32).cpu().numpy()
+    assert norm_err(y, r) <= TOL_F32
+
+
 @pytest.mark.parametrize("xdt", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("n,k", [(4096, 512), (4096, 2048), (16394, 1024), (8192, 2048), (4133, 4096),
                                  (14336, 4096), (4096, 8192)])
