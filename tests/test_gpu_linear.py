@@ -424,6 +424,8 @@ def test_mfma_gemm_edge_tiles(dev, qtype, m, n, k):
     (rq.Q6_K, 512, 32776, 1024),  # pipelined Q6_K, ragged last column tile, whole tiles staged
     (rq.Q6_K, 300, 32868, 384),  # Q6_K with k % 256 != 0: the per-chunk pipelined kernel, ragged
     (rq.Q8_0, 512, 32768, 640),  # pipelined, whole tiles staged
+    (rq.Q6_K, 100, 65600, 512),  # pipelined Q6_K, one M tile of 100 rows
+    (rq.Q4_K, 100, 65600, 384),  # pipelined, one M tile of 100 rows
 ])
 def test_large_gemm(dev, qtype, m, n, k):
     w, wf = make(qtype, n, k, 5 + m + k)
