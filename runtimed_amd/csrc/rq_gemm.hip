@@ -374,8 +374,11 @@ __device__ __forceinline__ void q6_pair_run(const Q6Pair &p, int hh, uint32_t (&
 // and loads two 16-byte activation chunks; the tile rows' activations of
 // step s + 4 are loaded during step s, the chunk pair of steps 4j .. 4j + 3
 // during step 4j - 7, and both are written into LDS stage (s + 2) % 4 during
-// step s.  Four stages, one barrier a step, LDS rows of 64 bytes with the
-// 16-byte chunk index XOR-ed with (row / 4) % 4.  Workgroups take tiles
+// step s.  Four stages, one barrier every two steps (before even steps:
+// the pair of steps reads stages s and s + 1 and writes s + 2 and s + 3, so
+// the first pass's fragments of an even step are read after its barrier;
+// head 660 -> 649-657 us against a barrier a step), LDS rows of 64 bytes with
+// the 16-byte chunk index XOR-ed with (row / 4) % 4.  Workgroups take tiles
 // XCD by XCD (XCD x the x-th eighth of the tiles, M fastest) so that the
 // workgroups sharing a weight tile share an L2.
 struct Pass8 {
@@ -427,16 +430,16 @@ struct PipeBases8 {
 // (one read after each of the first six) and running hook(f) after MFMA f:
 // the order is fixed (nothing is moved across the scheduling barriers), so
 // the hook's VALU work issues while the MFMAs before it run.
-template <int ST, int H, class Hook>
+template <int ST, int H, class Hook, bool READ = true>
 __device__ __forceinline__ void mfma_pass8(const Pass8 &cur, Pass8 &nxt, const PipeBases8 &pb, f32x16 (&acc)[4][2],
-                                           Hook &&hook) {
+                                           Hook &&hook, std::integral_constant<bool, READ> = {}) {
   static_for<4>([&](auto I) {
     static_for<2>([&](auto J) {
       acc[I][J] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16(cur.x[I]), as_bf16(cur.x[4 + J]), acc[I][J], 0, 0,
                                                           0);
       constexpr int f = 2 * decltype(I)::value + decltype(J)::value;
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (f < 6) nxt.x[f] = ds_read16_off<ST * P8_A + 2048 * (f < 4 ? f : f - 4)>(pb.rd[H][f < 4 ? 0 : 1]);
+      if constexpr (READ && f < 6) nxt.x[f] = ds_read16_off<ST * P8_A + 2048 * (f < 4 ? f : f - 4)>(pb.rd[H][f < 4 ? 0 : 1]);
       hook(std::integral_constant<int, f>{});
       __builtin_amdgcn_sched_barrier(0);
     });
@@ -525,15 +528,10 @@ __global__ __launch_bounds__(512) void k_q6_pipe8(const uint8_t *__restrict__ w,
     write_run8<1>(pb, o);
   }
   wait_lds_all();
-  __builtin_amdgcn_s_barrier();
   Pass8 P0, P1;
-  static_for<6>([&](auto F) {
-    constexpr int f = decltype(F)::value;
-    P0.x[f] = ds_read16_off<2048 * (f < 4 ? f : f - 4)>(pb.rd[0][f < 4 ? 0 : 1]);
-  });
-  wait_pass8(P0);
 
-  // Step s = 8u + B: pass 1 of stage s % 4, pass 0 of stage (s + 1) % 4, and
+  // Step s = 8u + B: pass 0 of stage s % 4 (read after the barrier on even
+  // steps, during the previous step on odd ones), pass 1 of it, and
   // the run of step s + 2 (pair (s + 2) / 4, chunk ((s + 2) / 2) % 2, run
   // (s + 2) % 2) from slot ((B + 2) / 4) % 2 into stage (s + 2) % 4; slot 0
   // is free after step 8u + 1 and takes pair 2u + 2, slot 1 after 8u + 5 and
@@ -542,7 +540,14 @@ __global__ __launch_bounds__(512) void k_q6_pipe8(const uint8_t *__restrict__ w,
     constexpr int B = decltype(Bc)::value;
     constexpr int T = (B + 2) & 7, CC = (T >> 1) & 1, RR = T & 1, SLOT = ((B + 2) >> 2) & 1;
     constexpr int ST = B & 3, ST1 = (B + 1) & 3, ST2 = (B + 2) & 3;
-    __builtin_amdgcn_s_barrier();
+    if constexpr ((B & 1) == 0) {
+      __builtin_amdgcn_s_barrier();
+      static_for<6>([&](auto F) {
+        constexpr int f = decltype(F)::value;
+        P0.x[f] = ds_read16_off<ST * P8_A + 2048 * (f < 4 ? f : f - 4)>(pb.rd[0][f < 4 ? 0 : 1]);
+      });
+      wait_pass8(P0);
+    }
     // stage (s + 2) % 4 was last read in steps s - 3 and s - 2: its activation
     // part is written first, the decoded run (during the first pass) early in
     // the second, so that no write is left to complete at the end of the step
@@ -557,13 +562,13 @@ __global__ __launch_bounds__(512) void k_q6_pipe8(const uint8_t *__restrict__ w,
     wait_pass8(P1);
     mfma_pass8<ST1, 0>(P1, P0, pb, acc, [&](auto F) {
       if constexpr (decltype(F)::value == 0) write_run8<ST2>(pb, o0);
-    });
+    }, std::integral_constant<bool, (B & 1) == 0>{});
     if constexpr (B == 1 || B == 5) {
       const int64_t jn = (s + 7) >> 2 < np ? (s + 7) >> 2 : np - 1;
       pp[B == 1 ? 0 : 1] = load_q6_pair(w, aux, rk0, jn, hh);
     }
-    wait_pass8(P0);
-    wait_lds_all();
+    if constexpr ((B & 1) == 0) wait_pass8(P0);
+    else wait_lds_all();
   };
   for (int64_t t = 0; t < nk; t += 8) {
     step(t, std::integral_constant<int, 0>{});
